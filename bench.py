@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X ternary-matmul hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-gemm]
+
+Workload (the batch-1 decode sweep): one step is the T=1 decode
+GEMV of every ternary matrix of one layer of each kind at the 27B shapes —
+GDN qkv 5120->10240, z 5120->6144, ssm_out 6144->5120; GQA q 5120->12288, k/v 5120->1024,
+o 6144->5120; FFN gate/up 5120->17408, down 17408->5120 — each call including its
+activation preparation (one per distinct input: 6 per step).  Weights are seeded
+synthetic PTQ1_0 (trits iid on {-1,0,1}, fp16 scales |N(0,0.02)|), activations fp16
+N(0,1).  Steps rotate over enough distinct weight copies (>= 512 MB) that no matrix is
+served from the 256 MB Infinity Cache.  `value` = packed weight bytes of all GEMVs of the
+timed steps / wall time of those steps (events on the launch stream), in GB/s.
+
+Also reported (same JSON line):
+  roofline     dominant kernel k_gemv_ptq1<1>: algorithmic bytes per launch (the packed
+               weight bytes, averaged over the sweep's matrices) / its average launch
+               duration, vs 8 TB/s HBM;
+  per_matrix   GB/s of each matrix kind alone (200 repeats over rotating copies);
+  prefill_gemm pp512 exact fp16 GEMM TFLOPS (M=512, 5120->17408 and 17408->5120),
+               vs 2.5 PFLOP/s dense fp16;
+  cpu_baseline the reference's host arithmetic for the path (PTQ1_0 decode + fp32 dot,
+               oracle/kata_oracle.c:orc_cpu_gemv_ptq1_f32) on a bounded row sample of the
+               same sweep, on this machine's host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+# (name, K, N) of one layer of each kind; x-sharing groups for the activation prep
+SWEEP = [
+    ("gdn_qkv", 5120, 10240, "gdn_in"), ("gdn_z", 5120, 6144, "gdn_in"), ("gdn_ssm_out", 6144, 5120, "gdn_out"),
+    ("attn_q", 5120, 12288, "attn_in"), ("attn_k", 5120, 1024, "attn_in"), ("attn_v", 5120, 1024, "attn_in"),
+    ("attn_o", 6144, 5120, "attn_out"),
+    ("ffn_gate", 5120, 17408, "ffn_in"), ("ffn_up", 5120, 17408, "ffn_in"), ("ffn_down", 17408, 5120, "ffn_mid"),
+]
+SEED = 20260501
+
+
+def packed_bytes(K, N):
+    return N * (K // 128) * 28
+
+
+def make_weights(torch, dev, K, N, seed, ops):
+    """One packed matrix built on the host with the library's packer, then on device."""
+    rng = np.random.default_rng(seed)
+    trits = rng.integers(-1, 2, size=(N, K), dtype=np.int8)
+    scales = np.abs(rng.normal(0.0, 0.02, size=(N, K // 128))).astype(np.float16)
+    return torch.from_numpy(ops.pack_ptq1(trits, scales)).to(dev)
+
+
+def cpu_baseline(sample_rows: int, threads: int):
+    """Times the reference's host decode + fp32 dot on `sample_rows` rows of every sweep
+    matrix (same shapes and distributions), returns GB/s of packed bytes."""
+    from oracle import oracle as orc
+    total_bytes, total_t = 0, 0.0
+    for i, (name, K, N, _) in enumerate(SWEEP):
+        rows = min(sample_rows, N)
+        W, _, _ = orc.synth_ptq1(rows, K, SEED + 1000 + i)
+        x = orc.synth_x(1, K, SEED + 2000 + i).astype(np.float32)
+        t0 = time.perf_counter()
+        orc.cpu_gemv_f32(W, x, K, rows, 1, 0, rows, threads)
+        total_t += time.perf_counter() - t0
+        total_bytes += packed_bytes(K, rows)
+    return total_bytes / total_t / 1e9, total_bytes
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=2048)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(the multi-GPU plan is design-only: decode is replicated, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+    from kata_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    # ---- weights: one layer-set per copy, copies until >= 512 MB
+    set_bytes = sum(packed_bytes(K, N) for _, K, N, _ in SWEEP)
+    ncopies = max(2, -(-512 * 1024 * 1024 // set_bytes))
+    base = [make_weights(torch, dev, K, N, SEED + i, ops) for i, (_, K, N, _) in enumerate(SWEEP)]
+    copies = [base] + [[w.clone() for w in base] for _ in range(ncopies - 1)]
+    xs = {}
+    for gi, grp in enumerate(sorted({g for *_, g in SWEEP})):
+        K = next(K for _, K, _, g in SWEEP if g == grp)
+        xs[grp] = torch.from_numpy(np.random.default_rng(SEED + 77 + gi).standard_normal((1, K))
+                                   .astype(np.float16)).to(dev)
+    xps = {g: torch.empty(ops.xprep_bytes(x.shape[1], 1), dtype=torch.uint8, device=dev) for g, x in xs.items()}
+    ys = [torch.empty((1, N), dtype=torch.float32, device=dev) for _, _, N, _ in SWEEP]
+
+    def step(i):
+        ws = copies[i % ncopies]
+        done = set()
+        for j, (name, K, N, grp) in enumerate(SWEEP):
+            if grp not in done:
+                ops.gemv_ptq1_prep(xs[grp], K, 1, out=xps[grp])
+                done.add(grp)
+            ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = e0.elapsed_time(e1)
+    ms_step = ms_total / args.steps
+    value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
+
+    # ---- dominant kernel alone: the GEMV launches of the sweep without the preps
+    reps = max(20, args.steps // 2)
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record(stream)
+    for i in range(reps):
+        ws = copies[i % ncopies]
+        for j, (name, K, N, grp) in enumerate(SWEEP):
+            ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
+    g1.record(stream)
+    torch.cuda.synchronize()
+    gemv_launch_us = g0.elapsed_time(g1) * 1e3 / (reps * len(SWEEP))
+    bytes_per_launch = set_bytes / len(SWEEP)
+    achieved = bytes_per_launch / (gemv_launch_us * 1e-6) / 1e9
+
+    # ---- per matrix kind (config 2: 200 repeats each over rotating copies)
+    per_matrix = {}
+    for j, (name, K, N, grp) in enumerate(SWEEP):
+        nrep = 200
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for r in range(nrep):
+            ops.gemv_ptq1_prepped(copies[r % ncopies][j], xps[grp], K, N, 1, out=ys[j])
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / nrep
+        per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
+                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
+
+    # ---- pp512 prefill GEMM (config 4), fp16 exact path
+    gemm = None
+    if not args.no_gemm:
+        gemm = {}
+        M = 512
+        A = {K: torch.from_numpy(np.random.default_rng(K).standard_normal((M, K)).astype(np.float16)).to(dev)
+             for K in (5120, 17408)}
+        for name, K, N, j in (("ffn_gate", 5120, 17408, 7), ("ffn_down", 17408, 5120, 9)):
+            C = torch.empty((M, N), dtype=torch.float16, device=dev)
+            for r in range(3):
+                ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
+            torch.cuda.synchronize()
+            nrep = 10
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for r in range(nrep):
+                ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / nrep
+            tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            gemm[name] = {"M": M, "K": K, "N": N, "us": round(us, 1), "TFLOPS": round(tflops, 1),
+                          "frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+
+    # ---- CPU baseline (reference host arithmetic, bounded sample)
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        gbs, nbytes = cpu_baseline(args.cpu_rows, threads)
+        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"first {args.cpu_rows} rows of each of the 10 sweep matrices "
+                         f"({nbytes/1e6:.1f} MB packed), fp32 decode+dot, OpenMP over rows"}
+
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_ptq1_sweep_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": "ternary GEMV HBM GB/s (% of peak) at bs=1; pp512 prefill GEMM TFLOPS",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded trits/scales/activations)",
+        "config": {"workload": "BASELINE configs[1]: bs=1 decode GEMV sweep, one layer of each kind "
+                               "(10 matrices, 6 activation preps per step)",
+                   "weight_copies": ncopies, "bytes_per_step": set_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_gemv_ptq1<1>", "avg_launch_us": round(gemv_launch_us, 3),
+                     "bytes_per_launch": bytes_per_launch},
+        "per_matrix": per_matrix,
+        "prefill_gemm": gemm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

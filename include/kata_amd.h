@@ -1,0 +1,139 @@
+/*
+ * kata_amd.h — C ABI of the MI355X (gfx950) ternary-matmul library.
+ *
+ * Drop-in for the matmul dispatch surface of the reference engine (src/engine.cpp,
+ * src/engine.h).  Every entry point:
+ *   - is stream ordered on the caller's HIP stream (`stream` is a hipStream_t; NULL means
+ *     the default stream) and returns without synchronising;
+ *   - takes device pointers only (except the host packers, marked HOST);
+ *   - returns 0 on success or a negative KATA_E* code; kata_last_error() then describes
+ *     the failure for the calling thread.  No entry point calls exit().
+ * Weights are read-only device bytes in the native GGUF block layout (PTQ1_0: 28-byte
+ * blocks, Q8_0: 34-byte blocks), row-major [N rows][K/group blocks], at any 4-byte
+ * aligned base; no weight copy or dequantised stage is ever made.
+ */
+#ifndef KATA_AMD_H
+#define KATA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KATA_OK 0
+#define KATA_EINVAL (-1)  /* bad shape, alignment, dtype or layout argument */
+#define KATA_ELAUNCH (-2) /* a HIP runtime call or kernel launch failed */
+#define KATA_ENOMEM (-3)  /* library work buffer could not be allocated */
+
+/* activation element types */
+#define KATA_F32 0
+#define KATA_F16 1
+/* activation layouts for the GEMVs */
+#define KATA_X_ROWS 0   /* x[T][K], one row per token */
+#define KATA_X_HALF2 1  /* x[K][2] fp16, the two tokens interleaved (T == 2 only) */
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* kata_last_error(void);
+
+/* Library version string. */
+const char* kata_version(void);
+
+/* ---------------------------------------------------------------- decode GEMVs -------
+ * y[t][n] = sum_b d[n,b] * sum_e trit[n,b,e] * x[t][128b+e], fp32 out, t < T, T in {1,2}.
+ * K % 128 == 0, N >= 1.  y is [T][N] fp32.
+ * Replaces Engine::dGemvPtq1 (src/engine.cpp:97-101, src/engine.h:155; kernel
+ * k_gemv_v1_nr4_sg4, shaders/gemv_fast.metal:9-50) for T = 1, and the `gv` lambda of
+ * Engine::verify2 (src/engine.cpp:440-443; k_gemv_lut2_nr4_sg4, shaders/mtp.metal:164-205,
+ * or k_gemv_v1h_t2, mtp.metal:66-103) for T = 2.  x_layout KATA_X_HALF2 accepts the
+ * interleaved activations k_gemv_lut2 reads (k_ilv2, shaders/mtp.metal:222-224).
+ * Uses a library-owned activation work buffer on the current device (allocated on first
+ * use); calls on one device must not overlap in time. */
+int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y,
+                   int K, int N, int T, void* stream);
+
+/* Split form of kata_gemv_ptq1 for callers that multiply one activation by several
+ * matrices (q/k/v, gate/up): prepare the activation once, then run any number of GEMVs
+ * on it.  xprep is caller-owned device memory of kata_gemv_ptq1_xprep_bytes(K, T) bytes,
+ * 256-byte aligned.  No counterpart function in the reference: there the producer kernels
+ * write the GEMV's activation layout directly (k_add_rms_fwht_t flag 4,
+ * shaders/prefill.metal:97). */
+size_t kata_gemv_ptq1_xprep_bytes(int K, int T);
+int kata_gemv_ptq1_prep(const void* x, int x_dtype, int x_layout, void* xprep, int K, int T,
+                        void* stream);
+int kata_gemv_ptq1_prepped(const uint8_t* W, const void* xprep, float* y, int K, int N, int T,
+                           void* stream);
+
+/* Q8_0 GEMV for the MTP head: y[t][n] = sum_b d[n,b] * sum_i q[n,b,i] * x[t][32b+i].
+ * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16, y [T][N] fp32.
+ * Replaces the `gq` lambda of Engine::mtpRows (src/engine.cpp:351; k_gemv_q8_t1/_t2,
+ * shaders/mtp.metal:5-22). */
+int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                   void* stream);
+
+/* ---------------------------------------------------------------- prefill ------------
+ * Exact fp16 prefill GEMM with the ternary decode fused into the LDS tile load:
+ * C[m][n] = sum_k A[m][k] * half(trit[n][k] * d[n][k/128]), fp32 accumulation.
+ * A is fp16 [M][lda] (lda >= K), C is [M][ldc] of c_dtype (KATA_F32 or KATA_F16).
+ * K % 128 == 0; any M >= 1, N >= 1.
+ * Replaces Engine::dExpandGemm's fp16 path (src/engine.cpp:208-219: k_expand_ptq1_v2 into
+ * a 178 MB stage, then Engine::dGemm / k_gemm_f16, shaders/prefill.metal:31-41). */
+int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
+                       int M, int K, int N, void* stream);
+
+/* Activation quantisation for the int8 prefill path: per (token m, 128-group g)
+ * scale = amax > 0 ? amax/127 : 1, Q = clamp(rint(x/scale), +-127), SX[g*ldS + m] = scale.
+ * X fp16 [M][K], Q int8 [M][K], SX fp32 [K/128][ldS], ldS >= M.
+ * Replaces k_quant_rows (shaders/prefill.metal:369-381; dispatched src/engine.cpp:230). */
+int kata_quant_rows_i8(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS, void* stream);
+
+/* int8 prefill GEMM with the ternary decode fused: per 128-group the exact int32 sum
+ * I = sum_k A8[m][k] * trit[n][k], then C[m][n] += float(I) * (d[n][g] * SX[g*ldS+m]).
+ * C is [M][ldc] of c_dtype.  K % 128 == 0.
+ * Replaces Engine::dExpandGemm's int8 path (src/engine.cpp:210-213: k_expand_i8_v2 +
+ * k_gemm_i8, shaders/prefill.metal:382-415,457-471). */
+int kata_gemm_ptq1_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C,
+                      int c_dtype, int ldc, int M, int K, int N, void* stream);
+
+/* Standalone expansions (verification and catch-up uses), natural row-major layout:
+ * out[n][k] = half(trit*d) (fp16 bits), T8[n][k] = trit, SW[n][k/128] = d.
+ * Replace k_expand_ptq1_v2 / k_expand_i8_v2 (shaders/prefill.metal:457-479); the
+ * reference writes tile-major [N/64][K][64], here the order is [N][K]. */
+int kata_expand_ptq1_f16(const uint8_t* W, uint16_t* out, int K, int N, void* stream);
+int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, void* stream);
+
+/* ---------------------------------------------------------------- HOST packers -------
+ * HOST: quantize_row_ptq1_0_ref over nrow rows of k floats (k % 128 == 0)
+ * (docs/reference/prism_ptq1_0_quant_dequant.c:4-52, quantize_ptq1_0 :86-96). */
+int kata_quantize_ptq1_0(const float* x, uint8_t* out, int64_t nrow, int64_t k);
+/* HOST: packs trits (int8 in {-1,0,1}, [nrow][k]) with given fp16 scales ([nrow][k/128],
+ * raw bits) using the same byte encoding; used to build synthetic weights. */
+int kata_pack_ptq1_0(const int8_t* trits, const uint16_t* scales, uint8_t* out, int64_t nrow, int64_t k);
+
+/* ---------------------------------------------------------------- dispatcher ---------
+ * An engine-side dispatcher that maps (byte offset into the weight file, K, N, matrix
+ * name) to the kernels above, with the reference's per-matrix int8 selection.
+ * Mirrors Engine::dGemvPtq1 / dExpandGemm / setI8 / i8 (src/engine.cpp:97-101,208-219,
+ * 529-537; src/engine.h:89-95).  Names: qkv z ssmout wq wk wv wo gate up down. */
+typedef struct kata_dispatch kata_dispatch;
+kata_dispatch* kata_dispatch_create(const uint8_t* wbase);
+void kata_dispatch_destroy(kata_dispatch* d);
+/* "all", "ffn" (gate+up), "none"/"", or a comma list of names; KATA_EINVAL on unknown. */
+int kata_dispatch_set_i8(kata_dispatch* d, const char* spec);
+int kata_dispatch_i8(const kata_dispatch* d, const char* name);   /* 1 if int8 path */
+uint32_t kata_dispatch_i8_mask(const kata_dispatch* d);
+/* T=1 decode GEMV of the matrix at byte offset wOff (x fp32 [K], y fp32 [N]). */
+int kata_dispatch_gemv(kata_dispatch* d, uint64_t wOff, const float* x, float* y, int K, int N,
+                       void* stream);
+/* Prefill matmul of the named matrix: fp16 exact path, or the int8 path when selected
+ * (then A is quantised into caller-provided A8 [M][K] / SX [K/128][ldS] work buffers;
+ * they may be NULL when the matrix is on the fp16 path).  C fp32 [M][N]. */
+int kata_dispatch_prefill(kata_dispatch* d, uint64_t wOff, const uint16_t* A, float* C, int M,
+                          int K, int N, const char* name, int8_t* A8, float* SX, int ldS,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KATA_AMD_H */

@@ -1,0 +1,329 @@
+// C ABI of the gfx950 ternary-matmul library: argument validation, error reporting,
+// the library-owned activation work buffer, the host packers and the engine-style
+// dispatcher.  Declarations and reference citations: include/kata_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/kata_amd.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int check_launch(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(KATA_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+    g_err.clear();
+    return KATA_OK;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// ---- library-owned activation work buffer, one per device ------------------------------
+constexpr int kMaxDevices = 64;
+struct Work {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_work_mu;
+Work g_work[kMaxDevices];
+
+int work_buffer(size_t need, void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(KATA_ELAUNCH, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lk(g_work_mu);
+    Work& w = g_work[dev];
+    if (w.bytes < need) {
+        if (w.ptr) (void)hipFree(w.ptr);   // hipFree waits for work that still uses it
+        w.ptr = nullptr;
+        w.bytes = 0;
+        const size_t sz = (need + (1 << 20) - 1) & ~(size_t)((1 << 20) - 1);
+        if (hipMalloc(&w.ptr, sz) != hipSuccess) return fail(KATA_ENOMEM, "hipMalloc(%zu) failed", sz);
+        w.bytes = sz;
+    }
+    *out = w.ptr;
+    return KATA_OK;
+}
+
+int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, const void* y, int K, int N,
+                    int T) {
+    if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
+    if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (x_layout != KATA_X_ROWS && x_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "x_layout=%d", x_layout);
+    if (x_layout == KATA_X_HALF2 && (T != 2 || x_dtype != KATA_F16))
+        return fail(KATA_EINVAL, "KATA_X_HALF2 needs T=2 and fp16 activations");
+    if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
+    if (!aligned(x, x_dtype == KATA_F16 ? 2 : 4)) return fail(KATA_EINVAL, "x misaligned");
+    return KATA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kata_last_error(void) { return g_err.c_str(); }
+const char* kata_version(void) { return "kata_amd 0.1 (gfx950)"; }
+
+// ------------------------------------------------------------------ PTQ1_0 GEMV
+size_t kata_gemv_ptq1_xprep_bytes(int K, int T) {
+    if (K <= 0 || K % 128 != 0 || (T != 1 && T != 2)) return 0;
+    return kata::xprep_layout(K, T).bytes;
+}
+
+int kata_gemv_ptq1_prep(const void* x, int x_dtype, int x_layout, void* xprep, int K, int T, void* stream) {
+    int rc = check_gemv_args((const void*)256, x, x_dtype, x_layout, (const void*)256, K, 1, T);   // x-only checks
+    if (rc) return rc;
+    if (!xprep || !aligned(xprep, 256)) return fail(KATA_EINVAL, "xprep must be non-null and 256-byte aligned");
+    return check_launch(kata::launch_gemv_prep(x, x_dtype, x_layout, (uint8_t*)xprep, K, T, (hipStream_t)stream),
+                        "gemv prep");
+}
+
+int kata_gemv_ptq1_prepped(const uint8_t* W, const void* xprep, float* y, int K, int N, int T, void* stream) {
+    int rc = check_gemv_args(W, (const void*)256, KATA_F32, KATA_X_ROWS, y, K, N, T);   // W/y checks
+    if (rc) return rc;
+    if (!xprep || !aligned(xprep, 256)) return fail(KATA_EINVAL, "xprep must be non-null and 256-byte aligned");
+    return check_launch(kata::launch_gemv_ptq1(W, (const uint8_t*)xprep, y, K, N, T, (hipStream_t)stream),
+                        "gemv ptq1");
+}
+
+int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
+                   void* stream) {
+    int rc = check_gemv_args(W, x, x_dtype, x_layout, y, K, N, T);
+    if (rc) return rc;
+    void* xp = nullptr;
+    rc = work_buffer(kata::xprep_layout(K, T).bytes, &xp);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    rc = check_launch(kata::launch_gemv_prep(x, x_dtype, x_layout, (uint8_t*)xp, K, T, s), "gemv prep");
+    if (rc) return rc;
+    return check_launch(kata::launch_gemv_ptq1(W, (const uint8_t*)xp, y, K, N, T, s), "gemv ptq1");
+}
+
+// ------------------------------------------------------------------ Q8_0 GEMV
+int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, void* stream) {
+    if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
+    if (K <= 0 || K % 32 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 32", K);
+    if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
+    if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (!aligned(W, 2)) return fail(KATA_EINVAL, "W must be 2-byte aligned");
+    if (!aligned(x, x_dtype == KATA_F16 ? 2 : 4)) return fail(KATA_EINVAL, "x misaligned");
+    return check_launch(kata::launch_gemv_q8(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv q8_0");
+}
+
+// ------------------------------------------------------------------ prefill
+int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M, int K,
+                       int N, void* stream) {
+    if (!A || !W || !C) return fail(KATA_EINVAL, "null pointer argument");
+    if (M <= 0 || N <= 0) return fail(KATA_EINVAL, "M=%d N=%d must be positive", M, N);
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (lda < K || lda % 8 != 0) return fail(KATA_EINVAL, "lda=%d must be >= K and a multiple of 8", lda);
+    if (ldc < N) return fail(KATA_EINVAL, "ldc=%d < N=%d", ldc, N);
+    if (c_dtype != KATA_F32 && c_dtype != KATA_F16) return fail(KATA_EINVAL, "c_dtype=%d", c_dtype);
+    if (!aligned(A, 16)) return fail(KATA_EINVAL, "A must be 16-byte aligned");
+    if (!aligned(W, 2)) return fail(KATA_EINVAL, "W must be 2-byte aligned");
+    return check_launch(kata::launch_gemm_f16(A, lda, W, C, c_dtype, ldc, M, K, N, (hipStream_t)stream),
+                        "gemm ptq1 f16");
+}
+
+int kata_quant_rows_i8(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS, void* stream) {
+    if (!X || !Q || !SX) return fail(KATA_EINVAL, "null pointer argument");
+    if (M <= 0) return fail(KATA_EINVAL, "M=%d must be positive", M);
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (ldS < M) return fail(KATA_EINVAL, "ldS=%d < M=%d", ldS, M);
+    if (!aligned(X, 4) || !aligned(Q, 2)) return fail(KATA_EINVAL, "X/Q misaligned");
+    return check_launch(kata::launch_quant_rows(X, Q, SX, M, K, ldS, (hipStream_t)stream), "quant rows");
+}
+
+int kata_gemm_ptq1_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C, int c_dtype, int ldc,
+                      int M, int K, int N, void* stream) {
+    if (!A8 || !SX || !W || !C) return fail(KATA_EINVAL, "null pointer argument");
+    if (M <= 0 || N <= 0) return fail(KATA_EINVAL, "M=%d N=%d must be positive", M, N);
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (ldS < M) return fail(KATA_EINVAL, "ldS=%d < M=%d", ldS, M);
+    if (ldc < N) return fail(KATA_EINVAL, "ldc=%d < N=%d", ldc, N);
+    if (c_dtype != KATA_F32 && c_dtype != KATA_F16) return fail(KATA_EINVAL, "c_dtype=%d", c_dtype);
+    if (!aligned(A8, 16)) return fail(KATA_EINVAL, "A8 must be 16-byte aligned");
+    if (!aligned(W, 2)) return fail(KATA_EINVAL, "W must be 2-byte aligned");
+    return check_launch(kata::launch_gemm_i8(A8, SX, ldS, W, C, c_dtype, ldc, M, K, N, (hipStream_t)stream),
+                        "gemm ptq1 i8");
+}
+
+int kata_expand_ptq1_f16(const uint8_t* W, uint16_t* out, int K, int N, void* stream) {
+    if (!W || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (N <= 0 || K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "bad shape K=%d N=%d", K, N);
+    if (!aligned(W, 2) || !aligned(out, 2)) return fail(KATA_EINVAL, "misaligned argument");
+    return check_launch(kata::launch_expand_f16(W, out, K, N, (hipStream_t)stream), "expand f16");
+}
+
+int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, void* stream) {
+    if (!W || !T8 || !SW) return fail(KATA_EINVAL, "null pointer argument");
+    if (N <= 0 || K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "bad shape K=%d N=%d", K, N);
+    if (!aligned(W, 2) || !aligned(SW, 4)) return fail(KATA_EINVAL, "misaligned argument");
+    return check_launch(kata::launch_expand_i8(W, T8, SW, K, N, (hipStream_t)stream), "expand i8");
+}
+
+// ------------------------------------------------------------------ host packers
+// Byte encoding of the quantiser (docs/reference/prism_ptq1_0_quant_dequant.c:20-46):
+// stages of 16 and 8 bytes carry 5 digits each (most significant first, element
+// m + n*c of the stage), the two qh bytes carry 4 digits then a zero digit; a 5-digit
+// base-3 number q is stored as ceil(q*256/243).
+}  // extern "C"
+
+namespace {
+inline uint8_t enc5(uint32_t q) { return (uint8_t)((q * 256u + 242u) / 243u); }
+
+template <typename DigitOf>
+void encode_block(uint8_t* blk, DigitOf digit_of) {
+    int base = 0, j = 0;
+    for (int c : {16, 8}) {
+        for (int m = 0; m < c; m++) {
+            uint32_t q = 0;
+            for (int n = 0; n < 5; n++) q = q * 3u + digit_of(base + m + n * c);
+            blk[j + m] = enc5(q);
+        }
+        base += 5 * c;
+        j += c;
+    }
+    for (int h = 0; h < 2; h++) {
+        uint32_t q = 0;
+        for (int n = 0; n < 4; n++) q = q * 3u + digit_of(base + h + n * 2);
+        blk[24 + h] = enc5(q * 3u);
+    }
+}
+}  // namespace
+
+extern "C" {
+
+int kata_quantize_ptq1_0(const float* x, uint8_t* out, int64_t nrow, int64_t k) {
+    if (!x || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (nrow < 0 || k <= 0 || k % 128 != 0) return fail(KATA_EINVAL, "bad shape");
+    const int64_t nb = k / 128;
+    for (int64_t i = 0; i < nrow * nb; i++) {
+        const float* xb = x + i * 128;
+        uint8_t* blk = out + i * 28;
+        float amax = 0.0f;
+        for (int e = 0; e < 128; e++) amax = std::fmax(amax, std::fabs(xb[e]));
+        const float id = amax != 0.0f ? 1.0f / amax : 0.0f;
+        encode_block(blk, [&](int e) { return (uint32_t)(std::lround(xb[e] * id) + 1); });
+        const _Float16 dh = (_Float16)amax;
+        uint16_t bits;
+        memcpy(&bits, &dh, 2);
+        blk[26] = (uint8_t)(bits & 0xff);
+        blk[27] = (uint8_t)(bits >> 8);
+    }
+    g_err.clear();
+    return KATA_OK;
+}
+
+int kata_pack_ptq1_0(const int8_t* trits, const uint16_t* scales, uint8_t* out, int64_t nrow, int64_t k) {
+    if (!trits || !scales || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (nrow < 0 || k <= 0 || k % 128 != 0) return fail(KATA_EINVAL, "bad shape");
+    const int64_t nb = k / 128;
+    for (int64_t i = 0; i < nrow * nb; i++) {
+        const int8_t* tb = trits + i * 128;
+        for (int e = 0; e < 128; e++)
+            if (tb[e] < -1 || tb[e] > 1) return fail(KATA_EINVAL, "trit out of range at %lld", (long long)(i * 128 + e));
+        uint8_t* blk = out + i * 28;
+        encode_block(blk, [&](int e) { return (uint32_t)(tb[e] + 1); });
+        blk[26] = (uint8_t)(scales[i] & 0xff);
+        blk[27] = (uint8_t)(scales[i] >> 8);
+    }
+    g_err.clear();
+    return KATA_OK;
+}
+
+// ------------------------------------------------------------------ dispatcher
+static const char* const kI8Names[] = {"qkv", "z", "ssmout", "wq", "wk", "wv", "wo", "gate", "up", "down"};
+
+static uint32_t i8_bit(const char* name, size_t len) {
+    for (uint32_t i = 0; i < 10; i++)
+        if (strlen(kI8Names[i]) == len && strncmp(kI8Names[i], name, len) == 0) return 1u << i;
+    return 0;
+}
+
+struct kata_dispatch {
+    const uint8_t* wbase;
+    uint32_t i8_mask;
+};
+
+kata_dispatch* kata_dispatch_create(const uint8_t* wbase) {
+    if (!wbase) {
+        fail(KATA_EINVAL, "null weight base");
+        return nullptr;
+    }
+    return new kata_dispatch{wbase, 0u};
+}
+
+void kata_dispatch_destroy(kata_dispatch* d) { delete d; }
+
+int kata_dispatch_set_i8(kata_dispatch* d, const char* spec) {
+    if (!d || !spec) return fail(KATA_EINVAL, "null argument");
+    uint32_t m = 0;
+    const std::string s(spec);
+    if (s == "all") {
+        m = (1u << 10) - 1;
+    } else if (s == "ffn") {
+        m = i8_bit("gate", 4) | i8_bit("up", 2);
+    } else if (!s.empty() && s != "none") {
+        size_t p = 0;
+        while (p <= s.size()) {
+            size_t q = s.find(',', p);
+            if (q == std::string::npos) q = s.size();
+            const uint32_t b = i8_bit(s.c_str() + p, q - p);
+            if (!b) return fail(KATA_EINVAL, "unknown matrix name in int8 spec '%s'", spec);
+            m |= b;
+            p = q + 1;
+        }
+    }
+    d->i8_mask = m;
+    g_err.clear();
+    return KATA_OK;
+}
+
+int kata_dispatch_i8(const kata_dispatch* d, const char* name) {
+    if (!d || !name) return 0;
+    return (d->i8_mask & i8_bit(name, strlen(name))) != 0;
+}
+
+uint32_t kata_dispatch_i8_mask(const kata_dispatch* d) { return d ? d->i8_mask : 0u; }
+
+int kata_dispatch_gemv(kata_dispatch* d, uint64_t wOff, const float* x, float* y, int K, int N, void* stream) {
+    if (!d) return fail(KATA_EINVAL, "null dispatcher");
+    return kata_gemv_ptq1(d->wbase + wOff, x, KATA_F32, KATA_X_ROWS, y, K, N, 1, stream);
+}
+
+int kata_dispatch_prefill(kata_dispatch* d, uint64_t wOff, const uint16_t* A, float* C, int M, int K, int N,
+                          const char* name, int8_t* A8, float* SX, int ldS, void* stream) {
+    if (!d || !name) return fail(KATA_EINVAL, "null argument");
+    const uint8_t* W = d->wbase + wOff;
+    if (kata_dispatch_i8(d, name)) {
+        if (!A8 || !SX) return fail(KATA_EINVAL, "int8 path for '%s' needs A8/SX work buffers", name);
+        int rc = kata_quant_rows_i8(A, A8, SX, M, K, ldS, stream);
+        if (rc) return rc;
+        return kata_gemm_ptq1_i8(A8, SX, ldS, W, C, KATA_F32, N, M, K, N, stream);
+    }
+    return kata_gemm_ptq1_f16(A, K, W, C, KATA_F32, N, M, K, N, stream);
+}
+
+}  // extern "C"

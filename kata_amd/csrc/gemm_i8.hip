@@ -1,0 +1,171 @@
+// int8 prefill path: activation quantisation and the int8 x trit GEMM with the per-group
+// scale epilogue, ternary decode fused into the LDS tile load.
+//
+// quant_rows (shaders/prefill.metal:369-381): per (token m, group g of 128):
+//   scale = amax > 0 ? amax/127 : 1; q = clamp(rint(x * (1/scale)), -127, 127);
+//   SX[g*ldS + m] = scale.   IEEE fp32 division and round-half-even, bit-exact.
+// gemm (shaders/prefill.metal:382-415): I = sum_{k in g} A8[m][k]*trit[n][k] (exact int32),
+//   C[m][n] = sum_g float(I) * (d[n][g] * SX[g][m]) in fp32, groups ascending.
+//
+// Design: 128x128 C tile per 256-thread workgroup, one K-step per 128-group; A8 tile
+// copied to LDS, W tile decoded to int8 trits in LDS (two adjacent-k trits per 16-bit
+// store).  Each wave runs 4x4 tiles of v_mfma_i32_16x16x64_i8 (two per group) and folds
+// the group's int32 result into fp32 accumulators with the row/column scales.
+#include "common.h"
+#include "launch.h"
+
+namespace kata {
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_quant_rows(const _Float16* __restrict__ X, int8_t* __restrict__ Q,
+                                                    float* __restrict__ SX, int K, int ldS) {
+    const int m = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int G = K / kGroup;
+    const _Float16* xr = X + (size_t)m * K;
+    int8_t* qr = Q + (size_t)m * K;
+    for (int g = wave; g < G; g += 4) {
+        const v2h v = *(const v2h*)(xr + g * kGroup + 2 * lane);
+        const float a = (float)v[0], b = (float)v[1];
+        float mx = fmaxf(fabsf(a), fabsf(b));
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float scale = mx > 0.0f ? mx / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        const float qa = fminf(fmaxf(rintf(a * inv), -127.0f), 127.0f);
+        const float qb = fminf(fmaxf(rintf(b * inv), -127.0f), 127.0f);
+        const uint16_t pk = (uint16_t)((uint8_t)(int8_t)qa | ((uint16_t)(uint8_t)(int8_t)qb << 8));
+        *(uint16_t*)(qr + g * kGroup + 2 * lane) = pk;
+        if (lane == 0) SX[(size_t)g * ldS + m] = scale;
+    }
+}
+
+constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int LDB_S = BK + 16;   // bytes per LDS row
+
+template <bool C_F16>
+__global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__ A8, const float* __restrict__ SX,
+                                                      int ldS, const uint8_t* __restrict__ W, void* __restrict__ C,
+                                                      int ldc, int M, int K, int N) {
+    __shared__ int8_t As[BM * LDB_S];
+    __shared__ int8_t Bs[BN * LDB_S];
+    __shared__ float sws[BN];
+    __shared__ float sxs[BM];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int nb = K / kGroup;
+    const int l16 = lane & 15, lg = lane >> 4;
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int jx = 0; jx < 4; jx++) acc[i][jx] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; kb < nb; ++kb) {
+        __syncthreads();
+        {
+            const int r = tid >> 1, h = tid & 1;
+            const int gm = m0 + r;
+            uint4* dst = (uint4*)(As + r * LDB_S + h * 64);
+            if (gm < M) {
+                const uint4* src = (const uint4*)(A8 + (size_t)gm * K + (size_t)kb * BK + h * 64);
+#pragma unroll
+                for (int c = 0; c < 4; c++) dst[c] = src[c];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; c++) dst[c] = make_uint4(0, 0, 0, 0);
+            }
+            if (tid < BM) sxs[tid] = (m0 + tid < M) ? SX[(size_t)kb * ldS + m0 + tid] : 0.0f;
+        }
+        for (int idx = tid; idx < BN * 13; idx += 256) {
+            const int r = idx / 13, pr = idx - r * 13;
+            const int gn = n0 + r;
+            const int p = 2 * pr;
+            uint16_t* brow = (uint16_t*)(Bs + r * LDB_S);
+            if (gn < N) {
+                const uint8_t* blk = W + ((size_t)gn * nb + kb) * kBlockBytes;
+                const uint32_t bb = *(const uint16_t*)(blk + p);
+                const uint32_t b0 = bb & 0xffu, b1 = bb >> 8;
+                const int nd = p < 24 ? 5 : 4;
+#pragma unroll
+                for (int n = 0; n < 5; n++) {
+                    if (n < nd) {
+                        const uint32_t t0 = (uint32_t)(uint8_t)(int8_t)((int)ptq1_digit(b0, n) - 1);
+                        const uint32_t t1 = (uint32_t)(uint8_t)(int8_t)((int)ptq1_digit(b1, n) - 1);
+                        brow[ptq1_slot_elem(p, n) >> 1] = (uint16_t)(t0 | (t1 << 8));
+                    }
+                }
+                if (pr == 0) sws[r] = half_bits_to_float(*(const uint16_t*)(blk + 26));
+            } else {
+#pragma unroll
+                for (int n = 0; n < 5; n++) {
+                    const int e = ptq1_slot_elem(p, n);
+                    if (e >= 0) brow[e >> 1] = 0;
+                }
+                if (pr == 0) sws[r] = 0.0f;
+            }
+        }
+        __syncthreads();
+        v4i ia[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jx = 0; jx < 4; jx++) ia[i][jx] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            v4i af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As + (wm * 64 + i * 16 + l16) * LDB_S + kk * 64 + lg * 16);
+#pragma unroll
+            for (int jx = 0; jx < 4; jx++) bf[jx] = *(const v4i*)(Bs + (wn * 64 + jx * 16 + l16) * LDB_S + kk * 64 + lg * 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int jx = 0; jx < 4; jx++)
+                    ia[i][jx] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[jx], ia[i][jx], 0, 0, 0);
+        }
+#pragma unroll
+        for (int jx = 0; jx < 4; jx++) {
+            const float sw = sws[wn * 64 + jx * 16 + l16];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc[i][jx][r] += (float)ia[i][jx][r] * (sw * sxs[wm * 64 + i * 16 + lg * 4 + r]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int jx = 0; jx < 4; jx++) {
+            const int gn = n0 + wn * 64 + jx * 16 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
+                if (gm < M && gn < N) {
+                    if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][jx][r];
+                    else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][jx][r];
+                }
+            }
+        }
+}
+
+}  // namespace
+
+hipError_t launch_quant_rows(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS, hipStream_t s) {
+    hipLaunchKernelGGL(k_quant_rows, dim3(M), dim3(256), 0, s, (const _Float16*)X, Q, SX, K, ldS);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C, int c_dtype,
+                          int ldc, int M, int K, int N, hipStream_t s) {
+    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM), block(256);
+    if (c_dtype == 1)
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, grid, block, 0, s, A8, SX, ldS, W, C, ldc, M, K, N);
+    else
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, grid, block, 0, s, A8, SX, ldS, W, C, ldc, M, K, N);
+    return hipGetLastError();
+}
+
+}  // namespace kata

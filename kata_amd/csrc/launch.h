@@ -1,0 +1,34 @@
+// Internal launch interface between the C ABI (capi.cpp) and the kernel files.
+// Arguments are validated by the caller; each function returns the hipError_t of the launch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kata {
+
+// ---- PTQ1_0 GEMV (gemv_ptq1.hip)
+struct XprepLayout {
+    size_t off_sx, off_sq, off_a, bytes;
+};
+XprepLayout xprep_layout(int K, int T);
+hipError_t launch_gemv_prep(const void* x, int x_dtype, int x_layout, uint8_t* xprep, int K, int T,
+                            hipStream_t s);
+hipError_t launch_gemv_ptq1(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int T,
+                            hipStream_t s);
+
+// ---- Q8_0 GEMV (gemv_q8.hip)
+hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                          hipStream_t s);
+
+// ---- prefill (gemm_f16.hip, gemm_i8.hip, expand.hip)
+hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
+                           int M, int K, int N, hipStream_t s);
+hipError_t launch_quant_rows(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS,
+                             hipStream_t s);
+hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C,
+                          int c_dtype, int ldc, int M, int K, int N, hipStream_t s);
+hipError_t launch_expand_f16(const uint8_t* W, uint16_t* out, int K, int N, hipStream_t s);
+hipError_t launch_expand_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, hipStream_t s);
+
+}  // namespace kata

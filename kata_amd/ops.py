@@ -1,0 +1,154 @@
+"""Torch-tensor front end of the C ABI (device memory and streams come from PyTorch; the
+arithmetic is the HIP library's).  Every op runs on the tensor's device, on torch's
+current stream, and raises KataError on a bad argument — there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from .capi import KATA_F16, KATA_F32, KATA_X_HALF2, KATA_X_ROWS, check, lib
+
+GROUP, BLOCK_BYTES = 128, 28
+Q8_GROUP, Q8_BLOCK_BYTES = 32, 34
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need_gpu(*ts: torch.Tensor):
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("kata_amd ops take device tensors (no CPU path)")
+        if not t.is_contiguous():
+            raise ValueError("kata_amd ops take contiguous tensors")
+
+
+def _xdtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.float16:
+        return KATA_F16
+    if x.dtype == torch.float32:
+        return KATA_F32
+    raise ValueError(f"activation dtype {x.dtype} not supported (fp16 or fp32)")
+
+
+# ----------------------------------------------------------------------------- GEMVs
+def gemv_ptq1(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1, half2: bool = False,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[T][N] fp32 = PTQ1_0 W (N x K) times x ([T][K], or [K][2] fp16 when half2)."""
+    _need_gpu(W, x)
+    y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
+    check(lib().kata_gemv_ptq1(_ptr(W), _ptr(x), _xdtype(x), KATA_X_HALF2 if half2 else KATA_X_ROWS,
+                               _ptr(y), K, N, T, _stream(W)))
+    return y
+
+
+def xprep_bytes(K: int, T: int) -> int:
+    return int(lib().kata_gemv_ptq1_xprep_bytes(K, T))
+
+
+def gemv_ptq1_prep(x: torch.Tensor, K: int, T: int = 1, half2: bool = False,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_gpu(x)
+    nbytes = xprep_bytes(K, T)
+    xp = out if out is not None else torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    check(lib().kata_gemv_ptq1_prep(_ptr(x), _xdtype(x), KATA_X_HALF2 if half2 else KATA_X_ROWS,
+                                    _ptr(xp), K, T, _stream(x)))
+    return xp
+
+
+def gemv_ptq1_prepped(W: torch.Tensor, xprep: torch.Tensor, K: int, N: int, T: int = 1,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_gpu(W, xprep)
+    y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
+    check(lib().kata_gemv_ptq1_prepped(_ptr(W), _ptr(xprep), _ptr(y), K, N, T, _stream(W)))
+    return y
+
+
+def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_gpu(W, x)
+    y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
+    check(lib().kata_gemv_q8_0(_ptr(W), _ptr(x), _xdtype(x), _ptr(y), K, N, T, _stream(W)))
+    return y
+
+
+# ----------------------------------------------------------------------------- prefill
+def gemm_ptq1_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=torch.float32,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_gpu(A, W)
+    if A.dtype != torch.float16:
+        raise ValueError("A must be fp16")
+    M = A.shape[0]
+    C = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=A.device)
+    cdt = KATA_F16 if C.dtype == torch.float16 else KATA_F32
+    check(lib().kata_gemm_ptq1_f16(_ptr(A), A.shape[1], _ptr(W), _ptr(C), cdt, C.shape[1], M, K, N, _stream(A)))
+    return C
+
+
+def quant_rows(X: torch.Tensor, ldS: int | None = None):
+    _need_gpu(X)
+    M, K = X.shape
+    ldS = M if ldS is None else ldS
+    Q = torch.empty((M, K), dtype=torch.int8, device=X.device)
+    SX = torch.zeros((K // GROUP, ldS), dtype=torch.float32, device=X.device)
+    check(lib().kata_quant_rows_i8(_ptr(X), _ptr(Q), _ptr(SX), M, K, ldS, _stream(X)))
+    return Q, SX
+
+
+def gemm_ptq1_i8(A8: torch.Tensor, SX: torch.Tensor, W: torch.Tensor, K: int, N: int,
+                 out_dtype=torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_gpu(A8, SX, W)
+    M = A8.shape[0]
+    C = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=A8.device)
+    cdt = KATA_F16 if C.dtype == torch.float16 else KATA_F32
+    check(lib().kata_gemm_ptq1_i8(_ptr(A8), _ptr(SX), SX.shape[1], _ptr(W), _ptr(C), cdt, C.shape[1],
+                                  M, K, N, _stream(A8)))
+    return C
+
+
+def expand_f16(W: torch.Tensor, K: int, N: int) -> torch.Tensor:
+    _need_gpu(W)
+    out = torch.empty((N, K), dtype=torch.float16, device=W.device)
+    check(lib().kata_expand_ptq1_f16(_ptr(W), _ptr(out), K, N, _stream(W)))
+    return out
+
+
+def expand_i8(W: torch.Tensor, K: int, N: int):
+    _need_gpu(W)
+    T8 = torch.empty((N, K), dtype=torch.int8, device=W.device)
+    SW = torch.empty((N, K // GROUP), dtype=torch.float32, device=W.device)
+    check(lib().kata_expand_ptq1_i8(_ptr(W), _ptr(T8), _ptr(SW), K, N, _stream(W)))
+    return T8, SW
+
+
+# ----------------------------------------------------------------------------- host packers
+def _np_ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def quantize_ptq1(x: np.ndarray) -> np.ndarray:
+    """Host quantize_row_ptq1_0_ref over the rows of a float32 [N][K] array."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    N, K = x.shape
+    out = np.empty((N, K // GROUP * BLOCK_BYTES), np.uint8)
+    check(lib().kata_quantize_ptq1_0(_np_ptr(x), _np_ptr(out), N, K))
+    return out
+
+
+def pack_ptq1(trits: np.ndarray, scales_f16: np.ndarray) -> np.ndarray:
+    """Host packer: int8 trits [N][K] + fp16 scales [N][K/128] -> PTQ1_0 bytes."""
+    trits = np.ascontiguousarray(trits, dtype=np.int8)
+    N, K = trits.shape
+    sc = np.ascontiguousarray(np.asarray(scales_f16, dtype=np.float16).view(np.uint16))
+    out = np.empty((N, K // GROUP * BLOCK_BYTES), np.uint8)
+    check(lib().kata_pack_ptq1_0(_np_ptr(trits), _np_ptr(sc), _np_ptr(out), N, K))
+    return out

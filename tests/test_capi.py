@@ -1,0 +1,121 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the header
+declares, validates arguments before touching the GPU, and its host packers and the
+int8 selection logic match the reference's behaviour.  No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from kata_amd import capi as L
+from kata_amd.capi import KATA_EINVAL
+from oracle import oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "kata_amd.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(kata_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_header_symbol():
+    syms = header_symbols()
+    assert len(syms) >= 20
+    lib = L.lib()
+    for s in syms:
+        assert hasattr(lib, s), s
+        assert s in L.SIGNATURES, f"{s} has no ctypes signature"
+    assert set(L.SIGNATURES) == set(syms)
+
+
+def test_exports_with_nm():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", L.library_path()], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (kata_[a-z0-9_]+)\b", out))
+    assert set(header_symbols()) <= exported
+
+
+def test_version():
+    assert b"gfx950" in L.lib().kata_version()
+
+
+FAKE = ctypes.c_void_p(0x10000)   # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("K,N,T,dt,layout", [
+    (100, 8, 1, 0, 0),     # K not a multiple of 128
+    (0, 8, 1, 0, 0),
+    (128, 0, 1, 0, 0),     # N = 0
+    (128, 8, 3, 0, 0),     # T = 3
+    (128, 8, 1, 5, 0),     # bad dtype
+    (128, 8, 1, 1, 1),     # half2 needs T = 2
+    (128, 8, 2, 0, 1),     # half2 needs fp16
+])
+def test_gemv_rejects_bad_arguments(K, N, T, dt, layout):
+    rc = L.lib().kata_gemv_ptq1(FAKE, FAKE, dt, layout, FAKE, K, N, T, None)
+    assert rc == KATA_EINVAL
+    assert L.lib().kata_last_error()
+
+
+def test_other_entry_points_reject_bad_shapes():
+    lib = L.lib()
+    assert lib.kata_gemv_ptq1(None, FAKE, 0, 0, FAKE, 128, 8, 1, None) == KATA_EINVAL
+    assert lib.kata_gemv_q8_0(FAKE, FAKE, 0, FAKE, 48, 8, 1, None) == KATA_EINVAL
+    assert lib.kata_gemm_ptq1_f16(FAKE, 120, FAKE, FAKE, 0, 8, 4, 128, 8, None) == KATA_EINVAL   # lda < K
+    assert lib.kata_gemm_ptq1_f16(FAKE, 128, FAKE, FAKE, 0, 4, 4, 128, 8, None) == KATA_EINVAL   # ldc < N
+    assert lib.kata_gemm_ptq1_f16(FAKE, 136, FAKE, FAKE, 0, 8, 4, 136, 8, None) == KATA_EINVAL   # K % 128
+    assert lib.kata_quant_rows_i8(FAKE, FAKE, FAKE, 4, 128, 2, None) == KATA_EINVAL            # ldS < M
+    assert lib.kata_gemm_ptq1_i8(FAKE, FAKE, 4, FAKE, FAKE, 0, 4, 4, 128, 8, None) == KATA_EINVAL  # ldc < N
+    assert lib.kata_gemv_ptq1_prep(FAKE, 0, 0, ctypes.c_void_p(0x10004), 128, 1, None) == KATA_EINVAL  # xprep align
+    assert lib.kata_gemv_ptq1_xprep_bytes(100, 1) == 0
+    assert lib.kata_gemv_ptq1_xprep_bytes(5120, 1) > 5120 // 128 * 512
+
+
+def test_host_pack_matches_oracle_and_golden(golden):
+    from kata_amd import ops
+    W = ops.pack_ptq1(golden["ptq1_trits"], golden["ptq1_scales"])
+    assert np.array_equal(W, golden["ptq1_W"])
+    rng = np.random.default_rng(5)
+    t = rng.integers(-1, 2, (33, 640)).astype(np.int8)
+    s = np.abs(rng.normal(0, 0.02, (33, 5))).astype(np.float16)
+    assert np.array_equal(ops.pack_ptq1(t, s), orc.pack(t, s))
+
+
+def test_host_pack_rejects_non_trits():
+    from kata_amd import ops
+    from kata_amd.capi import KataError
+    t = np.zeros((1, 128), np.int8); t[0, 3] = 2
+    with pytest.raises(KataError):
+        ops.pack_ptq1(t, np.ones((1, 1), np.float16))
+
+
+def test_host_quantize_matches_oracle():
+    from kata_amd import ops
+    rng = np.random.default_rng(6)
+    X = rng.standard_normal((9, 384)).astype(np.float32)
+    X[2, :128] = 0.0                      # amax = 0 block
+    X[3, 5] = 0.5 * np.abs(X[3, :128]).max()   # a rounding threshold value
+    assert np.array_equal(ops.quantize_ptq1(X), orc.quantize(X))
+
+
+def test_dispatch_i8_selection():
+    lib = L.lib()
+    h = ctypes.c_void_p(lib.kata_dispatch_create(FAKE))
+    try:
+        names = ["qkv", "z", "ssmout", "wq", "wk", "wv", "wo", "gate", "up", "down"]
+        assert lib.kata_dispatch_set_i8(h, b"ffn") == 0
+        assert [n for n in names if lib.kata_dispatch_i8(h, n.encode())] == ["gate", "up"]
+        assert lib.kata_dispatch_set_i8(h, b"all") == 0
+        assert lib.kata_dispatch_i8_mask(h) == (1 << 10) - 1
+        assert lib.kata_dispatch_set_i8(h, b"down,wq") == 0
+        assert lib.kata_dispatch_i8_mask(h) == (1 << 9) | (1 << 3)
+        assert lib.kata_dispatch_set_i8(h, b"none") == 0 and lib.kata_dispatch_i8_mask(h) == 0
+        assert lib.kata_dispatch_set_i8(h, b"") == 0 and lib.kata_dispatch_i8_mask(h) == 0
+        assert lib.kata_dispatch_set_i8(h, b"gate,bogus") == KATA_EINVAL
+        assert lib.kata_dispatch_set_i8(h, b"gate,,up") == KATA_EINVAL
+        assert not lib.kata_dispatch_i8(h, b"lm_head")
+    finally:
+        lib.kata_dispatch_destroy(h)

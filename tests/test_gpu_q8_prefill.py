@@ -1,0 +1,167 @@
+"""GPU parity of the Q8_0 GEMV, the PTQ1_0 expansions, the fused fp16 prefill GEMM and
+the int8 prefill path against the CPU oracle.
+
+Bars: decoded trits / fp16 weights / int8 codes / int32 group sums bit-exact;
+fp32-accumulated outputs within 1e-3 relative L2 per output vector (tighter where the
+arithmetic allows)."""
+import numpy as np
+import pytest
+import torch
+
+from kata_amd import ops
+from kata_amd.engine import Dispatch
+from oracle import oracle as orc
+from tests.conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+# ----------------------------------------------------------------------------- Q8_0
+def test_q8_golden(dev, golden):
+    W = torch.from_numpy(golden["q8_W"]).to(dev)
+    x = torch.from_numpy(golden["q8_x"]).to(dev)
+    y = ops.gemv_q8(W, x, 64, 8, 2).cpu().numpy()
+    assert rel_l2(y, golden["q8_y"]).max() < 1e-5
+
+
+@pytest.mark.parametrize("K,N,T,dtype", [
+    (64, 1, 1, np.float32), (96, 7, 2, np.float16),       # odd block count: 16-bit path
+    (5120, 40, 1, np.float16), (5120, 33, 2, np.float32),
+    (17408, 24, 2, np.float16), (10240, 16, 1, np.float32),
+])
+def test_q8_random(dev, K, N, T, dtype):
+    W_np, _, _ = orc.synth_q8(N, K, K + N)
+    x_np = orc.synth_x(T, K, K + N + 1, dtype)
+    y = ops.gemv_q8(torch.from_numpy(W_np).to(dev), torch.from_numpy(x_np).to(dev), K, N, T).cpu().numpy()
+    ref = orc.gemv_q8(W_np, x_np.astype(np.float32), K, N, T)
+    assert rel_l2(y, ref).max() < 1e-5
+
+
+# ----------------------------------------------------------------------------- expansions
+def test_expand_bit_exact(dev, golden):
+    K, N = int(golden["ptq1_K"]), int(golden["ptq1_N"])
+    W = torch.from_numpy(golden["ptq1_W"]).to(dev)
+    e = ops.expand_f16(W, K, N).cpu().numpy()
+    assert np.array_equal(e.view(np.uint16), golden["expand_f16"].view(np.uint16))
+    T8, SW = ops.expand_i8(W, K, N)
+    assert np.array_equal(T8.cpu().numpy(), golden["ptq1_trits"])
+    assert np.array_equal(SW.cpu().numpy(), golden["ptq1_scales"].astype(np.float32))
+
+
+def test_expand_random_bytes_bit_exact(dev):
+    # arbitrary bytes (incl. 243..255, never produced by the quantiser) decode like the oracle
+    rng = np.random.default_rng(11)
+    N, K = 64, 1024
+    W_np = rng.integers(0, 256, (N, K // 128 * 28), dtype=np.uint8)
+    W_np.reshape(N, K // 128, 28)[:, :, 26:28] = np.array([0.375], np.float16).view(np.uint8)  # finite scales
+    W = torch.from_numpy(W_np).to(dev)
+    e = ops.expand_f16(W, K, N).cpu().numpy()
+    assert np.array_equal(e.view(np.uint16), orc.expand_f16(W_np, K, N).view(np.uint16))
+    T8, _ = ops.expand_i8(W, K, N)
+    assert np.array_equal(T8.cpu().numpy(), orc.expand_i8(W_np, K, N)[0])
+
+
+# ----------------------------------------------------------------------------- fp16 GEMM
+def test_gemm_f16_golden(dev, golden):
+    K, N = int(golden["ptq1_K"]), int(golden["ptq1_N"])
+    A = torch.from_numpy(golden["gemm_A"]).to(dev)
+    W = torch.from_numpy(golden["ptq1_W"]).to(dev)
+    C = ops.gemm_ptq1_f16(A, W, K, N).cpu().numpy()
+    assert rel_l2(C, golden["gemm_C"]).max() < 1e-5
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 16), (5, 384, 130), (130, 1024, 64), (257, 640, 300)])
+def test_gemm_f16_random(dev, M, K, N):
+    W_np, _, _ = orc.synth_ptq1(N, K, M + K + N)
+    A_np = orc.synth_x(M, K, M + 1)
+    C = ops.gemm_ptq1_f16(torch.from_numpy(A_np).to(dev), torch.from_numpy(W_np).to(dev), K, N).cpu().numpy()
+    ref = orc.gemm_f16(A_np, W_np, M, K, N)
+    assert rel_l2(C, ref).max() < 1e-5
+
+
+@pytest.mark.parametrize("K,N", [(5120, 17408), (17408, 5120)])
+def test_gemm_f16_pp512_full_shape(dev, K, N):
+    """BASELINE config 4 shapes: every row vs torch fp32 on the bit-exact expanded weights,
+    plus oracle rows; fp16 output within fp16 rounding of the fp32 output."""
+    M = 512
+    W_np, _, _ = orc.synth_ptq1(N, K, K ^ N)
+    A_np = orc.synth_x(M, K, 99)
+    A = torch.from_numpy(A_np).to(dev)
+    W = torch.from_numpy(W_np).to(dev)
+    C = ops.gemm_ptq1_f16(A, W, K, N)
+    ref = A.float() @ ops.expand_f16(W, K, N).float().T
+    # both sides accumulate in fp32 in different orders: ~eps*sqrt(K) apart
+    assert rel_l2(C.cpu().numpy(), ref.cpu().numpy()).max() < 5e-5
+    Ch = ops.gemm_ptq1_f16(A, W, K, N, out_dtype=torch.float16)
+    assert torch.equal(Ch, C.half())
+    rows = [0, 1, 255, 511]
+    ref_o = orc.gemm_f16(np.ascontiguousarray(A_np[rows]), W_np[:64], len(rows), K, 64)
+    assert rel_l2(C.cpu().numpy()[rows, :64], ref_o).max() < 1e-5
+
+
+# ----------------------------------------------------------------------------- int8 path
+def test_quant_rows_bit_exact(dev, golden):
+    Q, SX = ops.quant_rows(torch.from_numpy(golden["qr_X"]).to(dev))
+    assert np.array_equal(Q.cpu().numpy(), golden["qr_Q"])
+    assert np.array_equal(SX.cpu().numpy().view(np.uint32), golden["qr_SX"].view(np.uint32))
+    X = orc.synth_x(37, 5120, 12)
+    X[3, 128:256] = 0
+    Q, SX = ops.quant_rows(torch.from_numpy(X).to(dev), ldS=64)
+    Qo, SXo = orc.quant_rows(X, 37, 5120, 64)
+    assert np.array_equal(Q.cpu().numpy(), Qo)
+    assert np.array_equal(SX.cpu().numpy()[:, :37].view(np.uint32), SXo[:, :37].view(np.uint32))
+
+
+def test_gemm_i8_integer_sums_exact(dev):
+    """Unit scales: C equals the exact integer sum (< 2^24), whatever the order."""
+    rng = np.random.default_rng(13)
+    M, K, N = 70, 1024, 96
+    t = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    W_np = orc.pack(t, np.ones((N, K // 128), np.float16))
+    A8 = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    SX = np.ones((K // 128, M), np.float32)
+    C = ops.gemm_ptq1_i8(torch.from_numpy(A8).to(dev), torch.from_numpy(SX).to(dev),
+                         torch.from_numpy(W_np).to(dev), K, N).cpu().numpy()
+    want = A8.astype(np.int64) @ t.astype(np.int64).T
+    assert np.array_equal(C.astype(np.int64), want)
+
+
+def test_gemm_i8_golden_and_random(dev, golden):
+    K, N = int(golden["ptq1_K"]), int(golden["ptq1_N"])
+    C = ops.gemm_ptq1_i8(torch.from_numpy(golden["qr_Q"]).to(dev), torch.from_numpy(golden["qr_SX"]).to(dev),
+                         torch.from_numpy(golden["ptq1_W"]).to(dev), K, N).cpu().numpy()
+    ref = orc.gemm_i8(golden["qr_Q"], golden["qr_SX"], golden["ptq1_W"], 3, K, N)
+    assert rel_l2(C, ref).max() < 1e-6
+    M, K, N = 200, 5120, 160
+    W_np, _, _ = orc.synth_ptq1(N, K, 14)
+    X = orc.synth_x(M, K, 15)
+    Q, SX = orc.quant_rows(X, M, K)
+    Cg = ops.gemm_ptq1_i8(torch.from_numpy(Q).to(dev), torch.from_numpy(SX).to(dev),
+                          torch.from_numpy(W_np).to(dev), K, N).cpu().numpy()
+    assert rel_l2(Cg, orc.gemm_i8(Q, SX, W_np, M, K, N)).max() < 1e-6
+
+
+# ----------------------------------------------------------------------------- dispatcher
+def test_dispatch_offsets_and_i8_selection(dev):
+    K, N = 1024, 64
+    W1, _, _ = orc.synth_ptq1(N, K, 21)
+    W2, _, _ = orc.synth_ptq1(N, K, 22)
+    buf = torch.from_numpy(np.concatenate([W1.ravel(), W2.ravel()])).to(dev)
+    d = Dispatch(buf)
+    off2 = W1.size
+    x = torch.from_numpy(orc.synth_x(1, K, 23, np.float32)).to(dev)
+    y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    d.gemv(off2, x, y, K, N)
+    assert rel_l2(y.cpu().numpy(), orc.gemv_ptq1(W2, x.cpu().numpy(), K, N, 1)).max() < 2e-4
+    M = 48
+    A = torch.from_numpy(orc.synth_x(M, K, 24)).to(dev)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    d.set_i8("ffn")
+    A8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    SX = torch.empty((K // 128, M), dtype=torch.float32, device=dev)
+    d.prefill(off2, A, C, K, N, "gate", A8, SX)          # int8 path
+    Q, SXo = orc.quant_rows(A.cpu().numpy(), M, K)
+    assert np.array_equal(A8.cpu().numpy(), Q)
+    assert rel_l2(C.cpu().numpy(), orc.gemm_i8(Q, SXo, W2, M, K, N)).max() < 1e-6
+    d.prefill(off2, A, C, K, N, "down")                  # fp16 exact path
+    assert rel_l2(C.cpu().numpy(), orc.gemm_f16(A.cpu().numpy(), W2, M, K, N)).max() < 1e-5
