@@ -42,7 +42,8 @@ const char* kata_version(void);
 
 /* ---------------------------------------------------------------- decode GEMVs -------
  * y[t][n] = sum_b d[n,b] * sum_e trit[n,b,e] * x[t][128b+e], fp32 out, t < T, T in {1,2}.
- * K % 128 == 0, N >= 1.  y is [T][N] fp32.
+ * K % 128 == 0, K <= kata_gemv_ptq1_max_k(T) (45056 for T=1, 20992 for T=2), N >= 1.
+ * y is [T][N] fp32.
  * Replaces Engine::dGemvPtq1 (src/engine.cpp:97-101, src/engine.h:155; kernel
  * k_gemv_v1_nr4_sg4, shaders/gemv_fast.metal:9-50) for T = 1, and the `gv` lambda of
  * Engine::verify2 (src/engine.cpp:440-443; k_gemv_lut2_nr4_sg4, shaders/mtp.metal:164-205,
@@ -60,6 +61,8 @@ int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, f
  * write the GEMV's activation layout directly (k_add_rms_fwht_t flag 4,
  * shaders/prefill.metal:97). */
 size_t kata_gemv_ptq1_xprep_bytes(int K, int T);
+/* Largest K the PTQ1_0 GEMV accepts for T tokens (its prepared activation lives in LDS). */
+int kata_gemv_ptq1_max_k(int T);
 int kata_gemv_ptq1_prep(const void* x, int x_dtype, int x_layout, void* xprep, int K, int T,
                         void* stream);
 int kata_gemv_ptq1_prepped(const uint8_t* W, const void* xprep, float* y, int K, int N, int T,

@@ -36,6 +36,7 @@ SIGNATURES = {
     "kata_version": (ctypes.c_char_p, []),
     "kata_gemv_ptq1": (I, [P, P, I, I, P, I, I, I, P]),
     "kata_gemv_ptq1_xprep_bytes": (SZ, [I, I]),
+    "kata_gemv_ptq1_max_k": (I, [I]),
     "kata_gemv_ptq1_prep": (I, [P, I, I, P, I, I, P]),
     "kata_gemv_ptq1_prepped": (I, [P, P, P, I, I, I, P]),
     "kata_gemv_q8_0": (I, [P, P, I, P, I, I, I, P]),

@@ -68,6 +68,7 @@ int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, con
     if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
     if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
     if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
+    if (K > kata::gemv_max_k(T)) return fail(KATA_EINVAL, "K=%d exceeds %d for T=%d", K, kata::gemv_max_k(T), T);
     if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
     if (x_layout != KATA_X_ROWS && x_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "x_layout=%d", x_layout);
     if (x_layout == KATA_X_HALF2 && (T != 2 || x_dtype != KATA_F16))
@@ -89,6 +90,8 @@ size_t kata_gemv_ptq1_xprep_bytes(int K, int T) {
     if (K <= 0 || K % 128 != 0 || (T != 1 && T != 2)) return 0;
     return kata::xprep_layout(K, T).bytes;
 }
+
+int kata_gemv_ptq1_max_k(int T) { return (T == 1 || T == 2) ? kata::gemv_max_k(T) : 0; }
 
 int kata_gemv_ptq1_prep(const void* x, int x_dtype, int x_layout, void* xprep, int K, int T, void* stream) {
     int rc = check_gemv_args((const void*)256, x, x_dtype, x_layout, (const void*)256, K, 1, T);   // x-only checks

@@ -16,6 +16,7 @@ hipError_t launch_gemv_prep(const void* x, int x_dtype, int x_layout, uint8_t* x
                             hipStream_t s);
 hipError_t launch_gemv_ptq1(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int T,
                             hipStream_t s);
+int gemv_max_k(int T);   // largest K whose prepared activation fits the GEMV's LDS
 
 // ---- Q8_0 GEMV (gemv_q8.hip)
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,

@@ -42,8 +42,12 @@ def test_golden_t1_t2(dev, golden):
     (128, 16, 1, np.float16), (128, 1, 1, np.float32), (256, 17, 2, np.float16),
     (640, 33, 1, np.float32), (1024, 64, 2, np.float32), (5120, 80, 1, np.float16),
     (6144, 48, 2, np.float16), (17408, 32, 1, np.float16), (17408, 20, 2, np.float32),
+    (-2, 16, 2, np.float16), (-1, 16, 1, np.float32),      # largest K per T (LDS bound)
 ])
 def test_random_vs_oracle(dev, K, N, T, dtype):
+    if K < 0:
+        from kata_amd.capi import lib
+        K = lib().kata_gemv_ptq1_max_k(-K)
     seed = K * 131 + N * 7 + T
     W, _, _ = orc.synth_ptq1(N, K, seed)
     x = orc.synth_x(T, K, seed + 1, dtype)
