@@ -83,6 +83,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=2048)
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -118,30 +119,52 @@ def main():
                 done.add(grp)
             ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
 
+    def gemvs_only(i):
+        ws = copies[i % ncopies]
+        for j, (name, K, N, grp) in enumerate(SWEEP):
+            ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
+
+    # One HIP graph per (function, weight copy): replaying graph i % ncopies is step i, so
+    # exactly K steps are timed, each with the per-launch overhead of a graph launch.
+    use_graph = not args.no_graph
+    cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
+    runners = {}
+    for fname, fn in (("step", step), ("gemv", gemvs_only)):
+        for i in range(2):
+            fn(i)                                 # first calls set kernel attributes
+        torch.cuda.synchronize()
+        if use_graph:
+            graphs = []
+            for i in range(ncopies):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=cap_stream):
+                    fn(i)
+                graphs.append(g)
+            runners[fname] = lambda i, graphs=graphs: graphs[i % ncopies].replay()
+        else:
+            runners[fname] = fn
+
+    def timed(fname, n_steps):
+        run = runners[fname]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(n_steps):
+            run(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
     for i in range(args.warmup):
-        step(i)
+        runners["step"](i)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_total = e0.elapsed_time(e1)
+    ms_total = timed("step", args.steps)
     ms_step = ms_total / args.steps
     value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
 
     # ---- dominant kernel alone: the GEMV launches of the sweep without the preps
-    reps = max(20, args.steps // 2)
-    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    g0.record(stream)
-    for i in range(reps):
-        ws = copies[i % ncopies]
-        for j, (name, K, N, grp) in enumerate(SWEEP):
-            ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
-    g1.record(stream)
-    torch.cuda.synchronize()
-    gemv_launch_us = g0.elapsed_time(g1) * 1e3 / (reps * len(SWEEP))
+    steps_g = max(20, args.steps // 2)
+    gemv_launch_us = timed("gemv", steps_g) * 1e3 / (steps_g * len(SWEEP))
     bytes_per_launch = set_bytes / len(SWEEP)
     achieved = bytes_per_launch / (gemv_launch_us * 1e-6) / 1e9
 

@@ -42,7 +42,7 @@ const char* kata_version(void);
 
 /* ---------------------------------------------------------------- decode GEMVs -------
  * y[t][n] = sum_b d[n,b] * sum_e trit[n,b,e] * x[t][128b+e], fp32 out, t < T, T in {1,2}.
- * K % 128 == 0, K <= kata_gemv_ptq1_max_k(T) (45056 for T=1, 20992 for T=2), N >= 1.
+ * K % 128 == 0, K <= kata_gemv_ptq1_max_k(T) (47104 for T=1, 23040 for T=2), N >= 1.
  * y is [T][N] fp32.
  * Replaces Engine::dGemvPtq1 (src/engine.cpp:97-101, src/engine.h:155; kernel
  * k_gemv_v1_nr4_sg4, shaders/gemv_fast.metal:9-50) for T = 1, and the `gv` lambda of

@@ -4,26 +4,24 @@
 // (shaders/gemv.metal:5-20; fast forms shaders/gemv_fast.metal:9-50, shaders/mtp.metal:164-205).
 //
 // Design (MI355X-first, not the reference's simdgroup float decode):
-//  * The packed weight bytes are never expanded in memory.  A wave owns a 16-row tile and
-//    a slice of its K blocks; per 128-weight block each lane holds 8 bytes of one row
-//    (lane group g = lane/16 takes block bytes 20..27, 0..7, 8..15, 16..19) and turns them
-//    into base-3 digits {0,1,2}: digits 1..4 of a byte come from one 4-byte LDS table
-//    entry, digit 0 = (3b) >> 8 from packed 16-bit multiplies.  The digits are the B
-//    operand (B[k][row]) of three v_mfma_i32_16x16x64_i8 per block.
+//  * The packed weight bytes are never expanded in memory.  Per 128-weight block four lanes
+//    each hold 8 bytes of it (lane group g = lane/16 takes block bytes 20..27, 0..7, 8..15
+//    or 16..19, rotated by the block's position) and turn them into base-3 digits {0,1,2}:
+//    digits 1..4 of a byte come from one 4-byte LDS table entry, digit 0 = (3b) >> 8 from
+//    16-bit-lane multiplies.  The digits are the B operand (B[k][column]) of three
+//    v_mfma_i32_16x16x64_i8 per block.
 //  * The activation is the A operand (A[i][k]) in a prepared integer form: per 128-block
 //    a scale s = amax/32639 and q = rint(x/s) split into two int8 limbs (q = 256*hi + lo);
-//    A rows are (token, limb), so T = 2 costs no extra matrix-core work.  The matrix core
-//    sums digit*limb exactly in int32; the epilogue forms sum(trit*q) = 256*D_hi + D_lo -
-//    sum(q) per block and token and accumulates y += d * s * that in fp32.  The only
+//    A rows are (block, token, limb), so T = 2 costs no extra matrix-core work.  The matrix
+//    core sums digit*limb exactly in int32; the epilogue forms sum(trit*q) = 256*D_hi +
+//    D_lo - sum(q) per block and token and accumulates y += d * s * that in fp32.  The only
 //    approximation is the 16-bit block-fixed-point activation (|x - s*q| <= amax/65278),
 //    far inside the 1e-3 relative-L2 contract.
-//  * Work unit = a 4-row tile.  The 16 B columns of the MFMA are (row r, K-quarter kq) and
-//    the 16 A rows are (K-quarter, token, limb), so one wave decodes all four quarters of
-//    four rows at once and the off-diagonal quarter products are never read.  Each wave
-//    owns whole tiles (wave w takes tiles w, w + waves, ...): no barriers and no partial
-//    sums outside the wave; the four quarter sums of a row are added with lane shuffles.
-//    The digit table and the prepared activation are put in LDS once per workgroup; each
-//    wave loads the next chunk's weight bytes while it decodes the current one.
+//  * Work unit = a 4-row tile.  The 16 B columns of the MFMA are (row r, block 4c + kq)
+//    and the 16 A rows are (block 4c + kq, token, limb), so one wave step decodes 4
+//    consecutive blocks of 4 rows (four 112-byte runs of the matrix) and the products of
+//    mismatched blocks are never read.  One 1024-thread workgroup per CU splits its tile
+//    range evenly over its 16 waves (see the kernel comment); no atomics, deterministic.
 #include "common.h"
 #include "launch.h"
 
@@ -37,46 +35,45 @@ constexpr float kQMax = 32639.0f;   // |q| <= 32639 keeps hi = (q+128)>>8 inside
 constexpr int kMfmaPerBlock = 3;
 constexpr int kAImageBytes = kMfmaPerBlock * 4 * 16;   // per block and A row (token, limb)
 
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // A block is read as four 8-byte segments starting at bytes 20, 0, 8, 16 (segment 3 uses
 // only bytes 16..19; bytes 20..23 belong to segment 0).  Segment 0 carries the scale.
-// Lane group g working on K-quarter kq reads segment (g - kq) & 3, so the lanes whose
-// result rows hold that quarter (g == kq) are the ones holding the scale.
+// Lane group g working on block 4c + kq reads segment (g - kq) & 3, so the lanes whose
+// result rows hold that block (g == kq) are the ones holding the scale.
 __host__ __device__ inline int gemv_seg_byte0(int seg) { return seg == 0 ? 20 : seg == 1 ? 0 : seg == 2 ? 8 : 16; }
 
 // Byte p and digit n of the A/B operand slot (segment seg, MFMA m, dword dw, byte kb),
 // or p = -1 for a slot that multiplies a zero activation.  With w0/w1 the lane's two
 // weight dwords (bytes b0..b7) the B dwords are
-//   m=0: L(b0) L(b1) L(b2) L(b3)     m=1: E(w0) O(w0) L(b4) L(b5)     m=2: L(b6) L(b7) E(w1) O(w1)
-// where L(b) = digits 1..4 of byte b and E/O = digit 0 of bytes (0,2) / (1,3) of the dword
-// in the low byte of each 16-bit half.
+//   m=0: L(b0) L(b1) L(b2) L(b3)     m=1: Z(w0) L(b4) L(b5) L(b6)     m=2: L(b7) Z(w1) 0 0
+// where L(b) = digits 1..4 of byte b and Z(w) = digit 0 of the dword's bytes 0..3.
 __host__ __device__ inline void gemv_slot(int seg, int m, int dw, int kb, int& p, int& n) {
     const int base = gemv_seg_byte0(seg);
     const int kind = m * 4 + dw;   // 0..11
-    // L slots: byte offset within the lane's 8 bytes; E/O slots: -(1 + word*2 + parity)
-    const int desc[12] = {0, 1, 2, 3, -1, -2, 4, 5, 6, 7, -3, -4};
+    // L slots: byte offset within the lane's 8 bytes; Z slots: -(1 + word); -9: unused
+    const int desc[12] = {0, 1, 2, 3, -1, 4, 5, 6, 7, -2, -9, -9};
     const int d = desc[kind];
+    if (d == -9) {
+        p = -1;
+        return;
+    }
     if (d >= 0) {
         p = base + d;
         n = kb + 1;
     } else {
-        const int s = -d - 1, word = s >> 1, par = s & 1;
-        if (kb & 1) { p = -1; return; }
-        p = base + word * 4 + par + kb;
+        p = base + (-d - 1) * 4 + kb;
         n = 0;
     }
     if (seg == 3 && p >= 20) p = -1;   // bytes 20..23 belong to segment 0
 }
 
-// One workgroup per virtual block vb (0 <= vb < 4*nq; blocks nb.. are zero padding so the
-// four K-quarters have nq blocks each).  Writes scale s and sum(q) per token and the A
-// image [m 3][g 4][i 2T][16 B], i = 2*t + limb, laid out for lane group g reading segment
-// (g - vb/nq) & 3.
+// One workgroup per virtual block vb (0 <= vb < 4*nq; blocks nb.. are zero padding so
+// every tile has nq steps of 4 blocks).  Writes the pair (scale s as float, sum(q) as int)
+// per token at scales[vb][t] and the A image [m 3][g 4][i 2T][16 B], i = 2*t + limb, laid
+// out for lane group g reading segment (g - (vb & 3)) & 3.
 template <int T>
 __global__ __launch_bounds__(128) void k_gemv_prep(const void* __restrict__ x, int x_dtype, int x_layout,
-                                                   uint8_t* __restrict__ xprep, int K, int nq, size_t off_sq,
-                                                   size_t off_a) {
+                                                   uint8_t* __restrict__ xprep, int K, int nq, size_t off_a) {
     __shared__ int16_t qs[T][128];
     __shared__ float red_f[2][T];
     __shared__ int red_i[2][T];
@@ -102,11 +99,11 @@ __global__ __launch_bounds__(128) void k_gemv_prep(const void* __restrict__ x, i
         int s = q;
         for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
         if (lane == 0) red_i[wv][t] = s;
-        if (e == 0) ((float*)xprep)[b * T + t] = amax / kQMax;
+        if (e == 0) ((float*)xprep)[(b * T + t) * 2] = amax / kQMax;
     }
     __syncthreads();
-    if (e < T) ((int*)(xprep + off_sq))[b * T + e] = red_i[0][e] + red_i[1][e];
-    const int kq = b / nq;
+    if (e < T) ((int*)xprep)[(b * T + e) * 2 + 1] = red_i[0][e] + red_i[1][e];
+    const int kq = b & 3;
     uint32_t* out = (uint32_t*)(xprep + off_a + (size_t)b * kAImageBytes * 2 * T);
     for (int w = e; w < kAImageBytes / 4 * 2 * T; w += 128) {
         const int dw = w & 3, i = (w >> 2) % (2 * T), g = (w / (8 * T)) & 3, m = w / (32 * T);
@@ -139,213 +136,277 @@ __device__ inline uint32_t lut_addr(uint32_t w, int q, uint32_t laneoff) {
 }
 __host__ __device__ constexpr int lut_bytes(int LR) { return 256 * (4 << LR); }
 
-// digit 0 of bytes (0,2) (odd = false) or (1,3) (odd = true) of w, in the low byte of each
-// 16-bit half; v_perm spreads the two bytes into the halves
-__device__ inline uint32_t digit0_pair(uint32_t w, bool odd) {
-    const uint32_t spread = __builtin_amdgcn_perm(0u, w, odd ? 0x0c030c01u : 0x0c020c00u);
-    u16x2 v = __builtin_bit_cast(u16x2, spread);
-    v = (v * (u16x2){3, 3}) >> (u16x2){8, 8};
-    return __builtin_bit_cast(uint32_t, v);
+// digit 0 = (3b) >> 8 of the four bytes of w, byte k of the result for byte k of w.  Bytes
+// (0,2) and (1,3) are spread into 16-bit lanes and tripled (3b < 768 cannot carry into the
+// next lane); the digit is then byte 1 of its lane.
+__device__ inline uint32_t digit0_word(uint32_t w) {
+    const uint32_t e = w & 0x00ff00ffu, o = __builtin_amdgcn_perm(0u, w, 0x0c030c01u);
+    const uint32_t e3 = e + (e << 1), o3 = o + (o << 1);
+    return __builtin_amdgcn_perm(o3, e3, 0x07030501u);
 }
 
-// 32-bit LDS load at a byte address of this kernel's dynamic LDS, which starts at address 0
-// (the kernel declares no static LDS), so table addresses need no base added.
-__device__ inline uint32_t lds_u32(uint32_t addr) {
-    return *(const __attribute__((address_space(3))) uint32_t*)(size_t)addr;
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+// 32-bit load at byte offset addr of an LDS array; for the digit table, the kernel's only
+// static LDS, the base is address 0 and folds away.
+__device__ inline uint32_t lds_u32(lds_u8* base, uint32_t addr) {
+    return *(__attribute__((address_space(3))) const uint32_t*)(base + addr);
 }
 
-// Work split: one 1024-thread workgroup (16 waves) per CU owns a contiguous range of
-// tiles, taken in rounds of up to RMAX tiles.  A round's (tile, block step) pairs are cut
-// into 16 equal contiguous runs, one per wave; a wave adds up each tile its run touches and
-// writes the partial sum to LDS, and after the round's barrier the partials are summed in
-// wave order (deterministic).  Lane x + 16*g: B column x = (row r = x & 3, quarter
-// kq = x >> 2), A row x = (quarter x >> 2, token (x >> 1) & 1, limb x & 1); result rows
-// 4g..4g+3 belong to quarter g, so lane r + 20*kq holds row r's quarter-kq sum.  Runs are
-// walked in chunks of at most CH steps inside one tile, the next chunk's weights in flight,
-// each block's operands issued one block ahead of its MFMAs.  Dynamic LDS: digit table,
-// A image (384*T B per virtual block, 64 B between quarters), scales and sums, partials.
+// Work split: one 1024-thread workgroup (16 waves) per CU owns the contiguous tile range
+// [wt0, wt0 + tpw).  Its (tile, block step) pairs, numbered s = (tile - wt0) * nq + c, are
+// cut into 16 equal contiguous runs, one per wave.  Lane x + 16*g: B column x = (row
+// r = x & 3, block 4c + kq with kq = x >> 2), A row x = (block 4c + (x >> 2), token
+// (x >> 1) & 1, limb x & 1); result rows 4g..4g+3 belong to block 4c + g, so lane
+// 20*q + r holds row r's sum over blocks 4c + q ("quarter" q of the tile's blocks).
+//
+// Timeline: the digit table is written and the activation staging (global -> LDS DMA) is
+// issued by every wave before any wave issues weight loads (vector-memory loads complete
+// in order per CU, so staging queued behind the ring would arrive only after it); then
+// every wave keeps D weight steps in flight in a register ring (step j in slot j % D) and
+// decodes step j as soon as its own load has landed.
+// Each step's operands are issued one step ahead of its MFMAs.  When a tile's last step
+// of a run is done the 16 diagonal lanes store their sums to the wave's LDS slot for that
+// tile; after one barrier the workgroup adds the slots of each tile over waves and quarters
+// in fixed order (deterministic).  Dynamic LDS: A image (384*T B per virtual block, 64 B
+// between quarters), (scale, sum) pairs, per-wave tile sums [16][slots][T][16].
 constexpr int kWaves = 16;
-constexpr int kRoundTiles = 32;
-template <int T, int LR, int CH>
+// LDS bytes of the A image (4 quarters, 64 B apart) and of the (scale, sum) pairs, rounded
+// up to whole staging chunks
+__host__ __device__ inline int gemv_a_lds_bytes(int qbytes) { return (4 * (qbytes + 64) + 1023) & ~1023; }
+__host__ __device__ inline int gemv_s_lds_bytes(int nbv, int T) { return (8 * nbv * T + 1023) & ~1023; }
+// static LDS of the GEMV kernel: digit table + run_tiles
+__host__ __device__ constexpr int gemv_static_lds_bytes(int LR) { return lut_bytes(LR) + kWaves * 8; }
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int T, int LR, int D>
 __global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xprep,
-                                                    float* __restrict__ y, int K, int N, int nq, int tpw,
-                                                    size_t off_sq, size_t off_a) {
+                                                    float* __restrict__ y, int K, int N, int nq, int tpw, int slots,
+                                                    size_t off_a) {
+    static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by step parity");
     constexpr int ASTRIDE = 4 * 2 * T * 16;      // A image bytes per (virtual block, MFMA)
     constexpr int REPS = 1 << LR;
     constexpr int QPAD = 64;
+    // digit table: the kernel's only static LDS besides run_tiles, at LDS address 0
+    __shared__ uint4 lut[lut_bytes(LR) / 16];
+    __shared__ int2 run_tiles[kWaves];          // first and last tile (local) of each wave's run
     extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int x = lane & 15, g = lane >> 4;
     const int r = x & 3, kq = x >> 2;
     const int nb = K >> 7, nbv = 4 * nq;
     const int tiles = (N + 3) >> 2;
     const int wt0 = blockIdx.x * tpw, wt1 = min(tiles, wt0 + tpw);
-    const size_t row_bytes = (size_t)nb * kBlockBytes;
-    const int seg_off = gemv_seg_byte0((g - kq) & 3);
-    const int qbase = kq * nq;                   // this lane's first (virtual) block
+    const int S = (wt1 - wt0) * nq;
+    const int s0 = (wave * S) / kWaves, s1 = ((wave + 1) * S) / kWaves;
+    const int n = s1 - s0;                       // this wave's run length (wave-uniform)
+    const int c0 = s0 % nq;
+    if (lane == 0) run_tiles[wave] = n > 0 ? make_int2(s0 / nq, (s1 - 1) / nq) : make_int2(1 << 30, -1);
 
-    uint32_t wl[CH], wh[CH];
-    auto load_chunk = [&](int tile, int c, int n) {
-        const uint8_t* rp = W + (size_t)min(tile * 4 + r, N - 1) * row_bytes + seg_off;
+    // Digit table.  Consecutive threads store consecutive 16-byte words (no bank
+    // conflicts); word o holds 4 replicas of entry o / (REPS / 4).
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            if (i < n) {
-                const int blk = min(qbase + c + i, nb - 1);   // padding blocks read any real block
-                const uint32_t* q = (const uint32_t*)(rp + (size_t)blk * kBlockBytes);
-                wl[i] = q[0];
-                wh[i] = q[1];
+    for (int i = 0; i < lut_bytes(LR) / 16 / 1024; i++) {
+        const int o = tid + i * 1024;
+        const uint32_t bv = (uint32_t)o / (REPS / 4);
+        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
+                       m4 = (m3 * 3u) & 0xffu;
+        const uint32_t e = ((m1 * 3u) >> 8) | (((m2 * 3u) >> 8) << 8) | (((m3 * 3u) >> 8) << 16) |
+                           (((m4 * 3u) >> 8) << 24);
+        lut[o] = make_uint4(e, e, e, e);
+    }
+
+    // Weight loads: raw buffer loads with 32-bit offsets; bytes past the matrix read as 0
+    // (rows >= N).  Padding blocks (past K) reread the row's last block; their activation,
+    // scale and sum are zero.  Every ring slot is reloaded once per step, also past the
+    // run's end, so all paths issue the same loads and the compiler's wait counts stay
+    // exact.
+    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
+    // loads past the run's end go through an empty descriptor: zeros, no memory access
+    const __amdgpu_buffer_rsrc_t wnone = __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, 0, 0x00020000);
+    const uint32_t qoff = (uint32_t)kq * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
+    const uint32_t qlim = (uint32_t)(nb - 1) * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
+    uint32_t rowoff = (uint32_t)((wt0 + s0 / nq) * 4 + r) * row_bytes;
+    int lc = c0, ld_left = n;                    // load cursor (wave-uniform)
+    uint32_t lcb = (uint32_t)c0 * 4 * kBlockBytes;   // lc * 4 blocks
+    uint32_t wl[D], wh[D];
+    auto load_next = [&](int slot) {
+        const uint32_t off = rowoff + min(qoff + lcb, qlim);
+        const u32x2 w =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ld_left > 0 ? wrsrc : wnone, (int)off, 0, 0));
+        wl[slot] = w.x;
+        wh[slot] = w.y;
+        if (ld_left > 1) {
+            lcb += 4 * kBlockBytes;
+            if (++lc == nq) {
+                lc = 0;
+                lcb = 0;
+                rowoff += 4 * row_bytes;
             }
         }
+        --ld_left;
     };
-    // this wave's run of round rt0..rt1: steps [s0, s1) of (tile - rt0) * nq + c
-    auto run_of = [&](int rt0, int rt1, int& s0, int& s1) {
-        const int S = (rt1 - rt0) * nq;
-        s0 = (wave * S) / kWaves;
-        s1 = ((wave + 1) * S) / kWaves;
-    };
-    auto chunk_len = [&](int s, int s1) { return min(min(CH, nq - s % nq), s1 - s); };
-    {
-        int s0, s1;
-        run_of(wt0, min(wt1, wt0 + kRoundTiles), s0, s1);
-        if (s0 < s1) load_chunk(wt0 + s0 / nq, s0 % nq, chunk_len(s0, s1));
-    }
-
+    // Activation staging by DMA; each wave fills whole 1 KB LDS chunks, padding slots load
+    // a duplicate in-range element.
     const int qbytes = nq * kAImageBytes * 2 * T;
-    uint8_t* As = smem + lut_bytes(LR);
-    const int a_bytes = 4 * (qbytes + QPAD);
-    float* sxs = (float*)(As + a_bytes);
-    int* sqs = (int*)(sxs + nbv * T);
-    float* part = (float*)(sqs + nbv * T);       // [kRoundTiles][kWaves][4 rows][T]
+    const int qvec = qbytes / 16;                // 16-byte vectors per quarter in xprep
+    const int a_bytes = gemv_a_lds_bytes(qbytes);
+    const int s_bytes = gemv_s_lds_bytes(nbv, T);
+    uint8_t* As = smem;
+    uint8_t* Ss = smem + a_bytes;                // (scale, sum) pairs [vb][t]
+    float* part = (float*)(Ss + s_bytes);        // [kWaves][slots][T][16]
     {
-        const uint4* src = (const uint4*)(xprep + off_a);
-        for (int o = tid; o < 4 * qbytes / 16; o += 1024) {
-            const int q = o / (qbytes / 16);
-            *(uint4*)(As + o * 16 + q * QPAD) = src[o];
+        typedef __attribute__((address_space(3))) void lds_void;
+        const uint4* a_src = (const uint4*)(xprep + off_a);
+        for (int ch = wave; ch < a_bytes / 1024; ch += kWaves) {
+            const int o = ch * 64 + lane;        // LDS vector index
+            // LDS quarter q holds blocks 4c + q, c = 0..nq-1, in order
+            const int q = o / (qvec + QPAD / 16), w = min(o - q * (qvec + QPAD / 16), qvec - 1);
+            const int bv = kAImageBytes * 2 * T / 16;   // vectors per block
+            const int src = (4 * (w / bv) + min(q, 3)) * bv + w % bv;
+            __builtin_amdgcn_global_load_lds(a_src + src, (lds_void*)(As + ch * 1024), 16, 0, 0);
         }
-        const float* gsx = (const float*)xprep;
-        const int* gsq = (const int*)(xprep + off_sq);
-        for (int o = tid; o < nbv * T; o += 1024) { sxs[o] = gsx[o]; sqs[o] = gsq[o]; }
-        // table: groups of 4 threads compute one entry each and fill its replicas 4 at a time
-        {
-            const uint32_t bv = (uint32_t)tid >> 2;
-            const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
-                           m4 = (m3 * 3u) & 0xffu;
-            const uint32_t e = ((m1 * 3u) >> 8) | (((m2 * 3u) >> 8) << 8) | (((m3 * 3u) >> 8) << 16) |
-                               (((m4 * 3u) >> 8) << 24);
-            uint4* row = (uint4*)smem + bv * (REPS / 4);
-            for (int k = tid & 3; k < REPS / 4; k += 4) row[k] = make_uint4(e, e, e, e);
+        const uint4* s_src = (const uint4*)xprep;
+        const int svec = nbv * T * 8 / 16;      // (scale, sum) pairs: 16-byte vectors (T=1: 2 blocks)
+        for (int ch = wave; ch < s_bytes / 1024; ch += kWaves) {
+            const int o = min(ch * 64 + lane, svec - 1);
+            __builtin_amdgcn_global_load_lds(s_src + o, (lds_void*)(Ss + ch * 1024), 16, 0, 0);
         }
     }
+    // All staging DMA of the workgroup is issued before any wave issues its ring, so the
+    // staging is at the head of the CU's in-order vector-memory queue (no wait here).
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int u = 0; u < D; u++) load_next(u);
+    // The staging DMA is older than the D ring loads, so "at most D vector-memory loads
+    // pending" means it has landed; lgkmcnt(0) covers the table stores.  A bare s_barrier
+    // (a release fence would also wait for the ring) then publishes both.
+    __builtin_amdgcn_s_waitcnt((D & 15) | ((D >> 4) << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
 
     const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
+    lds_u8* lb = (lds_u8*)lut;
     // A rows with token >= T only feed result rows the epilogue never reads: those lanes
     // skip the activation loads and keep whatever their registers hold.
     const bool a_active = ((x >> 1) & 1) < T;
-    const uint8_t* xa = As + kq * QPAD + g * (2 * T * 16) + (a_active ? (x & (2 * T - 1)) : 0) * 16;
-    v4i A0[kMfmaPerBlock], A1[kMfmaPerBlock];
+    const uint8_t* xa = As + kq * (qbytes + QPAD) + g * (2 * T * 16) + (a_active ? (x & (2 * T - 1)) : 0) * 16;
+    const uint8_t* xs = Ss + kq * (8 * T);
+    const bool sum_lane = g == kq;               // lane 20*q + r: the diagonal quarter
+    float* my_part = part + (size_t)wave * slots * T * 16 + g * 4 + r;
+    v4i A0[kMfmaPerBlock], A1[kMfmaPerBlock], B0[kMfmaPerBlock], B1[kMfmaPerBlock];
+    uint4 SQ0, SQ1;
 #pragma unroll
     for (int m = 0; m < kMfmaPerBlock; m++) { A0[m] = v4i{0, 0, 0, 0}; A1[m] = v4i{0, 0, 0, 0}; }
 
-    for (int rt0 = wt0; rt0 < wt1; rt0 += kRoundTiles) {
-        const int rt1 = min(wt1, rt0 + kRoundTiles);
-        for (int o = tid; o < kRoundTiles * kWaves * 4 * T; o += 1024) part[o] = 0.0f;
-        __syncthreads();
-        int s, s1;
-        run_of(rt0, rt1, s, s1);
-        if (rt0 != wt0 && s < s1) load_chunk(rt0 + s / nq, s % nq, chunk_len(s, s1));
-        float acc[T];
+    // operands of step c (block qbase + c of this lane's quarter)
+    auto issue = [&](int c, uint32_t w0, uint32_t w1, v4i* A, v4i* B, uint4& SQ) {
+        const uint8_t* pa = xa + c * (kMfmaPerBlock * ASTRIDE);
+        if (a_active) {
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[t] = 0.0f;
-        while (s < s1) {
-            const int tl = s / nq, c = s - tl * nq;
-            const int n = chunk_len(s, s1);
-            uint32_t cl[CH], chh[CH];
+            for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(pa + m * ASTRIDE);
+        }
+        if (T == 1) {
+            const uint2 v = *(const uint2*)(xs + c * 32);
+            SQ.x = v.x;
+            SQ.y = v.y;
+        } else {
+            SQ = *(const uint4*)(xs + c * 64);
+        }
+        B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 1, laneoff)),
+                   (int)lds_u32(lb, lut_addr<LR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 3, laneoff))};
+        B[1] = v4i{(int)digit0_word(w0), (int)lds_u32(lb, lut_addr<LR>(w1, 0, laneoff)),
+                   (int)lds_u32(lb, lut_addr<LR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w1, 2, laneoff))};
+        B[2] = v4i{(int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff)), (int)digit0_word(w1), 0, 0};
+    };
+    float acc[T];
 #pragma unroll
-            for (int i = 0; i < CH; i++) { cl[i] = wl[i]; chh[i] = wh[i]; }
-            const int sn = s + n;
-            if (sn < s1) load_chunk(rt0 + sn / nq, sn % nq, chunk_len(sn, s1));
+    for (int t = 0; t < T; t++) acc[t] = 0.0f;
+    auto finish = [&](uint32_t dbits, const v4i* A, const v4i* B, const uint4& SQ) {
+        v4i Dm = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], Dm, 0, 0, 0);
+        const float d = half_bits_to_float(dbits >> 16);
+        const uint32_t sq[4] = {SQ.x, SQ.y, SQ.z, SQ.w};
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const int v = Dm[2 * t] * 256 + Dm[2 * t + 1] - (int)sq[2 * t + 1];
+            acc[t] += (d * __builtin_bit_cast(float, sq[2 * t])) * (float)v;
+        }
+    };
 
-            auto issue = [&](int i, v4i* A, v4i* B) {
-                const int vb = qbase + c + i;
-                if (a_active) {
+    // compute cursor: step cc of the current tile, `left` steps of it remain in this run's
+    // view of the tile, cs = tile slot (0 = the run's first tile)
+    int cc = c0, left = nq - c0, cs = 0;
+    auto flush_if_done = [&]() {
+        if (--left == 0) {
+            if (sum_lane) {
 #pragma unroll
-                    for (int m = 0; m < kMfmaPerBlock; m++)
-                        A[m] = *(const v4i*)(xa + (vb * kMfmaPerBlock + m) * ASTRIDE);
-                }
-                const uint32_t w0 = cl[i], w1 = chh[i];
-                B[0] = v4i{(int)lds_u32(lut_addr<LR>(w0, 0, laneoff)),
-                           (int)lds_u32(lut_addr<LR>(w0, 1, laneoff)),
-                           (int)lds_u32(lut_addr<LR>(w0, 2, laneoff)),
-                           (int)lds_u32(lut_addr<LR>(w0, 3, laneoff))};
-                B[1] = v4i{(int)digit0_pair(w0, false), (int)digit0_pair(w0, true),
-                           (int)lds_u32(lut_addr<LR>(w1, 0, laneoff)),
-                           (int)lds_u32(lut_addr<LR>(w1, 1, laneoff))};
-                B[2] = v4i{(int)lds_u32(lut_addr<LR>(w1, 2, laneoff)),
-                           (int)lds_u32(lut_addr<LR>(w1, 3, laneoff)),
-                           (int)digit0_pair(w1, false), (int)digit0_pair(w1, true)};
-            };
-            auto finish = [&](int i, const v4i* A, const v4i* B) {
-                const int vb = qbase + c + i;
-                v4i D = {0, 0, 0, 0};
-#pragma unroll
-                for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], D, 0, 0, 0);
-                const float d = half_bits_to_float(chh[i] >> 16);
-#pragma unroll
-                for (int t = 0; t < T; t++) {
-                    const int v = D[2 * t] * 256 + D[2 * t + 1] - sqs[vb * T + t];
-                    acc[t] += (d * sxs[vb * T + t]) * (float)v;
-                }
-            };
-            v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
-            issue(0, A0, B0);
-#pragma unroll
-            for (int i = 0; i < CH; i++) {
-                if (i < n) {
-                    if (i + 1 < n) {
-                        if (i & 1) issue(i + 1, A0, B0);
-                        else issue(i + 1, A1, B1);
-                    }
-                    if (i & 1) finish(i, A1, B1);
-                    else finish(i, A0, B0);
-                }
+                for (int t = 0; t < T; t++) my_part[(cs * T + t) * 16] = acc[t];
             }
-            s = sn;
-            if (c + n == nq || s == s1) {
-                // this wave's part of tile tl: add the quarters (lane r + 20*kq) in order
 #pragma unroll
-                for (int t = 0; t < T; t++) {
-                    float sum = 0.0f;
+            for (int t = 0; t < T; t++) acc[t] = 0.0f;
+            ++cs;
+            left = nq;
+            cc = 0;
+        } else {
+            ++cc;
+        }
+    };
+    if (n > 0) issue(cc, wl[0], wh[0], A0, B0, SQ0);
+    // One loop over passes of the ring: every slot is reloaded after use (also past the
+    // run's end), so the loads do not depend on the branches and their waits stay exact.
+    for (int j = 0; j < n; j += D) {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) sum += __shfl(acc[t], (lane & 3) + 20 * q);
-                    if (lane < 4) part[((tl * kWaves + wave) * 4 + lane) * T + t] = sum;
-                    acc[t] = 0.0f;
+        for (int u = 0; u < D; u++) {
+            if (j + u < n) {
+                const int cn = left == 1 ? 0 : cc + 1;
+                if (j + u + 1 < n) {
+                    if (u & 1) issue(cn, wl[(u + 1) % D], wh[(u + 1) % D], A0, B0, SQ0);
+                    else issue(cn, wl[(u + 1) % D], wh[(u + 1) % D], A1, B1, SQ1);
                 }
+                if (u & 1) finish(wh[u], A1, B1, SQ1);
+                else finish(wh[u], A0, B0, SQ0);
+                flush_if_done();
+            }
+            load_next(u);
+        }
+    }
+    if (left != nq) {                            // the run ended inside a tile: store it
+        left = 1;
+        flush_if_done();
+    }
+    __syncthreads();
+
+    // tile sums: every wave whose run touches the tile, in wave order, quarters in order
+    for (int o = tid; o < (wt1 - wt0) * 4 * T; o += 1024) {
+        const int tl = o / (4 * T), rr = (o / T) & 3, t = o % T;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; w2++) {
+            const int f = run_tiles[w2].x, l = run_tiles[w2].y;
+            if (tl >= f && tl <= l) {
+                const float* p = part + ((size_t)(w2 * slots + tl - f) * T + t) * 16 + rr;
+#pragma unroll
+                for (int q = 0; q < 4; q++) sum += p[4 * q];
             }
         }
-        __syncthreads();
-        for (int o = tid; o < (rt1 - rt0) * 4 * T; o += 1024) {
-            const int tl = o / (4 * T), rr = (o / T) & 3, t = o % T;
-            float sum = 0.0f;
-#pragma unroll
-            for (int w2 = 0; w2 < kWaves; w2++) sum += part[((tl * kWaves + w2) * 4 + rr) * T + t];
-            const int row = (rt0 + tl) * 4 + rr;
-            if (row < N) y[(size_t)t * N + row] = sum;
-        }
-        __syncthreads();
+        const int row = (wt0 + tl) * 4 + rr;
+        if (row < N) y[(size_t)t * N + row] = sum;
     }
 }
 
 }  // namespace
 
-// blocks per K-quarter (the last quarter is zero-padded)
+// steps (of 4 blocks) per tile; blocks past K are zero padding
 static int gemv_nq(int K) { return (K / kGroup + 3) / 4; }
 
 XprepLayout xprep_layout(int K, int T) {
     const size_t nbv = 4 * (size_t)gemv_nq(K);
     XprepLayout L;
-    L.off_sx = 0;
-    L.off_sq = ((nbv * T * 4) + 255) & ~(size_t)255;
-    L.off_a = (L.off_sq + nbv * T * 4 + 255) & ~(size_t)255;
+    L.off_s = 0;
+    L.off_a = ((nbv * T * 8) + 255) & ~(size_t)255;
     L.bytes = L.off_a + nbv * kAImageBytes * 2 * (size_t)T;
     return L;
 }
@@ -356,18 +417,27 @@ hipError_t launch_gemv_prep(const void* x, int x_dtype, int x_layout, uint8_t* x
     const int nq = gemv_nq(K);
     const dim3 grid(4 * nq), block(128);
     if (T == 1)
-        hipLaunchKernelGGL(k_gemv_prep<1>, grid, block, 0, s, x, x_dtype, x_layout, xprep, K, nq, L.off_sq, L.off_a);
+        hipLaunchKernelGGL(k_gemv_prep<1>, grid, block, 0, s, x, x_dtype, x_layout, xprep, K, nq, L.off_a);
     else
-        hipLaunchKernelGGL(k_gemv_prep<2>, grid, block, 0, s, x, x_dtype, x_layout, xprep, K, nq, L.off_sq, L.off_a);
+        hipLaunchKernelGGL(k_gemv_prep<2>, grid, block, 0, s, x, x_dtype, x_layout, xprep, K, nq, L.off_a);
     return hipGetLastError();
 }
 
 constexpr int kLdsMax = 160 * 1024;
 
-// dynamic LDS of a GEMV launch: digit table + A image + scales/sums + round partials
-static int gemv_lds_bytes(int K, int T, int LR) {
+constexpr int kRing = 12;    // weight steps in flight per wave
+
+// tile slots a wave's run can touch when a workgroup owns tpw tiles
+static int gemv_slots(int nq, int tpw) {
+    const int run = (tpw * nq + kWaves - 1) / kWaves;
+    return (run + nq - 1) / nq + 1;
+}
+
+// LDS of a GEMV launch (the static digit table, then the dynamic part): digit table + A image + scales/sums + per-wave tile sums
+static int gemv_lds_bytes(int K, int T, int LR, int slots) {
     const int nbv = 4 * gemv_nq(K);
-    return lut_bytes(LR) + nbv * kAImageBytes * 2 * T + 4 * 64 + nbv * 8 * T + kRoundTiles * kWaves * 4 * T * 4;
+    return gemv_static_lds_bytes(LR) + gemv_a_lds_bytes(gemv_nq(K) * kAImageBytes * 2 * T) + gemv_s_lds_bytes(nbv, T) +
+           kWaves * slots * T * 16 * 4;
 }
 
 static int device_cus() {
@@ -382,31 +452,38 @@ static int device_cus() {
 }
 
 template <int T, int LR>
-static hipError_t launch_gemv_cfg(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, hipStream_t s,
-                                  const XprepLayout& L) {
-    constexpr int CH = 8;
+static hipError_t launch_gemv_cfg(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int tpw,
+                                  hipStream_t s, const XprepLayout& L) {
     static bool attr_done = false;
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, CH>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           kLdsMax - gemv_static_lds_bytes(LR));
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    const int tiles = (N + 3) / 4;
-    const int tpw = (tiles + device_cus() - 1) / device_cus();   // one workgroup per CU
+    const int tiles = (N + 3) / 4, nq = gemv_nq(K);
     const int grid = (tiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, CH>), dim3(grid), dim3(1024), gemv_lds_bytes(K, T, LR), s, W, xprep, y,
-                       K, N, gemv_nq(K), tpw, L.off_sq, L.off_a);
+    const int slots = gemv_slots(nq, tpw);
+    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing>), dim3(grid), dim3(1024), gemv_lds_bytes(K, T, LR, slots) - gemv_static_lds_bytes(LR), s, W,
+                       xprep, y, K, N, nq, tpw, slots, L.off_a);
     return hipGetLastError();
 }
 
-// Table size: 64 replicas (one v_perm per lookup) when the activation leaves room, else 16.
+// One workgroup per CU when its tile sums fit in LDS beside the table and activation, else
+// smaller tile ranges (more workgroups).  Table: 64 replicas (one v_perm per lookup) when
+// there is room, else 16.
 template <int T>
 static hipError_t launch_gemv_t(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, hipStream_t s,
                                 const XprepLayout& L) {
-    if (gemv_lds_bytes(K, T, 6) <= kLdsMax) return launch_gemv_cfg<T, 6>(W, xprep, y, K, N, s, L);
-    if (gemv_lds_bytes(K, T, 4) <= kLdsMax) return launch_gemv_cfg<T, 4>(W, xprep, y, K, N, s, L);
-    return hipErrorInvalidValue;
+    const int tiles = (N + 3) / 4, nq = gemv_nq(K), cus = device_cus();
+    for (int wgs = cus;; wgs *= 2) {
+        const int tpw = (tiles + wgs - 1) / wgs;
+        const int slots = gemv_slots(nq, tpw);
+        if (gemv_lds_bytes(K, T, 6, slots) <= kLdsMax) return launch_gemv_cfg<T, 6>(W, xprep, y, K, N, tpw, s, L);
+        if (gemv_lds_bytes(K, T, 4, slots) <= kLdsMax) return launch_gemv_cfg<T, 4>(W, xprep, y, K, N, tpw, s, L);
+        if (tpw == 1) return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv_ptq1(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int T,
@@ -417,7 +494,7 @@ hipError_t launch_gemv_ptq1(const uint8_t* W, const uint8_t* xprep, float* y, in
 
 int gemv_max_k(int T) {
     int K = kGroup;
-    while (gemv_lds_bytes(K + kGroup, T, 4) <= kLdsMax) K += kGroup;
+    while (gemv_lds_bytes(K + kGroup, T, 4, gemv_slots(gemv_nq(K + kGroup), 1)) <= kLdsMax) K += kGroup;
     return K;
 }
 

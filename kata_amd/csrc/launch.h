@@ -9,7 +9,7 @@ namespace kata {
 
 // ---- PTQ1_0 GEMV (gemv_ptq1.hip)
 struct XprepLayout {
-    size_t off_sx, off_sq, off_a, bytes;
+    size_t off_s, off_a, bytes;   // (scale, sum) pairs, A image, total
 };
 XprepLayout xprep_layout(int K, int T);
 hipError_t launch_gemv_prep(const void* x, int x_dtype, int x_layout, uint8_t* xprep, int K, int T,

@@ -53,10 +53,12 @@ FAKE = ctypes.c_void_p(0x10000)   # never dereferenced: validation fails first
     (128, 8, 1, 5, 0),     # bad dtype
     (128, 8, 1, 1, 1),     # half2 needs T = 2
     (128, 8, 2, 0, 1),     # half2 needs fp16
-    (45184, 8, 1, 0, 0),   # K beyond the LDS-resident activation limit (T=1)
-    (21120, 8, 2, 1, 0),   # same for T=2
+    (-1, 8, 1, 0, 0),      # K one group beyond the LDS-resident activation limit (T=1)
+    (-2, 8, 2, 1, 0),      # same for T=2
 ])
 def test_gemv_rejects_bad_arguments(K, N, T, dt, layout):
+    if K < 0:
+        K = L.lib().kata_gemv_ptq1_max_k(-K) + 128
     rc = L.lib().kata_gemv_ptq1(FAKE, FAKE, dt, layout, FAKE, K, N, T, None)
     assert rc == KATA_EINVAL
     assert L.lib().kata_last_error()
@@ -73,7 +75,9 @@ def test_other_entry_points_reject_bad_shapes():
     assert lib.kata_gemm_ptq1_i8(FAKE, FAKE, 4, FAKE, FAKE, 0, 4, 4, 128, 8, None) == KATA_EINVAL  # ldc < N
     assert lib.kata_gemv_ptq1_prep(FAKE, 0, 0, ctypes.c_void_p(0x10004), 128, 1, None) == KATA_EINVAL  # xprep align
     assert lib.kata_gemv_ptq1_xprep_bytes(100, 1) == 0
-    assert lib.kata_gemv_ptq1_max_k(1) == 45056 and lib.kata_gemv_ptq1_max_k(2) == 20992
+    # the 27B shapes (K up to 17408) must fit for both T
+    assert lib.kata_gemv_ptq1_max_k(1) >= 17408 and lib.kata_gemv_ptq1_max_k(2) >= 17408
+    assert lib.kata_gemv_ptq1_max_k(1) % 128 == 0 and lib.kata_gemv_ptq1_max_k(2) % 128 == 0
     assert lib.kata_gemv_ptq1_max_k(3) == 0
     assert lib.kata_gemv_ptq1_xprep_bytes(5120, 1) >= 5120 // 128 * (384 + 8)   # A image + scales/sums
 
