@@ -83,7 +83,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=2048)
-    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
+    ap.add_argument("--graph", action="store_true", help="replay per-step HIP graphs instead of eager launches")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -126,7 +126,7 @@ def main():
 
     # One HIP graph per (function, weight copy): replaying graph i % ncopies is step i, so
     # exactly K steps are timed, each with the per-launch overhead of a graph launch.
-    use_graph = not args.no_graph
+    use_graph = args.graph
     cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
     runners = {}
     for fname, fn in (("step", step), ("gemv", gemvs_only)):

@@ -18,6 +18,10 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkata_amd.so")
 SOURCES = ["gemv_ptq1.hip", "gemv_q8.hip", "gemm_f16.hip", "gemm_i8.hip", "expand.hip", "capi.cpp"]
+# Per-source extra flags.  The prefill GEMM keeps 144 fp32 accumulators per lane beside its
+# decode code; LLVM's iterative-ILP scheduler keeps them in place (the default one shuttles
+# them between register files every stage).
+EXTRA_FLAGS = {"gemm_f16.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
@@ -28,7 +32,7 @@ FLAGS = [
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, "-x", "hip", *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, "-x", "hip", *FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

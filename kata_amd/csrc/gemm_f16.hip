@@ -2,121 +2,288 @@
 //
 // Semantics (shaders/prefill.metal:31-41 after k_expand_ptq1_v2, :472-479):
 //   C[m][n] = sum_k A[m][k] * half(trit[n][k] * d[n][k/128]),  fp16 x fp16 -> fp32.
-// half(trit*d) is exact, so the product terms equal the reference's; only the fp32
+// half(trit*d) is exact, so every product term equals the reference's; only the fp32
 // summation order differs (tolerance-based parity).
 //
-// Design: no fp16 weight stage ever touches HBM (the reference writes 178 MB per matrix).
-// A 256-thread workgroup computes a 128x128 tile of C with K-steps of one PTQ1_0 block
-// (128).  Per step it copies the 128x128 fp16 A tile to LDS and decodes the 128-row x
-// 28-byte packed W tile straight into an fp16 [n][k] LDS tile: a thread takes two
-// neighbouring bytes of a row and emits, for each of their 4-5 base-3 digits, the two
-// adjacent-k weights as one 32-bit LDS store (element pairs 16n+m, 80+8n+m, 120+2n+h
-// are adjacent for even m, h).  Four waves (2x2) each run 4x4 v_mfma_f32_16x16x32_f16
-// tiles over the step.
+// Design (MI355X-first; the reference expands every matrix to a 178 MB fp16 stage first):
+//  * A workgroup (4 waves) computes a 128 x 16U tile of C, U = 1..18 column units of 16
+//    chosen per problem so the grid is close to a multiple of the CU count (pp512 gate/up:
+//    128 x 272 -> exactly 256 tiles).  Wave (wm, wn) owns rows 64wm..64wm+63 and about
+//    half of the units; each 16x16 output tile is accumulated by v_mfma_f32_16x16x32_f16.
+//  * K advances in stages of 64 (half a PTQ1_0 block) through a two-stage LDS pipeline:
+//    while the matrix cores consume stage s, the workgroup stores stage s+1's A tile (from
+//    registers loaded a stage earlier) and decodes stage s+1's weights straight from the
+//    packed bytes into fp16, and the loads for stage s+2 are in flight.  No fp16 weight
+//    copy ever touches HBM.
+//  * Decode: a group is 4 consecutive k of one row from the 4 bytes of one packed dword
+//    and one base-3 digit.  The bytes go to 16-bit lanes (b0,b2) and (b1,b3); the digit is
+//    ((b * 3^n) mod 256) * 3 >> 8 with packed 16-bit multiplies, and v_perm_b32 picks the
+//    fp16 value -d, 0 or +d for it from one register pair.  Within each group of 4 k the
+//    LDS tiles hold the order (k0, k2, k1, k3) - the same permutation for A and for the
+//    weights, so the dot products are unchanged - which lets each 16-bit-lane pair be
+//    stored as it is.  Wave i of the workgroup decodes the same 4 groups of every row.
+//  * LDS rows are 64 halves (128 B) of 8 chunks of 16 B; chunk c of row r is stored at
+//    c ^ (r & 7), so the MFMA operand reads (16 rows x one chunk) are conflict-free.
 #include "common.h"
 #include "launch.h"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace kata {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDA_S = BK + 8;   // halves; row stride 272 B
+constexpr int BM = 128;          // rows of A / C per workgroup
+constexpr int BKS = 64;          // k per stage (halves)
+constexpr int kMaxUnits = 18;    // 16-column units per workgroup
+constexpr int kMaxWaveUnits = 9;
+constexpr int ROWB = BKS * 2;    // LDS bytes per tile row
 
-template <bool C_F16>
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ inline uint32_t swz(int row, int chunk) { return (uint32_t)(row * ROWB + ((chunk ^ (row & 7)) << 4)); }
+
+// (h0..h7) -> (h0,h2,h1,h3, h4,h6,h5,h7): the within-4 k order of the LDS tiles
+__device__ inline uint4 permute_k4(uint4 v) {
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+    return o;
+}
+
+// fp16 of (digit_n(b) - 1) * d for bytes in 16-bit lanes (b_lo, b_hi); lo = (-d, 0),
+// hi = (+d, +d) as fp16 bit pairs.  Returns the two halves as one dword.
+__device__ inline uint32_t decode_pair(u16x2 b, uint32_t p3n, uint32_t lo, uint32_t hi) {
+    u16x2 m = b * __builtin_bit_cast(u16x2, p3n);
+    m &= (u16x2){0xff, 0xff};
+    const u16x2 dg = (m * (u16x2){3, 3}) >> (u16x2){8, 8};
+    const u16x2 sel = dg * (u16x2){0x0202, 0x0202} + (u16x2){0x0100, 0x0100};
+    return __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, sel));
+}
+
+// group: bytes of w, digit n -> LDS (b0, b2, b1, b3) at k..k+3 of the row
+__device__ inline void decode_group(uint8_t* brow, int row, int k, uint32_t w, uint32_t p3n, uint32_t lo, uint32_t hi) {
+    const u16x2 e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
+    const u16x2 o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00ff00ffu);
+    uint2 v;
+    v.x = decode_pair(e, p3n, lo, hi);
+    v.y = decode_pair(o, p3n, lo, hi);
+    *(uint2*)(brow + swz(row, k >> 3) + (k & 7) * 2) = v;
+}
+
+__host__ __device__ constexpr uint32_t p3x2(int n) {
+    return n == 0 ? 0x00010001u : n == 1 ? 0x00030003u : n == 2 ? 0x00090009u : n == 3 ? 0x001b001bu : 0x00510051u;
+}
+
+// Decode groups (e = element of the block, dword j = bytes 4j..4j+3, k = stage-relative
+// position = e - 64h).  A row has 16 groups per stage:
+//   h=0: dword i, digit n at e = 16n + 4i                         (i, n = 0..3)
+//   h=1: dword i digit 4 at e = 64 + 4i; dword 4+i digit n at e = 80 + 4i + 8n (n = 0..4);
+//        qh at e = 120..123 and 124..127
+// For the extra rows (256..) each wave takes 4 of a row's 16 groups:
+//   h=0: dword `wave`, digits 0..3
+//   h=1: wave 0: dw0 d4 @64, dw4 d0 @80, dw4 d1 @88, dw4 d2 @96
+//        wave 1: dw1 d4 @68, dw4 d3 @104, dw4 d4 @112, dw5 d0 @84
+//        wave 2: dw2 d4 @72, dw5 d1 @92, dw5 d2 @100, dw5 d3 @108
+//        wave 3: dw3 d4 @76, dw5 d4 @116, qh @120..123, qh @124..127
+constexpr int BROWS = 16 * kMaxUnits;              // weight-tile rows in LDS
+constexpr int kLdsBytes = 2 * BM * ROWB + 2 * BROWS * ROWB;
+
+template <bool C_F16, int NWU>
 __global__ __launch_bounds__(256) void k_gemm_ptq1_f16(const _Float16* __restrict__ A, int lda,
                                                        const uint8_t* __restrict__ W, void* __restrict__ C,
-                                                       int ldc, int M, int K, int N) {
-    __shared__ _Float16 As[BM * LDA_S];
-    __shared__ _Float16 Bs[BN * LDA_S];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                                       int ldc, int M, int K, int N, int G) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    auto As = [&](int buf) { return smem + buf * (BM * ROWB); };
+    auto Bs = [&](int buf) { return smem + 2 * BM * ROWB + buf * (BROWS * ROWB); };
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int nb = K / kGroup;
     const int l16 = lane & 15, lg = lane >> 4;
+    const int nb = K >> 7;
+    const int m0 = blockIdx.y * BM;
+    // column units of this workgroup and of this wave
+    const int U = (N + 15) >> 4;
+    const int u0 = (int)(((long)blockIdx.x * U) / G), u1 = (int)(((long)(blockIdx.x + 1) * U) / G);
+    const int nu = u1 - u0, n0 = u0 * 16, R = nu * 16;
+    const int wu0 = wn ? (nu + 1) >> 1 : 0;
+    const int nwu = wn ? nu >> 1 : (nu + 1) >> 1;
+    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
 
-    v4f acc[4][4];
+    // ---- A stage loads: thread -> row tid/2, chunks 4*(tid&1) .. +3
+    const int arow = tid >> 1, achunk = (tid & 1) * 4;
+    const _Float16* a_src = A + (size_t)min(m0 + arow, M - 1) * lda + achunk * 8;
+    uint4 areg[4];
+    auto load_a = [&](int s) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) areg[c] = *(const uint4*)(a_src + (size_t)s * BKS + c * 8);
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) *(uint4*)(As(buf) + swz(arow, achunk + c)) = permute_k4(areg[c]);
+    };
+
+    // ---- weight bytes: raw buffer loads, 32-bit row offsets, block offset in soffset.
+    // Rows 0..255 of the tile: lane `lane` of wave w owns row 64w + lane and loads its whole
+    // 28-byte block (one x4 and one x3 load, so a load instruction touches one line per
+    // row) and decodes all 16 groups of the row per stage.  Rows 256.. (R <= 288): each
+    // wave decodes 4 of the 16 groups of row 256 + lane (schedule in the table above).
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
+    const int rowM = 64 * wave + lane, rowX = 256 + lane;
+    const uint32_t offM = (uint32_t)min(n0 + min(rowM, R - 1), N - 1) * row_bytes;
+    const uint32_t offX = (uint32_t)min(n0 + min(rowX, R - 1), N - 1) * row_bytes;
+    const bool has_x = R > 256;                  // workgroup-uniform
+    uint32_t wm_cur[7], wm_nxt[7];               // main row: block being decoded / next
+    uint32_t x_cur[4], x_nxt[4];                 // extra row: dword `wave`, dwb, dword 5, dword 6
+    const int dwb = wave < 2 ? 4 : 5;
+    auto load_blk = [&](uint32_t* wm7, uint32_t* x4, int blk) {
+        const int so = blk * kBlockBytes;
+        const uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)offM, so, 0));
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 v1 = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(wrsrc, (int)offM + 16, so, 0));
+        wm7[0] = v0.x; wm7[1] = v0.y; wm7[2] = v0.z; wm7[3] = v0.w;
+        wm7[4] = v1.x; wm7[5] = v1.y; wm7[6] = v1.z;
+        x4[0] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * wave), so, 0);
+        x4[1] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * dwb), so, 0);
+        x4[2] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 20), so, 0);
+        x4[3] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 24), so, 0);
+    };
+    // Per-wave schedule of the extra row at h=1 as scalars (no branches, so the LDS wait
+    // counts stay exact): k (stage-relative) and multiplier pair of groups q = 1..3; group
+    // 0 is digit 4 of dword `wave` at k = 4 * wave.  Source: dwb, except wave 1 q3
+    // (dword 5) and wave 3 q2/q3 (the qh bytes as (qh0, qh1, qh0, qh1), digits a, a+1).
+    const uint32_t k1 = (0x341c2810u >> (8 * wave)) & 0xffu;     // 16, 40, 28, 52
+    const uint32_t k2 = (0x38243018u >> (8 * wave)) & 0xffu;     // 24, 48, 36, 56
+    const uint32_t k3 = (0x3c2c1420u >> (8 * wave)) & 0xffu;     // 32, 20, 44, 60
+    const uint32_t m1 = wave == 0 ? p3x2(0) : wave == 1 ? p3x2(3) : wave == 2 ? p3x2(1) : p3x2(4);
+    const uint32_t m2 = wave == 0 ? p3x2(1) : wave == 1 ? p3x2(4) : wave == 2 ? p3x2(2) : 0x00030001u;
+    const uint32_t m3 = wave == 0 ? p3x2(2) : wave == 1 ? p3x2(0) : wave == 2 ? p3x2(3) : 0x001b0009u;
+    // Decode group g (0..19) of stage h of the current block into buffer buf: g < 16 are
+    // the main row's groups, 16..19 the extra row's.
+    auto decode_one = [&](auto h_c, int buf, int g) {
+        constexpr int h = decltype(h_c)::value;
+        uint8_t* bt = Bs(buf);
+        if (g < 16) {
+            const uint32_t dbits = wm_cur[6] >> 16;
+            const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
+            if (h == 0) {
+                const int i = g & 3, n = g >> 2;
+                decode_group(bt, rowM, 16 * n + 4 * i, wm_cur[i], p3x2(n), lo, hi);
+            } else if (g < 4) {
+                decode_group(bt, rowM, 4 * g, wm_cur[g], p3x2(4), lo, hi);
+            } else if (g < 14) {
+                const int i = (g - 4) & 1, n = (g - 4) >> 1;      // dword 4 + i, digit n
+                decode_group(bt, rowM, 16 + 4 * i + 8 * n, wm_cur[4 + i], p3x2(n), lo, hi);
+            } else {
+                const uint32_t qh = __builtin_amdgcn_perm(0u, wm_cur[6], 0x01000100u);
+                decode_group(bt, rowM, g == 14 ? 56 : 60, qh, g == 14 ? 0x00030001u : 0x001b0009u, lo, hi);
+            }
+            return;
+        }
+        if (!has_x) return;
+        const int q = g - 16;
+        const uint32_t dbits = x_cur[3] >> 16;
+        const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
+        if (h == 0) {
+            decode_group(bt, rowX, 16 * q + 4 * wave, x_cur[0], p3x2(q), lo, hi);
+        } else if (q == 0) {
+            decode_group(bt, rowX, 4 * wave, x_cur[0], p3x2(4), lo, hi);
+        } else {
+            const uint32_t qh = __builtin_amdgcn_perm(0u, x_cur[3], 0x01000100u);
+            const uint32_t w = q == 1 ? x_cur[1] : (wave == 3 ? qh : (q == 3 && wave == 1 ? x_cur[2] : x_cur[1]));
+            decode_group(bt, rowX, (int)(q == 1 ? k1 : q == 2 ? k2 : k3), w, q == 1 ? m1 : q == 2 ? m2 : m3, lo, hi);
+        }
+    };
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    v4f acc[4][NWU];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int jx = 0; jx < 4; jx++) acc[i][jx] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NWU; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = 0; kb < nb; ++kb) {
-        __syncthreads();
-        // ---- A tile: 128 rows x 128 halves; thread -> (row tid/2, 64 halves)
-        {
-            const int r = tid >> 1, h = tid & 1;
-            const int gm = m0 + r;
-            uint4* dst = (uint4*)(As + r * LDA_S + h * 64);
-            if (gm < M) {
-                const uint4* src = (const uint4*)(A + (size_t)gm * lda + (size_t)kb * BK + h * 64);
+    // One stage: MFMAs over LDS buffer cbuf, with the decode of the next stage (h, par)
+    // into buffer dbuf interleaved (20 groups spread over the 2 * NWU MFMA units).
+    auto stage = [&](int cbuf, bool do_decode, auto h_c, int dbuf) {
+        const uint8_t* at = As(cbuf);
+        const uint8_t* bt = Bs(cbuf);
+        constexpr int NG = 20, NS = 2 * NWU;
 #pragma unroll
-                for (int c = 0; c < 8; c++) dst[c] = src[c];
-            } else {
+        for (int kk = 0; kk < BKS / 32; kk++) {
+            // all operands of the k-step are read up front (LDS latency exceeds the MFMA
+            // time of one unit)
+            v8h af[4], bfs[NWU];
 #pragma unroll
-                for (int c = 0; c < 8; c++) dst[c] = make_uint4(0, 0, 0, 0);
-            }
-        }
-        // ---- W tile: 128 rows x 13 byte pairs -> fp16 [n][k]
-        for (int idx = tid; idx < BN * 13; idx += 256) {
-            const int r = idx / 13, pr = idx - r * 13;
-            const int gn = n0 + r;
-            const int p = 2 * pr;
-            uint32_t* brow = (uint32_t*)(Bs + r * LDA_S);
-            if (gn < N) {
-                const uint8_t* blk = W + ((size_t)gn * nb + kb) * kBlockBytes;
-                const uint32_t bb = *(const uint16_t*)(blk + p);
-                const float d = half_bits_to_float(*(const uint16_t*)(blk + 26));
-                const uint32_t b0 = bb & 0xffu, b1 = bb >> 8;
-                const int nd = p < 24 ? 5 : 4;
+            for (int i = 0; i < 4; i++) af[i] = *(const v8h*)(at + swz(wm * 64 + i * 16 + l16, kk * 4 + lg));
 #pragma unroll
-                for (int n = 0; n < 5; n++) {
-                    if (n < nd) {
-                        const float t0 = (float)((int)ptq1_digit(b0, n) - 1) * d;
-                        const float t1 = (float)((int)ptq1_digit(b1, n) - 1) * d;
-                        const int e = ptq1_slot_elem(p, n);
-                        v2h hv = {(_Float16)t0, (_Float16)t1};
-                        brow[e >> 1] = *(uint32_t*)&hv;
-                    }
-                }
-            } else {
+            for (int j = 0; j < NWU; j++) bfs[j] = *(const v8h*)(bt + swz((wu0 + j) * 16 + l16, kk * 4 + lg));
 #pragma unroll
-                for (int n = 0; n < 5; n++) {
-                    const int e = ptq1_slot_elem(p, n);
-                    if (e >= 0) brow[e >> 1] = 0u;
+            for (int j = 0; j < NWU; j++) {
+                const v8h bf = bfs[j];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[i][j], 0, 0, 0);
+                if (do_decode) {
+                    const int sl = kk * NWU + j;
+#pragma unroll
+                    for (int g = sl * NG / NS; g < (sl + 1) * NG / NS; g++) decode_one(h_c, dbuf, g);
                 }
             }
         }
+    };
+
+    // ---- prologue: stage 0 in LDS, stage 1's A and block 0's bytes in registers
+    load_blk(wm_cur, x_cur, 0);
+    load_a(0);
+    store_a(0);
+#pragma unroll
+    for (int g = 0; g < 20; g++) decode_one(I0(), 0, g);
+    load_a(1);
+    __syncthreads();
+
+    // ---- main loop: one PTQ1_0 block (two stages) per iteration; the next block's bytes
+    // are loaded during the first stage and become current at the end of the iteration.
+    // Loads are issued unconditionally (the last block rereads itself) so that no branch
+    // hides them from the compiler's wait counting.
+    for (int b = 0; b < nb; b++) {
+        const bool more = b + 1 < nb;
+        const int bn = more ? b + 1 : b;
+        // stage 2b (h=0) in buffer 0; produce stage 2b+1 (h=1 of block b) into buffer 1
+        store_a(1);
+        load_blk(wm_nxt, x_nxt, bn);
+        load_a(2 * bn);
+        stage(0, true, I1(), 1);
         __syncthreads();
-        // ---- 4 k-substeps of 32
 #pragma unroll
-        for (int kk = 0; kk < BK / 32; kk++) {
-            v8h af[4], bf[4];
+        for (int i = 0; i < 7; i++) wm_cur[i] = wm_nxt[i];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                af[i] = *(const v8h*)(As + (wm * 64 + i * 16 + l16) * LDA_S + kk * 32 + lg * 8);
-#pragma unroll
-            for (int jx = 0; jx < 4; jx++)
-                bf[jx] = *(const v8h*)(Bs + (wn * 64 + jx * 16 + l16) * LDA_S + kk * 32 + lg * 8);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int jx = 0; jx < 4; jx++)
-                    acc[i][jx] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jx], acc[i][jx], 0, 0, 0);
-        }
+        for (int i = 0; i < 4; i++) x_cur[i] = x_nxt[i];
+        // stage 2b+1 in buffer 1; produce stage 2b+2 (h=0 of block b+1) into buffer 0
+        store_a(0);
+        load_a(2 * bn + 1);
+        stage(1, more, I0(), 0);
+        __syncthreads();
     }
+
     // ---- store: lane holds D[4*lg + r][l16] of each 16x16 tile
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int jx = 0; jx < 4; jx++) {
-            const int gn = n0 + wn * 64 + jx * 16 + l16;
+        for (int j = 0; j < NWU; j++) {
+            if (j < nwu) {
+                const int gn = n0 + (wu0 + j) * 16 + l16;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
-                if (gm < M && gn < N) {
-                    if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][jx][r];
-                    else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][jx][r];
+                for (int r = 0; r < 4; r++) {
+                    const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
+                    if (gm < M && gn < N) {
+                        if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][r];
+                        else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][r];
+                    }
                 }
             }
         }
@@ -124,14 +291,50 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_f16(const _Float16* __restric
 
 }  // namespace
 
+// Column groups: about (CUs / row tiles) groups of at most kMaxUnits units; the wave
+// unit count selects the kernel instance.
+template <int NWU>
+static hipError_t launch_nwu(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M,
+                             int K, int N, int G, dim3 grid, hipStream_t s) {
+    static bool attr_done = false;
+    if (!attr_done) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true, NWU>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false, NWU>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    if (c_dtype == 1)
+        hipLaunchKernelGGL((k_gemm_ptq1_f16<true, NWU>), grid, dim3(256), kLdsBytes, s, (const _Float16*)A, lda, W, C,
+                           ldc, M, K, N, G);
+    else
+        hipLaunchKernelGGL((k_gemm_ptq1_f16<false, NWU>), grid, dim3(256), kLdsBytes, s, (const _Float16*)A, lda, W,
+                           C, ldc, M, K, N, G);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
                            int M, int K, int N, hipStream_t s) {
-    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM), block(256);
-    if (c_dtype == 1)
-        hipLaunchKernelGGL(k_gemm_ptq1_f16<true>, grid, block, 0, s, (const _Float16*)A, lda, W, C, ldc, M, K, N);
-    else
-        hipLaunchKernelGGL(k_gemm_ptq1_f16<false>, grid, block, 0, s, (const _Float16*)A, lda, W, C, ldc, M, K, N);
-    return hipGetLastError();
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const int mt = (M + BM - 1) / BM;
+    const int U = (N + 15) / 16;
+    int G = std::max(1, n_cu / mt);
+    G = std::max(G, (U + kMaxUnits - 1) / kMaxUnits);
+    G = std::min(G, U);
+    const int umax = (U + G - 1) / G;                   // units of the widest workgroup
+    const int wmax = (umax + 1) / 2;                    // of its wider wave
+    const dim3 grid(G, mt);
+    if (wmax <= 3) return launch_nwu<3>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    if (wmax <= 5) return launch_nwu<5>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    return launch_nwu<kMaxWaveUnits>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
 }
 
 }  // namespace kata
