@@ -92,8 +92,13 @@ __host__ __device__ constexpr uint32_t p3x2(int n) {
 constexpr int BROWS = 16 * kMaxUnits;              // weight-tile rows in LDS
 constexpr int kLdsBytes = 2 * BM * ROWB + 2 * BROWS * ROWB;
 
+// Workgroup = 8 waves, two per SIMD: waves 0..3 are consumers (MFMAs over the LDS stage;
+// wave (wm, wn) owns rows 64wm.. and about half of the column units), waves 4..7 are
+// producers (A tile stores, weight decode and all global loads for the next stages).  The
+// SIMD interleaves a consumer's MFMAs with a producer's decode VALU work.  One barrier per
+// stage, preceded by an LDS-only wait: the producers' global prefetches stay in flight.
 template <bool C_F16, int NWU>
-__global__ __launch_bounds__(256) void k_gemm_ptq1_f16(const _Float16* __restrict__ A, int lda,
+__global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restrict__ A, int lda,
                                                        const uint8_t* __restrict__ W, void* __restrict__ C,
                                                        int ldc, int M, int K, int N, int G) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -101,192 +106,203 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_f16(const _Float16* __restric
     auto Bs = [&](int buf) { return smem + 2 * BM * ROWB + buf * (BROWS * ROWB); };
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int l16 = lane & 15, lg = lane >> 4;
+    const bool consumer = wave < 4;
     const int nb = K >> 7;
     const int m0 = blockIdx.y * BM;
-    // column units of this workgroup and of this wave
+    // column units of this workgroup
     const int U = (N + 15) >> 4;
     const int u0 = (int)(((long)blockIdx.x * U) / G), u1 = (int)(((long)(blockIdx.x + 1) * U) / G);
     const int nu = u1 - u0, n0 = u0 * 16, R = nu * 16;
-    const int wu0 = wn ? (nu + 1) >> 1 : 0;
-    const int nwu = wn ? nu >> 1 : (nu + 1) >> 1;
-    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
-
-    // ---- A stage loads: thread -> row tid/2, chunks 4*(tid&1) .. +3
-    const int arow = tid >> 1, achunk = (tid & 1) * 4;
-    const _Float16* a_src = A + (size_t)min(m0 + arow, M - 1) * lda + achunk * 8;
-    uint4 areg[4];
-    auto load_a = [&](int s) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) areg[c] = *(const uint4*)(a_src + (size_t)s * BKS + c * 8);
+    auto barrier = [&]() {
+        __builtin_amdgcn_s_waitcnt((15 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
     };
-    auto store_a = [&](int buf) {
+
+    if (consumer) {
+        const int wm = wave >> 1, wn = wave & 1;
+        const int l16 = lane & 15, lg = lane >> 4;
+        const int wu0 = wn ? (nu + 1) >> 1 : 0;
+        const int nwu = wn ? nu >> 1 : (nu + 1) >> 1;
+        v4f acc[4][NWU];
 #pragma unroll
-        for (int c = 0; c < 4; c++) *(uint4*)(As(buf) + swz(arow, achunk + c)) = permute_k4(areg[c]);
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < NWU; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        // all NWU units (a wave with fewer computes columns it never stores; the LDS tile
+        // has BROWS rows)
+        auto compute = [&](int buf) {
+            const uint8_t* at = As(buf);
+            const uint8_t* bt = Bs(buf);
+#pragma unroll
+            for (int kk = 0; kk < BKS / 32; kk++) {
+                v8h af[4], bfs[NWU];
+#pragma unroll
+                for (int i = 0; i < 4; i++) af[i] = *(const v8h*)(at + swz(wm * 64 + i * 16 + l16, kk * 4 + lg));
+#pragma unroll
+                for (int j = 0; j < NWU; j++) bfs[j] = *(const v8h*)(bt + swz((wu0 + j) * 16 + l16, kk * 4 + lg));
+#pragma unroll
+                for (int j = 0; j < NWU; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfs[j], acc[i][j], 0, 0, 0);
+            }
+        };
+        barrier();                                       // stage 0 produced
+        for (int b = 0; b < nb; b++) {
+            compute(0);
+            barrier();
+            compute(1);
+            barrier();
+        }
+        // ---- store: lane holds D[4*lg + r][l16] of each 16x16 tile
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < NWU; j++) {
+                if (j < nwu) {
+                    const int gn = n0 + (wu0 + j) * 16 + l16;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
+                        if (gm < M && gn < N) {
+                            if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][r];
+                            else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][r];
+                        }
+                    }
+                }
+            }
+        return;
+    }
+
+    // ================= producers =================
+    const int pw = wave - 4, ptid = tid - 256;
+    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
+    // ---- A: thread -> row ptid/2, chunks 4*(ptid&1) .. +3; stage t's A is loaded into
+    // register set t & 1 two stages before it is stored (index clamped to the last stage)
+    const int arow = ptid >> 1, achunk = (ptid & 1) * 4;
+    const _Float16* a_src = A + (size_t)min(m0 + arow, M - 1) * lda + achunk * 8;
+    uint4 areg[2][4];
+    const int last_stage = 2 * nb - 1;
+    auto load_a = [&](auto set_c, int st) {
+        constexpr int set = decltype(set_c)::value;
+        const int s2 = min(st, last_stage);
+#pragma unroll
+        for (int c = 0; c < 4; c++) areg[set][c] = *(const uint4*)(a_src + (size_t)s2 * BKS + c * 8);
+    };
+    auto store_a = [&](auto set_c, int buf) {
+        constexpr int set = decltype(set_c)::value;
+#pragma unroll
+        for (int c = 0; c < 4; c++) *(uint4*)(As(buf) + swz(arow, achunk + c)) = permute_k4(areg[set][c]);
     };
 
     // ---- weight bytes: raw buffer loads, 32-bit row offsets, block offset in soffset.
-    // Rows 0..255 of the tile: lane `lane` of wave w owns row 64w + lane and loads its whole
-    // 28-byte block (one x4 and one x3 load, so a load instruction touches one line per
-    // row) and decodes all 16 groups of the row per stage.  Rows 256.. (R <= 288): each
-    // wave decodes 4 of the 16 groups of row 256 + lane (schedule in the table above).
+    // Rows 0..255 of the tile: lane `lane` of producer pw owns row 64pw + lane and loads its
+    // whole 28-byte block (one x4 and one x3 load, so a load instruction touches one line
+    // per row) and decodes all 16 groups of the row per stage.  Rows 256.. (R <= 288): each
+    // producer decodes 4 of the 16 groups of row 256 + lane (schedule in the table above).
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
-    const int rowM = 64 * wave + lane, rowX = 256 + lane;
+    const int rowM = 64 * pw + lane, rowX = 256 + lane;
     const uint32_t offM = (uint32_t)min(n0 + min(rowM, R - 1), N - 1) * row_bytes;
     const uint32_t offX = (uint32_t)min(n0 + min(rowX, R - 1), N - 1) * row_bytes;
     const bool has_x = R > 256;                  // workgroup-uniform
     uint32_t wm_cur[7], wm_nxt[7];               // main row: block being decoded / next
-    uint32_t x_cur[4], x_nxt[4];                 // extra row: dword `wave`, dwb, dword 5, dword 6
-    const int dwb = wave < 2 ? 4 : 5;
+    uint32_t x_cur[4], x_nxt[4];                 // extra row: dword pw, dwb, dword 5, dword 6
+    const int dwb = pw < 2 ? 4 : 5;
     auto load_blk = [&](uint32_t* wm7, uint32_t* x4, int blk) {
-        const int so = blk * kBlockBytes;
+        const int so = min(blk, nb - 1) * kBlockBytes;
         const uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)offM, so, 0));
         typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
         const u32x3 v1 = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(wrsrc, (int)offM + 16, so, 0));
         wm7[0] = v0.x; wm7[1] = v0.y; wm7[2] = v0.z; wm7[3] = v0.w;
         wm7[4] = v1.x; wm7[5] = v1.y; wm7[6] = v1.z;
-        x4[0] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * wave), so, 0);
+        x4[0] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * pw), so, 0);
         x4[1] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * dwb), so, 0);
         x4[2] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 20), so, 0);
         x4[3] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 24), so, 0);
     };
-    // Per-wave schedule of the extra row at h=1 as scalars (no branches, so the LDS wait
-    // counts stay exact): k (stage-relative) and multiplier pair of groups q = 1..3; group
-    // 0 is digit 4 of dword `wave` at k = 4 * wave.  Source: dwb, except wave 1 q3
-    // (dword 5) and wave 3 q2/q3 (the qh bytes as (qh0, qh1, qh0, qh1), digits a, a+1).
-    const uint32_t k1 = (0x341c2810u >> (8 * wave)) & 0xffu;     // 16, 40, 28, 52
-    const uint32_t k2 = (0x38243018u >> (8 * wave)) & 0xffu;     // 24, 48, 36, 56
-    const uint32_t k3 = (0x3c2c1420u >> (8 * wave)) & 0xffu;     // 32, 20, 44, 60
-    const uint32_t m1 = wave == 0 ? p3x2(0) : wave == 1 ? p3x2(3) : wave == 2 ? p3x2(1) : p3x2(4);
-    const uint32_t m2 = wave == 0 ? p3x2(1) : wave == 1 ? p3x2(4) : wave == 2 ? p3x2(2) : 0x00030001u;
-    const uint32_t m3 = wave == 0 ? p3x2(2) : wave == 1 ? p3x2(0) : wave == 2 ? p3x2(3) : 0x001b0009u;
-    // Decode group g (0..19) of stage h of the current block into buffer buf: g < 16 are
-    // the main row's groups, 16..19 the extra row's.
-    auto decode_one = [&](auto h_c, int buf, int g) {
+    // Per-producer schedule of the extra row at h=1 as scalars: k (stage-relative) and
+    // multiplier pair of groups q = 1..3; group 0 is digit 4 of dword pw at k = 4 * pw.
+    // Source: dwb, except producer 1 q3 (dword 5) and producer 3 q2/q3 (the qh bytes as
+    // (qh0, qh1, qh0, qh1), digits a, a+1 per lane half).
+    const uint32_t k1 = (0x341c2810u >> (8 * pw)) & 0xffu;       // 16, 40, 28, 52
+    const uint32_t k2 = (0x38243018u >> (8 * pw)) & 0xffu;       // 24, 48, 36, 56
+    const uint32_t k3 = (0x3c2c1420u >> (8 * pw)) & 0xffu;       // 32, 20, 44, 60
+    const uint32_t m1 = pw == 0 ? p3x2(0) : pw == 1 ? p3x2(3) : pw == 2 ? p3x2(1) : p3x2(4);
+    const uint32_t m2 = pw == 0 ? p3x2(1) : pw == 1 ? p3x2(4) : pw == 2 ? p3x2(2) : 0x00030001u;
+    const uint32_t m3 = pw == 0 ? p3x2(2) : pw == 1 ? p3x2(0) : pw == 2 ? p3x2(3) : 0x001b0009u;
+    // stage h of the current block into buffer buf: the main row's 16 groups, then the
+    // extra row's 4
+    auto decode = [&](auto h_c, int buf) {
         constexpr int h = decltype(h_c)::value;
         uint8_t* bt = Bs(buf);
-        if (g < 16) {
+        {
             const uint32_t dbits = wm_cur[6] >> 16;
             const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
             if (h == 0) {
-                const int i = g & 3, n = g >> 2;
-                decode_group(bt, rowM, 16 * n + 4 * i, wm_cur[i], p3x2(n), lo, hi);
-            } else if (g < 4) {
-                decode_group(bt, rowM, 4 * g, wm_cur[g], p3x2(4), lo, hi);
-            } else if (g < 14) {
-                const int i = (g - 4) & 1, n = (g - 4) >> 1;      // dword 4 + i, digit n
-                decode_group(bt, rowM, 16 + 4 * i + 8 * n, wm_cur[4 + i], p3x2(n), lo, hi);
+#pragma unroll
+                for (int g = 0; g < 16; g++) {
+                    const int i = g & 3, n = g >> 2;
+                    decode_group(bt, rowM, 16 * n + 4 * i, wm_cur[i], p3x2(n), lo, hi);
+                }
             } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) decode_group(bt, rowM, 4 * i, wm_cur[i], p3x2(4), lo, hi);
+#pragma unroll
+                for (int g = 0; g < 10; g++) {
+                    const int i = g & 1, n = g >> 1;          // dword 4 + i, digit n
+                    decode_group(bt, rowM, 16 + 4 * i + 8 * n, wm_cur[4 + i], p3x2(n), lo, hi);
+                }
                 const uint32_t qh = __builtin_amdgcn_perm(0u, wm_cur[6], 0x01000100u);
-                decode_group(bt, rowM, g == 14 ? 56 : 60, qh, g == 14 ? 0x00030001u : 0x001b0009u, lo, hi);
+                decode_group(bt, rowM, 56, qh, 0x00030001u, lo, hi);
+                decode_group(bt, rowM, 60, qh, 0x001b0009u, lo, hi);
             }
-            return;
         }
-        if (!has_x) return;
-        const int q = g - 16;
-        const uint32_t dbits = x_cur[3] >> 16;
-        const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
-        if (h == 0) {
-            decode_group(bt, rowX, 16 * q + 4 * wave, x_cur[0], p3x2(q), lo, hi);
-        } else if (q == 0) {
-            decode_group(bt, rowX, 4 * wave, x_cur[0], p3x2(4), lo, hi);
-        } else {
-            const uint32_t qh = __builtin_amdgcn_perm(0u, x_cur[3], 0x01000100u);
-            const uint32_t w = q == 1 ? x_cur[1] : (wave == 3 ? qh : (q == 3 && wave == 1 ? x_cur[2] : x_cur[1]));
-            decode_group(bt, rowX, (int)(q == 1 ? k1 : q == 2 ? k2 : k3), w, q == 1 ? m1 : q == 2 ? m2 : m3, lo, hi);
+        if (has_x) {
+            const uint32_t dbits = x_cur[3] >> 16;
+            const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
+            if (h == 0) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) decode_group(bt, rowX, 16 * q + 4 * pw, x_cur[0], p3x2(q), lo, hi);
+            } else {
+                decode_group(bt, rowX, 4 * pw, x_cur[0], p3x2(4), lo, hi);
+                const uint32_t qh = __builtin_amdgcn_perm(0u, x_cur[3], 0x01000100u);
+                const uint32_t w23 = pw == 3 ? qh : x_cur[1];
+                decode_group(bt, rowX, (int)k1, x_cur[1], m1, lo, hi);
+                decode_group(bt, rowX, (int)k2, w23, m2, lo, hi);
+                decode_group(bt, rowX, (int)k3, pw == 1 ? x_cur[2] : w23, m3, lo, hi);
+            }
         }
     };
-
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    v4f acc[4][NWU];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < NWU; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    // One stage: MFMAs over LDS buffer cbuf, with the decode of the next stage (h, par)
-    // into buffer dbuf interleaved (20 groups spread over the 2 * NWU MFMA units).
-    auto stage = [&](int cbuf, bool do_decode, auto h_c, int dbuf) {
-        const uint8_t* at = As(cbuf);
-        const uint8_t* bt = Bs(cbuf);
-        constexpr int NG = 20, NS = 2 * NWU;
-#pragma unroll
-        for (int kk = 0; kk < BKS / 32; kk++) {
-            // all operands of the k-step are read up front (LDS latency exceeds the MFMA
-            // time of one unit)
-            v8h af[4], bfs[NWU];
-#pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = *(const v8h*)(at + swz(wm * 64 + i * 16 + l16, kk * 4 + lg));
-#pragma unroll
-            for (int j = 0; j < NWU; j++) bfs[j] = *(const v8h*)(bt + swz((wu0 + j) * 16 + l16, kk * 4 + lg));
-#pragma unroll
-            for (int j = 0; j < NWU; j++) {
-                const v8h bf = bfs[j];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[i][j], 0, 0, 0);
-                if (do_decode) {
-                    const int sl = kk * NWU + j;
-#pragma unroll
-                    for (int g = sl * NG / NS; g < (sl + 1) * NG / NS; g++) decode_one(h_c, dbuf, g);
-                }
-            }
-        }
-    };
-
-    // ---- prologue: stage 0 in LDS, stage 1's A and block 0's bytes in registers
+    // ---- prologue: stage 0 into buffer 0; stage 1's A, block 1's bytes in flight.  All
+    // loads below are unconditional (indices clamped) so the wait counts stay exact.
     load_blk(wm_cur, x_cur, 0);
-    load_a(0);
-    store_a(0);
-#pragma unroll
-    for (int g = 0; g < 20; g++) decode_one(I0(), 0, g);
-    load_a(1);
-    __syncthreads();
-
-    // ---- main loop: one PTQ1_0 block (two stages) per iteration; the next block's bytes
-    // are loaded during the first stage and become current at the end of the iteration.
-    // Loads are issued unconditionally (the last block rereads itself) so that no branch
-    // hides them from the compiler's wait counting.
+    load_a(I0(), 0);
+    load_a(I1(), 1);
+    load_blk(wm_nxt, x_nxt, 1);
+    store_a(I0(), 0);
+    load_a(I0(), 2);
+    decode(I0(), 0);
+    barrier();
     for (int b = 0; b < nb; b++) {
-        const bool more = b + 1 < nb;
-        const int bn = more ? b + 1 : b;
-        // stage 2b (h=0) in buffer 0; produce stage 2b+1 (h=1 of block b) into buffer 1
-        store_a(1);
-        load_blk(wm_nxt, x_nxt, bn);
-        load_a(2 * bn);
-        stage(0, true, I1(), 1);
-        __syncthreads();
+        // consumers on stage 2b (buffer 0); produce stage 2b+1 = h1 of block b into buffer 1
+        store_a(I1(), 1);
+        load_a(I1(), 2 * b + 3);
+        decode(I1(), 1);
+        barrier();
+        // consumers on stage 2b+1 (buffer 1); produce stage 2b+2 = h0 of block b+1
 #pragma unroll
         for (int i = 0; i < 7; i++) wm_cur[i] = wm_nxt[i];
 #pragma unroll
         for (int i = 0; i < 4; i++) x_cur[i] = x_nxt[i];
-        // stage 2b+1 in buffer 1; produce stage 2b+2 (h=0 of block b+1) into buffer 0
-        store_a(0);
-        load_a(2 * bn + 1);
-        stage(1, more, I0(), 0);
-        __syncthreads();
+        load_blk(wm_nxt, x_nxt, b + 2);
+        store_a(I0(), 0);
+        load_a(I0(), 2 * b + 4);
+        decode(I0(), 0);
+        barrier();
     }
-
-    // ---- store: lane holds D[4*lg + r][l16] of each 16x16 tile
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < NWU; j++) {
-            if (j < nwu) {
-                const int gn = n0 + (wu0 + j) * 16 + l16;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
-                    if (gm < M && gn < N) {
-                        if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][r];
-                        else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][r];
-                    }
-                }
-            }
-        }
 }
 
 }  // namespace
@@ -307,10 +323,10 @@ static hipError_t launch_nwu(const uint16_t* A, int lda, const uint8_t* W, void*
         attr_done = true;
     }
     if (c_dtype == 1)
-        hipLaunchKernelGGL((k_gemm_ptq1_f16<true, NWU>), grid, dim3(256), kLdsBytes, s, (const _Float16*)A, lda, W, C,
+        hipLaunchKernelGGL((k_gemm_ptq1_f16<true, NWU>), grid, dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W, C,
                            ldc, M, K, N, G);
     else
-        hipLaunchKernelGGL((k_gemm_ptq1_f16<false, NWU>), grid, dim3(256), kLdsBytes, s, (const _Float16*)A, lda, W,
+        hipLaunchKernelGGL((k_gemm_ptq1_f16<false, NWU>), grid, dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W,
                            C, ldc, M, K, N, G);
     return hipGetLastError();
 }
