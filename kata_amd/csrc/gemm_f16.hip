@@ -23,7 +23,8 @@
 //    weights, so the dot products are unchanged - which lets each 16-bit-lane pair be
 //    stored as it is.  Wave i of the workgroup decodes the same 4 groups of every row.
 //  * LDS rows are 64 halves (128 B) of 8 chunks of 16 B; chunk c of row r is stored at
-//    c ^ (r & 7), so the MFMA operand reads (16 rows x one chunk) are conflict-free.
+//    c ^ ((r >> 1) & 7), so the MFMA operand reads and the decode stores spread evenly
+//    over the LDS banks.
 #include "common.h"
 #include "launch.h"
 
@@ -37,12 +38,15 @@ namespace {
 constexpr int BM = 128;          // rows of A / C per workgroup
 constexpr int BKS = 64;          // k per stage (halves)
 constexpr int kMaxUnits = 18;    // 16-column units per workgroup
-constexpr int kMaxWaveUnits = 9;
 constexpr int ROWB = BKS * 2;    // LDS bytes per tile row
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
-__device__ inline uint32_t swz(int row, int chunk) { return (uint32_t)(row * ROWB + ((chunk ^ (row & 7)) << 4)); }
+// chunk c of row r lives at slot c ^ ((r >> 1) & 7): with the row's parity that gives 16
+// distinct 16-byte bank positions over any 16 consecutive rows (MFMA operand reads: 16
+// rows x 4 chunks) and over 64 consecutive rows at one chunk (decode stores)
+__device__ inline uint32_t swz(int row, int chunk) { return (uint32_t)(row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4)); }
 
 // (h0..h7) -> (h0,h2,h1,h3, h4,h6,h5,h7): the within-4 k order of the LDS tiles
 __device__ inline uint4 permute_k4(uint4 v) {
@@ -89,7 +93,9 @@ __host__ __device__ constexpr uint32_t p3x2(int n) {
 //        wave 1: dw1 d4 @68, dw4 d3 @104, dw4 d4 @112, dw5 d0 @84
 //        wave 2: dw2 d4 @72, dw5 d1 @92, dw5 d2 @100, dw5 d3 @108
 //        wave 3: dw3 d4 @76, dw5 d4 @116, qh @120..123, qh @124..127
-constexpr int BROWS = 16 * kMaxUnits;              // weight-tile rows in LDS
+// weight-tile rows in LDS: 2 waves x 5 tiles of 32 columns (rows past the tile's R are
+// read by the MFMAs but never stored)
+constexpr int BROWS = 320;
 constexpr int kLdsBytes = 2 * BM * ROWB + 2 * BROWS * ROWB;
 
 // Workgroup = 8 waves, two per SIMD: waves 0..3 are consumers (MFMAs over the LDS stage;
@@ -119,32 +125,40 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
     };
 
     if (consumer) {
+        // 32x32x16 MFMAs (the 16x16x32 form issues at half the rate on gfx950): wave (wm, wn)
+        // owns rows 64wm..64wm+63 (two 32-row tiles) and 32-column tiles [wt0, wt0 + nwt)
+        // of the workgroup's ceil(nu / 2); the last tile may include 16 columns past R,
+        // computed from LDS rows that are never stored.
         const int wm = wave >> 1, wn = wave & 1;
-        const int l16 = lane & 15, lg = lane >> 4;
-        const int wu0 = wn ? (nu + 1) >> 1 : 0;
-        const int nwu = wn ? nu >> 1 : (nu + 1) >> 1;
-        v4f acc[4][NWU];
+        const int l32 = lane & 31, lh = lane >> 5;
+        const int T = (nu + 1) >> 1;
+        const int wt0 = wn ? (T + 1) >> 1 : 0;
+        const int nwt = wn ? T >> 1 : (T + 1) >> 1;
+        v16f acc[2][NWU];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < NWU; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        // all NWU units (a wave with fewer computes columns it never stores; the LDS tile
-        // has BROWS rows)
+            for (int j = 0; j < NWU; j++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
+        // all NWU tiles (a wave with fewer computes tiles it never stores; the LDS weight
+        // tile has BROWS >= 2 * 32 * NWU rows)
         auto compute = [&](int buf) {
             const uint8_t* at = As(buf);
             const uint8_t* bt = Bs(buf);
 #pragma unroll
-            for (int kk = 0; kk < BKS / 32; kk++) {
-                v8h af[4], bfs[NWU];
+            for (int kk = 0; kk < BKS / 16; kk++) {
+                // lane l: row / column l % 32, k = 16 kk + 8 (l / 32) .. +7 = chunk 2kk + l/32
+                v8h af[2], bfs[NWU];
 #pragma unroll
-                for (int i = 0; i < 4; i++) af[i] = *(const v8h*)(at + swz(wm * 64 + i * 16 + l16, kk * 4 + lg));
+                for (int i = 0; i < 2; i++) af[i] = *(const v8h*)(at + swz(wm * 64 + i * 32 + l32, 2 * kk + lh));
 #pragma unroll
-                for (int j = 0; j < NWU; j++) bfs[j] = *(const v8h*)(bt + swz((wu0 + j) * 16 + l16, kk * 4 + lg));
+                for (int j = 0; j < NWU; j++) bfs[j] = *(const v8h*)(bt + swz((wt0 + j) * 32 + l32, 2 * kk + lh));
 #pragma unroll
                 for (int j = 0; j < NWU; j++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bfs[j], acc[i][j], 0, 0, 0);
+                    for (int i = 0; i < 2; i++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfs[j], acc[i][j], 0, 0, 0);
             }
         };
         barrier();                                       // stage 0 produced
@@ -154,19 +168,20 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
             compute(1);
             barrier();
         }
-        // ---- store: lane holds D[4*lg + r][l16] of each 16x16 tile
+        // ---- store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < NWU; j++) {
-                if (j < nwu) {
-                    const int gn = n0 + (wu0 + j) * 16 + l16;
+                if (j < nwt) {
+                    const int gc = (wt0 + j) * 32 + l32;            // tile column
+                    const int gn = n0 + gc;
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
-                        if (gm < M && gn < N) {
-                            if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][r];
-                            else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][r];
+                    for (int q = 0; q < 16; q++) {
+                        const int gm = m0 + wm * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
+                        if (gm < M && gc < R && gn < N) {
+                            if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][q];
+                            else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][q];
                         }
                     }
                 }
@@ -231,6 +246,23 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
     const uint32_t m1 = pw == 0 ? p3x2(0) : pw == 1 ? p3x2(3) : pw == 2 ? p3x2(1) : p3x2(4);
     const uint32_t m2 = pw == 0 ? p3x2(1) : pw == 1 ? p3x2(4) : pw == 2 ? p3x2(2) : 0x00030001u;
     const uint32_t m3 = pw == 0 ? p3x2(2) : pw == 1 ? p3x2(0) : pw == 2 ? p3x2(3) : 0x001b0009u;
+    // Main row decode, batched over the 8 independent byte pairs of 4 dwords (the 16-bit
+    // lanes (b0,b2), (b1,b3) of each) so the dependent digit chains interleave.  Digits are
+    // iterated: t = 3m, digit = t >> 8, next m = t mod 256 (m0 = b); the h=0 stage leaves
+    // the pairs' remainders after digit 3 in mrem for digit 4 at h=1.
+    u16x2 mrem[8];
+    auto emit = [&](uint8_t* bt, int k, u16x2 te, u16x2 to, uint32_t lo, uint32_t hi) {
+        const u16x2 se = (te >> (u16x2){8, 8}) * (u16x2){0x0202, 0x0202} + (u16x2){0x0100, 0x0100};
+        const u16x2 so = (to >> (u16x2){8, 8}) * (u16x2){0x0202, 0x0202} + (u16x2){0x0100, 0x0100};
+        uint2 v;
+        v.x = __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, se));
+        v.y = __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, so));
+        *(uint2*)(bt + swz(rowM, k >> 3) + (k & 7) * 2) = v;
+    };
+    auto split = [&](uint32_t w, u16x2& e, u16x2& o) {
+        e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
+        o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00ff00ffu);
+    };
     // stage h of the current block into buffer buf: the main row's 16 groups, then the
     // extra row's 4
     auto decode = [&](auto h_c, int buf) {
@@ -240,18 +272,39 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
             const uint32_t dbits = wm_cur[6] >> 16;
             const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
             if (h == 0) {
+                u16x2 m[8];
 #pragma unroll
-                for (int g = 0; g < 16; g++) {
-                    const int i = g & 3, n = g >> 2;
-                    decode_group(bt, rowM, 16 * n + 4 * i, wm_cur[i], p3x2(n), lo, hi);
+                for (int i = 0; i < 4; i++) split(wm_cur[i], m[2 * i], m[2 * i + 1]);
+#pragma unroll
+                for (int n = 0; n < 4; n++) {
+                    u16x2 t[8];
+#pragma unroll
+                    for (int p = 0; p < 8; p++) t[p] = m[p] * (u16x2){3, 3};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) emit(bt, 16 * n + 4 * i, t[2 * i], t[2 * i + 1], lo, hi);
+#pragma unroll
+                    for (int p = 0; p < 8; p++) m[p] = t[p] & (u16x2){0xff, 0xff};
                 }
+#pragma unroll
+                for (int p = 0; p < 8; p++) mrem[p] = m[p];
             } else {
+                // digit 4 of dwords 0..3 at k = 4i
 #pragma unroll
-                for (int i = 0; i < 4; i++) decode_group(bt, rowM, 4 * i, wm_cur[i], p3x2(4), lo, hi);
+                for (int i = 0; i < 4; i++)
+                    emit(bt, 4 * i, mrem[2 * i] * (u16x2){3, 3}, mrem[2 * i + 1] * (u16x2){3, 3}, lo, hi);
+                // dwords 4, 5: digits 0..4 at k = 16 + 4i + 8n
+                u16x2 m[4];
+                split(wm_cur[4], m[0], m[1]);
+                split(wm_cur[5], m[2], m[3]);
 #pragma unroll
-                for (int g = 0; g < 10; g++) {
-                    const int i = g & 1, n = g >> 1;          // dword 4 + i, digit n
-                    decode_group(bt, rowM, 16 + 4 * i + 8 * n, wm_cur[4 + i], p3x2(n), lo, hi);
+                for (int n = 0; n < 5; n++) {
+                    u16x2 t[4];
+#pragma unroll
+                    for (int p = 0; p < 4; p++) t[p] = m[p] * (u16x2){3, 3};
+#pragma unroll
+                    for (int i = 0; i < 2; i++) emit(bt, 16 + 4 * i + 8 * n, t[2 * i], t[2 * i + 1], lo, hi);
+#pragma unroll
+                    for (int p = 0; p < 4; p++) m[p] = t[p] & (u16x2){0xff, 0xff};
                 }
                 const uint32_t qh = __builtin_amdgcn_perm(0u, wm_cur[6], 0x01000100u);
                 decode_group(bt, rowM, 56, qh, 0x00030001u, lo, hi);
@@ -346,11 +399,12 @@ hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C
     G = std::max(G, (U + kMaxUnits - 1) / kMaxUnits);
     G = std::min(G, U);
     const int umax = (U + G - 1) / G;                   // units of the widest workgroup
-    const int wmax = (umax + 1) / 2;                    // of its wider wave
+    const int tmax = ((umax + 1) / 2 + 1) / 2;          // 32-column tiles of its wider wave
     const dim3 grid(G, mt);
-    if (wmax <= 3) return launch_nwu<3>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
-    if (wmax <= 5) return launch_nwu<5>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
-    return launch_nwu<kMaxWaveUnits>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    if (tmax <= 1) return launch_nwu<1>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    if (tmax <= 2) return launch_nwu<2>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    if (tmax <= 3) return launch_nwu<3>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    return launch_nwu<5>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
 }
 
 }  // namespace kata
