@@ -18,6 +18,8 @@ Also reported (same JSON line):
                weight bytes, averaged over the sweep's matrices) / its average launch
                duration, vs 8 TB/s HBM;
   per_matrix   GB/s of each matrix kind alone (200 repeats over rotating copies);
+  verify_t2    config 3: the T=2 verify GEMV on the FFN and attention shapes;
+  q8_0_t1      config 3: the Q8_0 MTP-head GEMV, 17408x5120 and 5120x17408;
   prefill_gemm pp512 exact fp16 GEMM TFLOPS (M=512, 5120->17408 and 17408->5120),
                vs 2.5 PFLOP/s dense fp16;
   cpu_baseline the reference's host arithmetic for the path (PTQ1_0 decode + fp32 dot,
@@ -84,6 +86,9 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=2048)
     ap.add_argument("--graph", action="store_true", help="replay per-step HIP graphs instead of eager launches")
+    ap.add_argument("--reps", type=int, default=200, help="repeats per matrix for the per-matrix tables")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
+                    help="only run 20 plain torch copies of MB MiB (HBM-counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -96,6 +101,18 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
+
+    if args.calib_copy:
+        # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE readings give the
+        # counters' scale factor for the HBM-traffic figure
+        n = args.calib_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": n}))
+        return
 
     # ---- weights: one layer-set per copy, copies until >= 512 MB
     set_bytes = sum(packed_bytes(K, N) for _, K, N, _ in SWEEP)
@@ -170,8 +187,20 @@ def main():
 
     # ---- per matrix kind (config 2: 200 repeats each over rotating copies)
     per_matrix = {}
+    def time_reps(fn, nrep):
+        for r in range(3):
+            fn(r)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for r in range(nrep):
+            fn(r)
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / nrep
+
     for j, (name, K, N, grp) in enumerate(SWEEP):
-        nrep = 200
+        nrep = args.reps
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for r in range(nrep):
@@ -181,6 +210,36 @@ def main():
         us = a.elapsed_time(b) * 1e3 / nrep
         per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
                             "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
+
+    # ---- config 3: T=2 speculative-verify GEMV (two fp16 activation columns, one prep
+    # shared per input) and the Q8_0 MTP-head GEMV (17408x5120 and 5120x17408, T=1)
+    verify_t2 = {}
+    for j, (name, K, N, grp) in enumerate(SWEEP):
+        if name not in ("gdn_qkv", "attn_q", "attn_o", "ffn_gate", "ffn_down"):
+            continue
+        x2 = torch.from_numpy(np.random.default_rng(SEED + 300 + j).standard_normal((2, K))
+                              .astype(np.float16)).to(dev)
+        xp2 = ops.gemv_ptq1_prep(x2, K, 2)
+        y2 = torch.empty((2, N), dtype=torch.float32, device=dev)
+        us = time_reps(lambda r: ops.gemv_ptq1_prepped(copies[r % ncopies][j], xp2, K, N, 2, out=y2), args.reps)
+        verify_t2[name] = {"K": K, "N": N, "us": round(us, 3),
+                           "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
+    q8 = {}
+    for name, K, N in (("gate", 5120, 17408), ("down", 17408, 5120)):
+        nb = N * (K // 32) * 34
+        nq8 = max(2, -(-512 * 1024 * 1024 // nb))
+        rng = np.random.default_rng(SEED + 400 + K)
+        blk = rng.integers(-127, 128, size=(N, K // 32, 34), dtype=np.int64).astype(np.int8).view(np.uint8)
+        d = np.abs(rng.normal(0.0, 0.02, size=(N, K // 32))).astype(np.float16).view(np.uint8).reshape(N, K // 32, 2)
+        blk[:, :, 0:2] = d
+        Wq = torch.from_numpy(np.ascontiguousarray(blk).reshape(N, -1)).to(dev)
+        Wqs = [Wq] + [Wq.clone() for _ in range(nq8 - 1)]
+        xq = torch.from_numpy(np.random.default_rng(SEED + 500 + K).standard_normal((1, K))
+                              .astype(np.float16)).to(dev)
+        yq = torch.empty((1, N), dtype=torch.float32, device=dev)
+        us = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq, K, N, 1, out=yq), max(20, args.reps // 4))
+        q8[name] = {"K": K, "N": N, "us": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
+        del Wqs, Wq
 
     # ---- pp512 prefill GEMM (config 4), fp16 exact path
     gemm = None
@@ -215,11 +274,14 @@ def main():
                "sample": f"first {args.cpu_rows} rows of each of the 10 sweep matrices "
                          f"({nbytes/1e6:.1f} MB packed), fp32 decode+dot, OpenMP over rows"}
 
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary
     traffic = None
-    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_ptq1_sweep_traffic.json")
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_ptq1_decode_sweep.md")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    traffic = int(line.split(":")[1])
 
     out = {
         "metric": "ternary GEMV HBM GB/s (% of peak) at bs=1; pp512 prefill GEMM TFLOPS",
@@ -242,6 +304,8 @@ def main():
                      "kernel": "k_gemv_ptq1<1>", "avg_launch_us": round(gemv_launch_us, 3),
                      "bytes_per_launch": bytes_per_launch},
         "per_matrix": per_matrix,
+        "verify_t2": verify_t2,
+        "q8_0_t1": q8,
         "prefill_gemm": gemm,
         "cpu_baseline": cpu,
     }
