@@ -6,8 +6,8 @@
 Workload (the batch-1 decode sweep): one step is the T=1 decode
 GEMV of every ternary matrix of one layer of each kind at the 27B shapes —
 GDN qkv 5120->10240, z 5120->6144, ssm_out 6144->5120; GQA q 5120->12288, k/v 5120->1024,
-o 6144->5120; FFN gate/up 5120->17408, down 17408->5120 — each call including its
-activation preparation (one per distinct input: 6 per step).  Weights are seeded
+o 6144->5120; FFN gate/up 5120->17408, down 17408->5120 — one kernel launch each (the
+activation is quantised inside the GEMV kernel).  Weights are seeded
 synthetic PTQ1_0 (trits iid on {-1,0,1}, fp16 scales |N(0,0.02)|), activations fp16
 N(0,1).  Steps rotate over enough distinct weight copies (>= 512 MB) that no matrix is
 served from the 256 MB Infinity Cache.  `value` = packed weight bytes of all GEMVs of the
@@ -39,7 +39,7 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
-# (name, K, N) of one layer of each kind; x-sharing groups for the activation prep
+# (name, K, N, input) of one layer of each kind; matrices of one input share its activation
 SWEEP = [
     ("gdn_qkv", 5120, 10240, "gdn_in"), ("gdn_z", 5120, 6144, "gdn_in"), ("gdn_ssm_out", 6144, 5120, "gdn_out"),
     ("attn_q", 5120, 12288, "attn_in"), ("attn_k", 5120, 1024, "attn_in"), ("attn_v", 5120, 1024, "attn_in"),
@@ -124,29 +124,19 @@ def main():
         K = next(K for _, K, _, g in SWEEP if g == grp)
         xs[grp] = torch.from_numpy(np.random.default_rng(SEED + 77 + gi).standard_normal((1, K))
                                    .astype(np.float16)).to(dev)
-    xps = {g: torch.empty(ops.xprep_bytes(x.shape[1], 1), dtype=torch.uint8, device=dev) for g, x in xs.items()}
     ys = [torch.empty((1, N), dtype=torch.float32, device=dev) for _, _, N, _ in SWEEP]
 
     def step(i):
         ws = copies[i % ncopies]
-        done = set()
         for j, (name, K, N, grp) in enumerate(SWEEP):
-            if grp not in done:
-                ops.gemv_ptq1_prep(xs[grp], K, 1, out=xps[grp])
-                done.add(grp)
-            ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
-
-    def gemvs_only(i):
-        ws = copies[i % ncopies]
-        for j, (name, K, N, grp) in enumerate(SWEEP):
-            ops.gemv_ptq1_prepped(ws[j], xps[grp], K, N, 1, out=ys[j])
+            ops.gemv_ptq1(ws[j], xs[grp], K, N, 1, out=ys[j])
 
     # One HIP graph per (function, weight copy): replaying graph i % ncopies is step i, so
     # exactly K steps are timed, each with the per-launch overhead of a graph launch.
     use_graph = args.graph
     cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
     runners = {}
-    for fname, fn in (("step", step), ("gemv", gemvs_only)):
+    for fname, fn in (("step", step),):
         for i in range(2):
             fn(i)                                 # first calls set kernel attributes
         torch.cuda.synchronize()
@@ -179,9 +169,8 @@ def main():
     ms_step = ms_total / args.steps
     value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
 
-    # ---- dominant kernel alone: the GEMV launches of the sweep without the preps
-    steps_g = max(20, args.steps // 2)
-    gemv_launch_us = timed("gemv", steps_g) * 1e3 / (steps_g * len(SWEEP))
+    # ---- dominant kernel: a step is nothing but its 10 GEMV launches
+    gemv_launch_us = ms_total * 1e3 / (args.steps * len(SWEEP))
     bytes_per_launch = set_bytes / len(SWEEP)
     achieved = bytes_per_launch / (gemv_launch_us * 1e-6) / 1e9
 
@@ -204,14 +193,14 @@ def main():
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for r in range(nrep):
-            ops.gemv_ptq1_prepped(copies[r % ncopies][j], xps[grp], K, N, 1, out=ys[j])
+            ops.gemv_ptq1(copies[r % ncopies][j], xs[grp], K, N, 1, out=ys[j])
         b.record(stream)
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / nrep
         per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
                             "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
 
-    # ---- config 3: T=2 speculative-verify GEMV (two fp16 activation columns, one prep
+    # ---- config 3: T=2 speculative-verify GEMV (two fp16 activation columns
     # shared per input) and the Q8_0 MTP-head GEMV (17408x5120 and 5120x17408, T=1)
     verify_t2 = {}
     for j, (name, K, N, grp) in enumerate(SWEEP):
@@ -219,9 +208,8 @@ def main():
             continue
         x2 = torch.from_numpy(np.random.default_rng(SEED + 300 + j).standard_normal((2, K))
                               .astype(np.float16)).to(dev)
-        xp2 = ops.gemv_ptq1_prep(x2, K, 2)
         y2 = torch.empty((2, N), dtype=torch.float32, device=dev)
-        us = time_reps(lambda r: ops.gemv_ptq1_prepped(copies[r % ncopies][j], xp2, K, N, 2, out=y2), args.reps)
+        us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], x2, K, N, 2, out=y2), args.reps)
         verify_t2[name] = {"K": K, "N": N, "us": round(us, 3),
                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
     q8 = {}
@@ -297,7 +285,7 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded trits/scales/activations)",
         "config": {"workload": "BASELINE configs[1]: bs=1 decode GEMV sweep, one layer of each kind "
-                               "(10 matrices, 6 activation preps per step)",
+                               "(10 matrices, one GEMV launch each)",
                    "weight_copies": ncopies, "bytes_per_step": set_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -25,7 +25,6 @@ extern "C" {
 #define KATA_OK 0
 #define KATA_EINVAL (-1)  /* bad shape, alignment, dtype or layout argument */
 #define KATA_ELAUNCH (-2) /* a HIP runtime call or kernel launch failed */
-#define KATA_ENOMEM (-3)  /* library work buffer could not be allocated */
 
 /* activation element types */
 #define KATA_F32 0
@@ -42,31 +41,18 @@ const char* kata_version(void);
 
 /* ---------------------------------------------------------------- decode GEMVs -------
  * y[t][n] = sum_b d[n,b] * sum_e trit[n,b,e] * x[t][128b+e], fp32 out, t < T, T in {1,2}.
- * K % 128 == 0, K <= kata_gemv_ptq1_max_k(T) (47104 for T=1, 23040 for T=2), N >= 1.
- * y is [T][N] fp32.
+ * K % 128 == 0, K <= kata_gemv_ptq1_max_k(T), N >= 1.  x is 16-byte aligned; y is [T][N]
+ * fp32.  One kernel launch; no work buffer (the activation is quantised in-kernel).
  * Replaces Engine::dGemvPtq1 (src/engine.cpp:97-101, src/engine.h:155; kernel
  * k_gemv_v1_nr4_sg4, shaders/gemv_fast.metal:9-50) for T = 1, and the `gv` lambda of
  * Engine::verify2 (src/engine.cpp:440-443; k_gemv_lut2_nr4_sg4, shaders/mtp.metal:164-205,
  * or k_gemv_v1h_t2, mtp.metal:66-103) for T = 2.  x_layout KATA_X_HALF2 accepts the
- * interleaved activations k_gemv_lut2 reads (k_ilv2, shaders/mtp.metal:222-224).
- * Uses a library-owned activation work buffer on the current device (allocated on first
- * use); calls on one device must not overlap in time. */
+ * interleaved activations k_gemv_lut2 reads (k_ilv2, shaders/mtp.metal:222-224). */
 int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y,
                    int K, int N, int T, void* stream);
 
-/* Split form of kata_gemv_ptq1 for callers that multiply one activation by several
- * matrices (q/k/v, gate/up): prepare the activation once, then run any number of GEMVs
- * on it.  xprep is caller-owned device memory of kata_gemv_ptq1_xprep_bytes(K, T) bytes,
- * 256-byte aligned.  No counterpart function in the reference: there the producer kernels
- * write the GEMV's activation layout directly (k_add_rms_fwht_t flag 4,
- * shaders/prefill.metal:97). */
-size_t kata_gemv_ptq1_xprep_bytes(int K, int T);
-/* Largest K the PTQ1_0 GEMV accepts for T tokens (its prepared activation lives in LDS). */
+/* Largest K the PTQ1_0 GEMV accepts for T tokens (its activation image lives in LDS). */
 int kata_gemv_ptq1_max_k(int T);
-int kata_gemv_ptq1_prep(const void* x, int x_dtype, int x_layout, void* xprep, int K, int T,
-                        void* stream);
-int kata_gemv_ptq1_prepped(const uint8_t* W, const void* xprep, float* y, int K, int N, int T,
-                           void* stream);
 
 /* Q8_0 GEMV for the MTP head: y[t][n] = sum_b d[n,b] * sum_i q[n,b,i] * x[t][32b+i].
  * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16, y [T][N] fp32.

@@ -14,7 +14,7 @@ _lib = None
 
 KATA_F32, KATA_F16 = 0, 1
 KATA_X_ROWS, KATA_X_HALF2 = 0, 1
-KATA_EINVAL, KATA_ELAUNCH, KATA_ENOMEM = -1, -2, -3
+KATA_EINVAL, KATA_ELAUNCH = -1, -2
 
 
 class KataError(RuntimeError):
@@ -35,10 +35,7 @@ SIGNATURES = {
     "kata_last_error": (ctypes.c_char_p, []),
     "kata_version": (ctypes.c_char_p, []),
     "kata_gemv_ptq1": (I, [P, P, I, I, P, I, I, I, P]),
-    "kata_gemv_ptq1_xprep_bytes": (SZ, [I, I]),
     "kata_gemv_ptq1_max_k": (I, [I]),
-    "kata_gemv_ptq1_prep": (I, [P, I, I, P, I, I, P]),
-    "kata_gemv_ptq1_prepped": (I, [P, P, P, I, I, I, P]),
     "kata_gemv_q8_0": (I, [P, P, I, P, I, I, I, P]),
     "kata_gemm_ptq1_f16": (I, [P, I, P, P, I, I, I, I, I, P]),
     "kata_quant_rows_i8": (I, [P, P, P, I, I, I, P]),

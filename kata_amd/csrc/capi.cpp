@@ -1,5 +1,5 @@
 // C ABI of the gfx950 ternary-matmul library: argument validation, error reporting,
-// the library-owned activation work buffer, the host packers and the engine-style
+// the host packers and the engine-style
 // dispatcher.  Declarations and reference citations: include/kata_amd.h.
 #include <hip/hip_runtime.h>
 
@@ -7,7 +7,6 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <mutex>
 #include <string>
 
 #include "../../include/kata_amd.h"
@@ -35,33 +34,6 @@ int check_launch(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// ---- library-owned activation work buffer, one per device ------------------------------
-constexpr int kMaxDevices = 64;
-struct Work {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-std::mutex g_work_mu;
-Work g_work[kMaxDevices];
-
-int work_buffer(size_t need, void** out) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-        return fail(KATA_ELAUNCH, "hipGetDevice failed");
-    std::lock_guard<std::mutex> lk(g_work_mu);
-    Work& w = g_work[dev];
-    if (w.bytes < need) {
-        if (w.ptr) (void)hipFree(w.ptr);   // hipFree waits for work that still uses it
-        w.ptr = nullptr;
-        w.bytes = 0;
-        const size_t sz = (need + (1 << 20) - 1) & ~(size_t)((1 << 20) - 1);
-        if (hipMalloc(&w.ptr, sz) != hipSuccess) return fail(KATA_ENOMEM, "hipMalloc(%zu) failed", sz);
-        w.bytes = sz;
-    }
-    *out = w.ptr;
-    return KATA_OK;
-}
-
 int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, const void* y, int K, int N,
                     int T) {
     if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
@@ -74,7 +46,7 @@ int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, con
     if (x_layout == KATA_X_HALF2 && (T != 2 || x_dtype != KATA_F16))
         return fail(KATA_EINVAL, "KATA_X_HALF2 needs T=2 and fp16 activations");
     if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
-    if (!aligned(x, x_dtype == KATA_F16 ? 2 : 4)) return fail(KATA_EINVAL, "x misaligned");
+    if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
     return KATA_OK;
 }
 
@@ -86,40 +58,14 @@ const char* kata_last_error(void) { return g_err.c_str(); }
 const char* kata_version(void) { return "kata_amd 0.1 (gfx950)"; }
 
 // ------------------------------------------------------------------ PTQ1_0 GEMV
-size_t kata_gemv_ptq1_xprep_bytes(int K, int T) {
-    if (K <= 0 || K % 128 != 0 || (T != 1 && T != 2)) return 0;
-    return kata::xprep_layout(K, T).bytes;
-}
-
 int kata_gemv_ptq1_max_k(int T) { return (T == 1 || T == 2) ? kata::gemv_max_k(T) : 0; }
-
-int kata_gemv_ptq1_prep(const void* x, int x_dtype, int x_layout, void* xprep, int K, int T, void* stream) {
-    int rc = check_gemv_args((const void*)256, x, x_dtype, x_layout, (const void*)256, K, 1, T);   // x-only checks
-    if (rc) return rc;
-    if (!xprep || !aligned(xprep, 256)) return fail(KATA_EINVAL, "xprep must be non-null and 256-byte aligned");
-    return check_launch(kata::launch_gemv_prep(x, x_dtype, x_layout, (uint8_t*)xprep, K, T, (hipStream_t)stream),
-                        "gemv prep");
-}
-
-int kata_gemv_ptq1_prepped(const uint8_t* W, const void* xprep, float* y, int K, int N, int T, void* stream) {
-    int rc = check_gemv_args(W, (const void*)256, KATA_F32, KATA_X_ROWS, y, K, N, T);   // W/y checks
-    if (rc) return rc;
-    if (!xprep || !aligned(xprep, 256)) return fail(KATA_EINVAL, "xprep must be non-null and 256-byte aligned");
-    return check_launch(kata::launch_gemv_ptq1(W, (const uint8_t*)xprep, y, K, N, T, (hipStream_t)stream),
-                        "gemv ptq1");
-}
 
 int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                    void* stream) {
     int rc = check_gemv_args(W, x, x_dtype, x_layout, y, K, N, T);
     if (rc) return rc;
-    void* xp = nullptr;
-    rc = work_buffer(kata::xprep_layout(K, T).bytes, &xp);
-    if (rc) return rc;
-    hipStream_t s = (hipStream_t)stream;
-    rc = check_launch(kata::launch_gemv_prep(x, x_dtype, x_layout, (uint8_t*)xp, K, T, s), "gemv prep");
-    if (rc) return rc;
-    return check_launch(kata::launch_gemv_ptq1(W, (const uint8_t*)xp, y, K, N, T, s), "gemv ptq1");
+    return check_launch(kata::launch_gemv_ptq1(W, x, x_dtype, x_layout, y, K, N, T, (hipStream_t)stream),
+                        "gemv ptq1");
 }
 
 // ------------------------------------------------------------------ Q8_0 GEMV

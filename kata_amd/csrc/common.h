@@ -31,7 +31,7 @@ __host__ __device__ inline uint32_t ptq1_digit(uint32_t b, uint32_t n) {
 }
 
 // (byte index, digit) of element e of a block
-__host__ __device__ inline void ptq1_elem_src(int e, int& p, int& n) {
+__host__ __device__ constexpr void ptq1_elem_src(int e, int& p, int& n) {
     if (e < 80) { p = e & 15; n = e >> 4; }
     else if (e < 120) { p = 16 + ((e - 80) & 7); n = (e - 80) >> 3; }
     else { p = 24 + ((e - 120) & 1); n = (e - 120) >> 1; }

@@ -6,26 +6,29 @@
 // Design (MI355X-first, not the reference's simdgroup float decode):
 //  * The packed weight bytes are never expanded in memory.  Per 128-weight block four lanes
 //    each hold 8 bytes of it (lane group g = lane/16 takes block bytes 20..27, 0..7, 8..15
-//    or 16..19, rotated by the block's position) and turn them into base-3 digits {0,1,2}:
-//    digits 1..4 of a byte come from one 4-byte LDS table entry, digit 0 = (3b) >> 8 from
-//    16-bit-lane multiplies.  The digits are the B operand (B[k][column]) of three
-//    v_mfma_i32_16x16x64_i8 per block.
-//  * The activation is the A operand (A[i][k]) in a prepared integer form: per 128-block
-//    a scale s = amax/32639 and q = rint(x/s) split into two int8 limbs (q = 256*hi + lo);
+//    or 16..19, rotated by the block's position) and turn them into trits {-1,0,1} as int8:
+//    the trits of digits 1..4 of a byte come from one 4-byte LDS table entry, the digit-0
+//    trit ((3b) >> 8) - 1 from 16-bit-lane multiply-adds.  The trits are the B operand
+//    (B[k][column]) of three v_mfma_i32_16x16x64_i8 per block.
+//  * The activation is the A operand (A[i][k]) in an integer form the kernel builds itself
+//    in LDS from the fp16/fp32 input (no separate preparation launch): per 128-block a
+//    scale s = amax/32639 and q = rint(x/s) split into two int8 limbs (q = 256*hi + lo);
 //    A rows are (block, token, limb), so T = 2 costs no extra matrix-core work.  The matrix
-//    core sums digit*limb exactly in int32; the epilogue forms sum(trit*q) = 256*D_hi +
-//    D_lo - sum(q) per block and token and accumulates y += d * s * that in fp32.  The only
-//    approximation is the 16-bit block-fixed-point activation (|x - s*q| <= amax/65278),
-//    far inside the 1e-3 relative-L2 contract.
-//  * Work unit = a 4-row tile.  The 16 B columns of the MFMA are (row r, block 4c + kq)
-//    and the 16 A rows are (block 4c + kq, token, limb), so one wave step decodes 4
-//    consecutive blocks of 4 rows (four 112-byte runs of the matrix) and the products of
-//    mismatched blocks are never read.  One 1024-thread workgroup per CU splits its tile
-//    range evenly over its 16 waves (see the kernel comment); no atomics, deterministic.
+//    core sums trit*limb exactly in int32, so sum(trit*q) = 256*D_hi + D_lo per block and
+//    token, and y += d * s * that in fp32.  The only approximation is the 16-bit
+//    block-fixed-point activation (|x - s*q| <= amax/65278), far inside the 1e-3
+//    relative-L2 contract.
+//  * Work item = 4 consecutive blocks of a 4-row tile.  The 16 B columns of the MFMA are
+//    (row r, block 4c + kq) and the 16 A rows are (block 4c + kq, token, limb), so one item
+//    decodes four 112-byte runs of the matrix and the products of mismatched blocks are
+//    never read.  One 1024-thread workgroup per CU; each wave keeps one block step's A
+//    operand in registers while it walks the CU's tiles (see the kernel comment); no
+//    atomics, deterministic.
 #include "common.h"
 #include "launch.h"
 
-#include <stdlib.h>
+#include <algorithm>
+#include <type_traits>
 
 namespace kata {
 
@@ -34,100 +37,52 @@ namespace {
 constexpr float kQMax = 32639.0f;   // |q| <= 32639 keeps hi = (q+128)>>8 inside int8
 constexpr int kMfmaPerBlock = 3;
 constexpr int kAImageBytes = kMfmaPerBlock * 4 * 16;   // per block and A row (token, limb)
-
+constexpr int kWaves = 16;
+constexpr int kChunkMax = 3;   // 8-element activation chunks per thread: K <= 3 * 8 * 1024
 
 // A block is read as four 8-byte segments starting at bytes 20, 0, 8, 16 (segment 3 uses
 // only bytes 16..19; bytes 20..23 belong to segment 0).  Segment 0 carries the scale.
 // Lane group g working on block 4c + kq reads segment (g - kq) & 3, so the lanes whose
 // result rows hold that block (g == kq) are the ones holding the scale.
-__host__ __device__ inline int gemv_seg_byte0(int seg) { return seg == 0 ? 20 : seg == 1 ? 0 : seg == 2 ? 8 : 16; }
+__host__ __device__ constexpr int gemv_seg_byte0(int seg) { return seg == 0 ? 20 : seg == 1 ? 0 : seg == 2 ? 8 : 16; }
 
-// Byte p and digit n of the A/B operand slot (segment seg, MFMA m, dword dw, byte kb),
-// or p = -1 for a slot that multiplies a zero activation.  With w0/w1 the lane's two
-// weight dwords (bytes b0..b7) the B dwords are
+// Offset of element e of a block with quarter kq (block index & 3) inside the block's A
+// image [m 3][g 4][i 2T][16 B] (row i = 0: token 0's high limb).  Element e sits at byte
+// p, digit n (ptq1_elem_src); byte p is in segment seg at d = p - gemv_seg_byte0(seg), and
+// lane group g = (seg + kq) & 3 reads that segment.  With b0..b7 the lane's 8 bytes
+// (w0 = b0..b3, w1 = b4..b7) the B dwords are
 //   m=0: L(b0) L(b1) L(b2) L(b3)     m=1: Z(w0) L(b4) L(b5) L(b6)     m=2: L(b7) Z(w1) 0 0
-// where L(b) = digits 1..4 of byte b and Z(w) = digit 0 of the dword's bytes 0..3.
-__host__ __device__ inline void gemv_slot(int seg, int m, int dw, int kb, int& p, int& n) {
-    const int base = gemv_seg_byte0(seg);
-    const int kind = m * 4 + dw;   // 0..11
-    // L slots: byte offset within the lane's 8 bytes; Z slots: -(1 + word); -9: unused
-    const int desc[12] = {0, 1, 2, 3, -1, 4, 5, 6, 7, -2, -9, -9};
-    const int d = desc[kind];
-    if (d == -9) {
-        p = -1;
-        return;
-    }
-    if (d >= 0) {
-        p = base + d;
-        n = kb + 1;
-    } else {
-        p = base + (-d - 1) * 4 + kb;
-        n = 0;
-    }
-    if (seg == 3 && p >= 20) p = -1;   // bytes 20..23 belong to segment 0
+// where L(b) = digits 1..4 of byte b (byte kb holds digit kb + 1) and Z(w) = digit 0 of
+// the dword's bytes (byte kb for byte kb).  Image bytes that carry no element (the scale
+// bytes, qh digit 4, bytes 20..23 as read by segment 3) hold a zero activation.
+__host__ __device__ constexpr int gemv_elem_img_off(int e, int kq, int T) {
+    int p = 0, n = 0;
+    ptq1_elem_src(e, p, n);
+    const int seg = p < 8 ? 1 : p < 16 ? 2 : p < 20 ? 3 : 0;
+    const int d = p - gemv_seg_byte0(seg), g = (seg + kq) & 3;
+    const int kind = n > 0 ? (d < 4 ? d : d + 1) : (d < 4 ? 4 : 9);
+    const int kb = n > 0 ? n - 1 : d & 3;
+    return (kind >> 2) * (4 * 2 * T * 16) + g * (2 * T * 16) + (kind & 3) * 4 + kb;
 }
 
-// One workgroup per virtual block vb (0 <= vb < 4*nq; blocks nb.. are zero padding so
-// every tile has nq steps of 4 blocks).  Writes the pair (scale s as float, sum(q) as int)
-// per token at scales[vb][t] and the A image [m 3][g 4][i 2T][16 B], i = 2*t + limb, laid
-// out for lane group g reading segment (g - (vb & 3)) & 3.
-template <int T>
-__global__ __launch_bounds__(128) void k_gemv_prep(const void* __restrict__ x, int x_dtype, int x_layout,
-                                                   uint8_t* __restrict__ xprep, int K, int nq, size_t off_a) {
-    __shared__ int16_t qs[T][128];
-    __shared__ float red_f[2][T];
-    __shared__ int red_i[2][T];
-    const int b = blockIdx.x, e = threadIdx.x, lane = e & 63, wv = e >> 6;
-    const bool real = b < K / kGroup;
-    float v[T];
-#pragma unroll
-    for (int t = 0; t < T; t++) {
-        const size_t idx = x_layout == 1 ? ((size_t)b * 128 + e) * 2 + t : (size_t)t * K + (size_t)b * 128 + e;
-        v[t] = !real ? 0.0f : x_dtype == 1 ? (float)((const _Float16*)x)[idx] : ((const float*)x)[idx];
-        float a = fabsf(v[t]);
-        for (int o = 32; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
-        if (lane == 0) red_f[wv][t] = a;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < T; t++) {
-        const float amax = fmaxf(red_f[0][t], red_f[1][t]);
-        const float inv = amax > 0.0f ? kQMax / amax : 0.0f;
-        const float r = fminf(fmaxf(rintf(v[t] * inv), -kQMax), kQMax);
-        const int q = (int)r;
-        qs[t][e] = (int16_t)q;
-        int s = q;
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-        if (lane == 0) red_i[wv][t] = s;
-        if (e == 0) ((float*)xprep)[(b * T + t) * 2] = amax / kQMax;
-    }
-    __syncthreads();
-    if (e < T) ((int*)xprep)[(b * T + e) * 2 + 1] = red_i[0][e] + red_i[1][e];
-    const int kq = b & 3;
-    uint32_t* out = (uint32_t*)(xprep + off_a + (size_t)b * kAImageBytes * 2 * T);
-    for (int w = e; w < kAImageBytes / 4 * 2 * T; w += 128) {
-        const int dw = w & 3, i = (w >> 2) % (2 * T), g = (w / (8 * T)) & 3, m = w / (32 * T);
-        const int t = i >> 1, limb = i & 1;
-        uint32_t word = 0;
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            int p, n;
-            gemv_slot((g - kq) & 3, m, dw, kb, p, n);
-            const int el = p >= 0 ? ptq1_slot_elem(p, n) : -1;
-            if (el >= 0) {
-                const int qq = qs[t][el];
-                const int hi = (qq + 128) >> 8, lo = qq - 256 * hi;
-                word |= (uint32_t)(uint8_t)(int8_t)(limb ? lo : hi) << (8 * kb);
-            }
-        }
-        out[w] = word;
-    }
+// Image offsets of the 8 elements a quantising thread owns: thread index & 63 =
+// 16*kq + sub, elements 8*sub .. 8*sub + 7 of a block with quarter kq; [T - 1][idx][e].
+struct alignas(16) ImgOffTable {
+    uint16_t v[2][64][8];
+};
+constexpr ImgOffTable make_img_off_table() {
+    ImgOffTable t{};
+    for (int T = 1; T <= 2; T++)
+        for (int idx = 0; idx < 64; idx++)
+            for (int e = 0; e < 8; e++) t.v[T - 1][idx][e] = (uint16_t)gemv_elem_img_off(8 * (idx & 15) + e, idx >> 4, T);
+    return t;
 }
+__constant__ ImgOffTable kImgOff = make_img_off_table();
 
 // Digit table: 256 entries of 4 bytes (digits 1..4 of the byte value), each replicated
 // 2^LR times; lane l reads replica l mod 2^LR so the lanes an LDS cycle serves hit distinct
 // banks.  With 64 replicas (LR = 6) an entry row is 256 bytes and one v_perm_b32 forms
-// the address [replica*4, byte, 0, 0]; smaller tables (when the prepared activation needs
+// the address [replica*4, byte, 0, 0]; smaller tables (when the activation image needs
 // the LDS) use a shift and an or.
 template <int LR>
 __device__ inline uint32_t lut_addr(uint32_t w, int q, uint32_t laneoff) {
@@ -136,264 +91,409 @@ __device__ inline uint32_t lut_addr(uint32_t w, int q, uint32_t laneoff) {
 }
 __host__ __device__ constexpr int lut_bytes(int LR) { return 256 * (4 << LR); }
 
-// digit 0 = (3b) >> 8 of the four bytes of w, byte k of the result for byte k of w.  Bytes
-// (0,2) and (1,3) are spread into 16-bit lanes and tripled (3b < 768 cannot carry into the
-// next lane); the digit is then byte 1 of its lane.
-__device__ inline uint32_t digit0_word(uint32_t w) {
-    const uint32_t e = w & 0x00ff00ffu, o = __builtin_amdgcn_perm(0u, w, 0x0c030c01u);
-    const uint32_t e3 = e + (e << 1), o3 = o + (o << 1);
-    return __builtin_amdgcn_perm(o3, e3, 0x07030501u);
-}
-
 typedef __attribute__((address_space(3))) const uint8_t lds_u8;
-// 32-bit load at byte offset addr of an LDS array; for the digit table, the kernel's only
-// static LDS, the base is address 0 and folds away.
+// 32-bit load at byte offset addr of an LDS array; for the digit table, the kernel's first
+// static LDS array, the base is address 0 and folds away.
 __device__ inline uint32_t lds_u32(lds_u8* base, uint32_t addr) {
     return *(__attribute__((address_space(3))) const uint32_t*)(base + addr);
 }
 
-// Work split: one 1024-thread workgroup (16 waves) per CU owns the contiguous tile range
-// [wt0, wt0 + tpw).  Its (tile, block step) pairs, numbered s = (tile - wt0) * nq + c, are
-// cut into 16 equal contiguous runs, one per wave.  Lane x + 16*g: B column x = (row
-// r = x & 3, block 4c + kq with kq = x >> 2), A row x = (block 4c + (x >> 2), token
-// (x >> 1) & 1, limb x & 1); result rows 4g..4g+3 belong to block 4c + g, so lane
-// 20*q + r holds row r's sum over blocks 4c + q ("quarter" q of the tile's blocks).
-//
-// Timeline: the digit table is written and the activation staging (global -> LDS DMA) is
-// issued by every wave before any wave issues weight loads (vector-memory loads complete
-// in order per CU, so staging queued behind the ring would arrive only after it); then
-// every wave keeps D weight steps in flight in a register ring (step j in slot j % D) and
-// decodes step j as soon as its own load has landed.
-// Each step's operands are issued one step ahead of its MFMAs.  When a tile's last step
-// of a run is done the 16 diagonal lanes store their sums to the wave's LDS slot for that
-// tile; after one barrier the workgroup adds the slots of each tile over waves and quarters
-// in fixed order (deterministic).  Dynamic LDS: A image (384*T B per virtual block, 64 B
-// between quarters), (scale, sum) pairs, per-wave tile sums [16][slots][T][16].
-constexpr int kWaves = 16;
-// LDS bytes of the A image (4 quarters, 64 B apart) and of the (scale, sum) pairs, rounded
-// up to whole staging chunks
-__host__ __device__ inline int gemv_a_lds_bytes(int qbytes) { return (4 * (qbytes + 64) + 1023) & ~1023; }
-__host__ __device__ inline int gemv_s_lds_bytes(int nbv, int T) { return (8 * nbv * T + 1023) & ~1023; }
-// static LDS of the GEMV kernel: digit table + run_tiles
-__host__ __device__ constexpr int gemv_static_lds_bytes(int LR) { return lut_bytes(LR) + kWaves * 8; }
+// LDS bytes of the A image (4 quarters, 64 B apart) and of the (scale, 0) pairs
+__host__ __device__ inline int gemv_a_lds_bytes(int qbytes) { return 4 * (qbytes + 64); }
+__host__ __device__ inline int gemv_s_lds_bytes(int nbv, int T) { return (8 * nbv * T + 15) & ~15; }
+// static LDS of the GEMV kernel: the trit table
+__host__ __device__ constexpr int gemv_static_lds_bytes(int LR) { return lut_bytes(LR); }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <int T, int LR, int D>
-__global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ W, const uint8_t* __restrict__ xprep,
-                                                    float* __restrict__ y, int K, int N, int nq, int tpw, int slots,
-                                                    size_t off_a) {
-    static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by step parity");
+// LDS DMA of 16 bytes per lane: lane l's 16 bytes at g go to LDS byte address lds + 16*l
+// (lds wave-uniform).  Issued through inline assembly so that the compiler does not make
+// every later LDS access wait for all vector-memory loads in flight (it cannot tell which
+// LDS bytes a DMA writes); the kernel waits for these copies explicitly.  M0 is restored.
+__device__ inline void dma16(const void* g, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(lds)
+                 : "memory");
+}
+__device__ inline uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p);
+}
+
+// 8 consecutive activations x[t][k0..k0+7] as floats.  Layouts: rows x[T][K] (fp16 or
+// fp32), or half2-interleaved x[K][2] fp16 (T = 2).
+template <int T>
+__device__ inline void load_x8(const void* x, int x_dtype, int x_layout, int K, int k0, float (&v)[T][8]) {
+    if (x_layout == 1) {
+        const uint4* p = (const uint4*)((const _Float16*)x + (size_t)k0 * 2);
+        const uint4 a = p[0], b = p[1];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const v2h h = __builtin_bit_cast(v2h, w[i]);
+            v[0][i] = (float)h[0];
+            if (T == 2) v[T - 1][i] = (float)h[1];
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        if (x_dtype == 1) {
+            const uint4 a = *(const uint4*)((const _Float16*)x + (size_t)t * K + k0);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const v2h h = __builtin_bit_cast(v2h, w[i]);
+                v[t][2 * i] = (float)h[0];
+                v[t][2 * i + 1] = (float)h[1];
+            }
+        } else {
+            const float4* p = (const float4*)((const float*)x + (size_t)t * K + k0);
+            const float4 a = p[0], b = p[1];
+            v[t][0] = a.x; v[t][1] = a.y; v[t][2] = a.z; v[t][3] = a.w;
+            v[t][4] = b.x; v[t][5] = b.y; v[t][6] = b.z; v[t][7] = b.w;
+        }
+    }
+}
+
+// The same from a raw copy of x in LDS (same layouts).
+template <int T>
+__device__ inline void load_x8_lds(const uint8_t* xs, int x_dtype, int x_layout, int K, int k0, float (&v)[T][8]) {
+    if (x_layout == 1) {
+        const uint4* p = (const uint4*)(xs + (size_t)k0 * 4);
+        const uint4 a = p[0], b = p[1];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const v2h h = __builtin_bit_cast(v2h, w[i]);
+            v[0][i] = (float)h[0];
+            if (T == 2) v[T - 1][i] = (float)h[1];
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        if (x_dtype == 1) {
+            const uint4 a = *(const uint4*)(xs + ((size_t)t * K + k0) * 2);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const v2h h = __builtin_bit_cast(v2h, w[i]);
+                v[t][2 * i] = (float)h[0];
+                v[t][2 * i + 1] = (float)h[1];
+            }
+        } else {
+            const float4* p = (const float4*)(xs + ((size_t)t * K + k0) * 4);
+            const float4 a = p[0], b = p[1];
+            v[t][0] = a.x; v[t][1] = a.y; v[t][2] = a.z; v[t][3] = a.w;
+            v[t][4] = b.x; v[t][5] = b.y; v[t][6] = b.z; v[t][7] = b.w;
+        }
+    }
+}
+
+// f(integral_constant<int, i>) for i = 0 .. NN-1, unrolled at compile time
+template <int I, int NN, typename F>
+__device__ inline void static_for_impl(F&& f) {
+    if constexpr (I < NN) {
+        f(std::integral_constant<int, I>{});
+        static_for_impl<I + 1, NN>(f);
+    }
+}
+template <int NN, typename F>
+__device__ inline void static_for(F&& f) {
+    static_for_impl<0, NN>(f);
+}
+
+// Butterfly max / sum over the 16 lanes of a DPP row (xor 1, xor 2, then the half-row
+// and row mirrors), every lane ends with the result; fixed order, so deterministic.
+__device__ inline float row16_max(float a) {
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xb1, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4e, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x141, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x140, 0xf, 0xf, false)));
+    return a;
+}
+__device__ inline int row16_sum(int a) {
+    a += __builtin_amdgcn_mov_dpp(a, 0xb1, 0xf, 0xf, false);
+    a += __builtin_amdgcn_mov_dpp(a, 0x4e, 0xf, 0xf, false);
+    a += __builtin_amdgcn_mov_dpp(a, 0x141, 0xf, 0xf, false);
+    a += __builtin_amdgcn_mov_dpp(a, 0x140, 0xf, 0xf, false);
+    return a;
+}
+__device__ inline float row16_fsum(float a) {
+    a += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xb1, 0xf, 0xf, false));
+    a += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4e, 0xf, 0xf, false));
+    a += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x141, 0xf, 0xf, false));
+    a += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x140, 0xf, 0xf, false));
+    return a;
+}
+
+// trit 0 = ((3b) >> 8) - 1 of the four bytes of w as int8, byte k for byte k of w.  Bytes
+// (0,2) and (1,3) are spread into 16-bit lanes; 3b - 256 (no carry between the lanes) has
+// the trit in its high byte.
+__device__ inline uint32_t trit0_word(uint32_t w) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
+    const u16x2 o = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c030c01u));
+    const u16x2 e3 = e * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    const u16x2 o3 = o * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, o3), __builtin_bit_cast(uint32_t, e3), 0x07030501u);
+}
+
+// Work split ("activation-stationary").  One 1024-thread workgroup (16 waves) per CU owns
+// the contiguous tile range [wt0, wt0 + Tt) (4 rows per tile).  Its work items (c, tile) —
+// 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered c-major,
+// s = c * Tt + tile, and cut into 16 equal contiguous runs, one per wave, so a wave keeps
+// the A operand of one block step c in registers across many tiles and reloads it from
+// LDS only when c changes.  Lane x + 16*g: B column x = (row r = x & 3, block 4c + kq with
+// kq = x >> 2), A row x = (block 4c + (x >> 2), token (x >> 1) & 1, limb x & 1); result
+// rows 4g..4g+3 belong to block 4c + g, so lane 20*q + r holds row r's sum over block
+// 4c + q.  Those 16 lanes store their scaled sums to the item's LDS slot (the other lanes
+// store to a scratch slot: no exec-mask changes in the loop); at the end each output row
+// adds its nq * 4 slots in a fixed order (deterministic, no atomics).
+//
+// Timeline.  (1) Wave 0 (the first wave of the workgroup to launch) copies the scatter
+// offsets and (XS) the raw activation into LDS by DMA before any weight load is queued on
+// the CU; every wave writes its part of the trit table and clears the A image, then issues
+// its first weight items into a register ring of D slots (item j in slot j % D).  (2) After a
+// barrier each thread quantises its activation chunks (block amax by DPP) and (3) scatters
+// the limbs into the A image.  (4) Every wave decodes item j + 1 while the matrix cores
+// run item j and reloads each ring slot after use; the loop body keeps scalar bookkeeping
+// to a few instructions per item (the CU issues one scalar instruction per SIMD every
+// four cycles, the same rate as the wave64 vector instructions).
+// Dynamic LDS: A image (384*T B per virtual block, quarters 64 B apart), (scale, 0)
+// pairs [vb][t], the scatter offsets (1 KB), a scratch slot for the off-diagonal lanes
+// (512 B), then item sums [S][T][16] floats, which with XS first hold the raw activation.
+template <int T, int LR, int D, bool PAD, bool XS>
+__global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ W, const void* __restrict__ x,
+                                                    int x_dtype, int x_layout, float* __restrict__ y, int K, int N,
+                                                    int nq, int tpw) {
+    static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by item parity");
     constexpr int ASTRIDE = 4 * 2 * T * 16;      // A image bytes per (virtual block, MFMA)
+    constexpr int BLK = kMfmaPerBlock * ASTRIDE;  // A image bytes per virtual block
     constexpr int REPS = 1 << LR;
     constexpr int QPAD = 64;
-    // digit table: the kernel's only static LDS besides run_tiles, at LDS address 0
+    // trit table first: the kernel's static LDS starts at address 0
     __shared__ uint4 lut[lut_bytes(LR) / 16];
-    __shared__ int2 run_tiles[kWaves];          // first and last tile (local) of each wave's run
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int x = lane & 15, g = lane >> 4;
-    const int r = x & 3, kq = x >> 2;
+    const int x_ = lane & 15, g = lane >> 4;
+    const int r = x_ & 3, kq = x_ >> 2;
     const int nb = K >> 7, nbv = 4 * nq;
     const int tiles = (N + 3) >> 2;
-    const int wt0 = blockIdx.x * tpw, wt1 = min(tiles, wt0 + tpw);
-    const int S = (wt1 - wt0) * nq;
+    const int wt0 = blockIdx.x * tpw;
+    const int Tt = min(tiles, wt0 + tpw) - wt0;
+    const int S = nq * Tt;
     const int s0 = (wave * S) / kWaves, s1 = ((wave + 1) * S) / kWaves;
     const int n = s1 - s0;                       // this wave's run length (wave-uniform)
-    const int c0 = s0 % nq;
-    if (lane == 0) run_tiles[wave] = n > 0 ? make_int2(s0 / nq, (s1 - 1) / nq) : make_int2(1 << 30, -1);
+    const int qbytes = nq * BLK;                 // A image bytes per quarter
+    uint8_t* As = smem;
+    uint8_t* Ss = smem + gemv_a_lds_bytes(qbytes);            // (scale, 0) pairs [vb][t]
+    uint8_t* Os = Ss + gemv_s_lds_bytes(nbv, T);               // scatter offsets [64][8] u16
+    uint8_t* Js = Os + 1024;                                   // scratch slot [T][64] floats
+    float* part = (float*)(Js + 512);                          // [S][T][16]
+    uint8_t* Xs = (uint8_t*)part;                // XS: raw activation, until the main loop
 
-    // Digit table.  Consecutive threads store consecutive 16-byte words (no bank
-    // conflicts); word o holds 4 replicas of entry o / (REPS / 4).
+    // (1a) wave 0: DMA of the scatter offsets and (XS) the raw activation; without XS every
+    // thread loads its own chunks.  Chunk j = tid + 1024 i covers k = 8j..8j+7 of every
+    // token; the 16 chunks of a block are 16 consecutive lanes (one DPP row), and their
+    // quarter (j >> 4) & 3 and sub-block position j & 15 do not depend on i.
+    const int nch = K >> 3;
+    const int xbytes = T * K * (x_dtype == 1 ? 2 : 4);
+    float v[XS ? 1 : kChunkMax][T][8];
+    if (wave == 0) {
+        dma16((const uint4*)&kImgOff.v[T - 1][0][0] + lane, lds_addr(Os));
+        if constexpr (XS) {
+            const int xvec = xbytes / 16;
+            for (int o = 0; o < xvec; o += 64) dma16((const uint4*)x + min(o + lane, xvec - 1), lds_addr(Xs + o * 16));
+        }
+    }
+    if constexpr (!XS) {
+#pragma unroll
+        for (int i = 0; i < kChunkMax; i++) {
+            const int j = tid + 1024 * i;
+            if (j < nch) load_x8<T>(x, x_dtype, x_layout, K, 8 * j, v[i]);
+        }
+    }
+
+    // (1b) trit table.  Consecutive threads store consecutive 16-byte words (no bank
+    // conflicts); word o holds 4 replicas of entry o / (REPS / 4): trits of digits 1..4.
 #pragma unroll
     for (int i = 0; i < lut_bytes(LR) / 16 / 1024; i++) {
         const int o = tid + i * 1024;
         const uint32_t bv = (uint32_t)o / (REPS / 4);
         const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
                        m4 = (m3 * 3u) & 0xffu;
-        const uint32_t e = ((m1 * 3u) >> 8) | (((m2 * 3u) >> 8) << 8) | (((m3 * 3u) >> 8) << 16) |
-                           (((m4 * 3u) >> 8) << 24);
+        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
+                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
         lut[o] = make_uint4(e, e, e, e);
     }
+    // clear the A image (slots without an element and padding blocks stay zero) and the
+    // scales of the padding blocks
+    for (int o = tid; o < gemv_a_lds_bytes(qbytes) / 16; o += 1024) ((uint4*)As)[o] = make_uint4(0, 0, 0, 0);
+    for (int o = nb * T + tid; o < nbv * T; o += 1024) ((int2*)Ss)[o] = make_int2(0, 0);
 
-    // Weight loads: raw buffer loads with 32-bit offsets; bytes past the matrix read as 0
-    // (rows >= N).  Padding blocks (past K) reread the row's last block; their activation,
-    // scale and sum are zero.  Every ring slot is reloaded once per step, also past the
-    // run's end, so all paths issue the same loads and the compiler's wait counts stay
-    // exact.
+    // (1c) weight ring.  Raw buffer loads: per-lane offset (row r of the tile, block kq of
+    // the step, the lane group's segment) plus a wave-uniform item offset; bytes past the
+    // matrix read as 0 (rows >= N; with PAD also the padding blocks of the last row).
+    // Loads past the run's end use an offset beyond the buffer: zeros, no memory access.
     const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
+    const uint32_t tstep = 4 * row_bytes;        // next tile
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
-    // loads past the run's end go through an empty descriptor: zeros, no memory access
-    const __amdgpu_buffer_rsrc_t wnone = __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, 0, 0x00020000);
-    const uint32_t qoff = (uint32_t)kq * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
-    const uint32_t qlim = (uint32_t)(nb - 1) * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
-    uint32_t rowoff = (uint32_t)((wt0 + s0 / nq) * 4 + r) * row_bytes;
-    int lc = c0, ld_left = n;                    // load cursor (wave-uniform)
-    uint32_t lcb = (uint32_t)c0 * 4 * kBlockBytes;   // lc * 4 blocks
+    const uint32_t voff = (uint32_t)r * row_bytes + (uint32_t)kq * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
+    int lt = s0 % Tt;                            // load cursor: tile, item offset, items left
+    uint32_t lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(s0 / Tt) * 4 * kBlockBytes;
+    int lrem = n;
+    const uint32_t cwrap = 4 * kBlockBytes - (uint32_t)(Tt - 1) * tstep;   // last tile -> next c
     uint32_t wl[D], wh[D];
     auto load_next = [&](int slot) {
-        const uint32_t off = rowoff + min(qoff + lcb, qlim);
-        const u32x2 w =
-            __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ld_left > 0 ? wrsrc : wnone, (int)off, 0, 0));
+        const uint32_t so = lrem > 0 ? lso : 0x80000000u;
+        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, (int)voff, (int)so, 0));
         wl[slot] = w.x;
         wh[slot] = w.y;
-        if (ld_left > 1) {
-            lcb += 4 * kBlockBytes;
-            if (++lc == nq) {
-                lc = 0;
-                lcb = 0;
-                rowoff += 4 * row_bytes;
-            }
-        }
-        --ld_left;
+        const bool wrap = ++lt == Tt;
+        lt = wrap ? 0 : lt;
+        lso += wrap ? cwrap : tstep;
+        --lrem;
     };
-    // Activation staging by DMA; each wave fills whole 1 KB LDS chunks, padding slots load
-    // a duplicate in-range element.
-    const int qbytes = nq * kAImageBytes * 2 * T;
-    const int qvec = qbytes / 16;                // 16-byte vectors per quarter in xprep
-    const int a_bytes = gemv_a_lds_bytes(qbytes);
-    const int s_bytes = gemv_s_lds_bytes(nbv, T);
-    uint8_t* As = smem;
-    uint8_t* Ss = smem + a_bytes;                // (scale, sum) pairs [vb][t]
-    float* part = (float*)(Ss + s_bytes);        // [kWaves][slots][T][16]
-    {
-        typedef __attribute__((address_space(3))) void lds_void;
-        const uint4* a_src = (const uint4*)(xprep + off_a);
-        for (int ch = wave; ch < a_bytes / 1024; ch += kWaves) {
-            const int o = ch * 64 + lane;        // LDS vector index
-            // LDS quarter q holds blocks 4c + q, c = 0..nq-1, in order
-            const int q = o / (qvec + QPAD / 16), w = min(o - q * (qvec + QPAD / 16), qvec - 1);
-            const int bv = kAImageBytes * 2 * T / 16;   // vectors per block
-            const int src = (4 * (w / bv) + min(q, 3)) * bv + w % bv;
-            __builtin_amdgcn_global_load_lds(a_src + src, (lds_void*)(As + ch * 1024), 16, 0, 0);
-        }
-        const uint4* s_src = (const uint4*)xprep;
-        const int svec = nbv * T * 8 / 16;      // (scale, sum) pairs: 16-byte vectors (T=1: 2 blocks)
-        for (int ch = wave; ch < s_bytes / 1024; ch += kWaves) {
-            const int o = min(ch * 64 + lane, svec - 1);
-            __builtin_amdgcn_global_load_lds(s_src + o, (lds_void*)(Ss + ch * 1024), 16, 0, 0);
-        }
-    }
-    // All staging DMA of the workgroup is issued before any wave issues its ring, so the
-    // staging is at the head of the CU's in-order vector-memory queue (no wait here).
-    __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int u = 0; u < D; u++) load_next(u);
-    // The staging DMA is older than the D ring loads, so "at most D vector-memory loads
-    // pending" means it has landed; lgkmcnt(0) covers the table stores.  A bare s_barrier
-    // (a release fence would also wait for the ring) then publishes both.
-    __builtin_amdgcn_s_waitcnt((D & 15) | ((D >> 4) << 14) | (7 << 4) | (0 << 8));
+
+    // the staged offsets and activation (wave 0: everything but the D ring loads has
+    // landed), the trit table and the cleared image are visible after this barrier
+    __builtin_amdgcn_s_waitcnt((D & 15) | ((D >> 4) << 14) | (7 << 4) | (0 << 8));   // vmcnt(D) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
 
+    // (2) quantise: per block and token s = amax / 32639, q = rint(x * (32639 / amax))
+    // (0 if amax = 0; |q| <= 32639, so hi = (q + 128) >> 8 fits int8), and (3) scatter the
+    // limbs hi and lo = q - 256 hi (the low byte of q): element 8*(j & 15) + e of block
+    // j >> 4 goes to image offset gemv_elem_img_off(8*(j & 15) + e, (j >> 4) & 3, T) +
+    // 16*(2t + limb) of that block
+    {
+        const uint4 offw = *(const uint4*)(Os + (tid & 63) * 16);
+        const uint32_t ow[4] = {offw.x, offw.y, offw.z, offw.w};
+        int off[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) off[e] = (int)((ow[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        auto process = [&](int j, float (&vv)[T][8]) {
+            const int b = j >> 4;
+            uint8_t* img = As + (b & 3) * (qbytes + QPAD) + (b >> 2) * BLK;
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(vv[t][e]));
+                a = row16_max(a);
+                const float inv = a > 0.0f ? kQMax / a : 0.0f;
+                if ((j & 15) == 0) ((int2*)Ss)[b * T + t] = make_int2(__builtin_bit_cast(int, a * (1.0f / kQMax)), 0);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int q = (int)rintf(vv[t][e] * inv);
+                    img[off[e] + 32 * t] = (uint8_t)((q + 128) >> 8);
+                    img[off[e] + 32 * t + 16] = (uint8_t)q;
+                }
+            }
+        };
+        if constexpr (XS) {
+            for (int j = tid; j < nch; j += 1024) {   // whole 16-lane rows drop out together
+                float vv[T][8];
+                load_x8_lds<T>(Xs, x_dtype, x_layout, K, 8 * j, vv);
+                process(j, vv);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kChunkMax; i++) {
+                const int j = tid + 1024 * i;
+                if (j < nch) process(j, v[i]);
+            }
+        }
+    }
+    // LDS-only barrier: a release fence here would also wait for the weight ring
+    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+
+    // (4) main loop
     const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
     lds_u8* lb = (lds_u8*)lut;
-    // A rows with token >= T only feed result rows the epilogue never reads: those lanes
-    // skip the activation loads and keep whatever their registers hold.
-    const bool a_active = ((x >> 1) & 1) < T;
-    const uint8_t* xa = As + kq * (qbytes + QPAD) + g * (2 * T * 16) + (a_active ? (x & (2 * T - 1)) : 0) * 16;
-    const uint8_t* xs = Ss + kq * (8 * T);
-    const bool sum_lane = g == kq;               // lane 20*q + r: the diagonal quarter
-    float* my_part = part + (size_t)wave * slots * T * 16 + g * 4 + r;
-    v4i A0[kMfmaPerBlock], A1[kMfmaPerBlock], B0[kMfmaPerBlock], B1[kMfmaPerBlock];
-    uint4 SQ0, SQ1;
+    // A rows with token >= T only feed result rows that are never stored
+    const uint8_t* xa = As + kq * (qbytes + QPAD) + g * (2 * T * 16) + (x_ & (2 * T - 1)) * 16;
+    const float* xs = (const float*)Ss + kq * (2 * T);
+    // item sums: the diagonal lanes 20*q + r store to slot 4q + r of the item, the others to
+    // their scratch word: address = base + diag * item offset
+    const uint32_t diag = g == kq ? 1u : 0u;
+    uint8_t* pbase = diag ? (uint8_t*)part + (g * 4 + r) * 4 : Js + lane * 4;
+    v4i A[kMfmaPerBlock];
+    float sc[T];
+    auto load_a = [&](int c) {
 #pragma unroll
-    for (int m = 0; m < kMfmaPerBlock; m++) { A0[m] = v4i{0, 0, 0, 0}; A1[m] = v4i{0, 0, 0, 0}; }
-
-    // operands of step c (block qbase + c of this lane's quarter)
-    auto issue = [&](int c, uint32_t w0, uint32_t w1, v4i* A, v4i* B, uint4& SQ) {
-        const uint8_t* pa = xa + c * (kMfmaPerBlock * ASTRIDE);
-        if (a_active) {
+        for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(xa + c * BLK + m * ASTRIDE);
 #pragma unroll
-            for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(pa + m * ASTRIDE);
-        }
-        if (T == 1) {
-            const uint2 v = *(const uint2*)(xs + c * 32);
-            SQ.x = v.x;
-            SQ.y = v.y;
-        } else {
-            SQ = *(const uint4*)(xs + c * 64);
-        }
+        for (int t = 0; t < T; t++) sc[t] = xs[c * 8 * T + 2 * t];
+    };
+    auto decode = [&](uint32_t w0, uint32_t w1, v4i* B) {
         B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 1, laneoff)),
                    (int)lds_u32(lb, lut_addr<LR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 3, laneoff))};
-        B[1] = v4i{(int)digit0_word(w0), (int)lds_u32(lb, lut_addr<LR>(w1, 0, laneoff)),
+        B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<LR>(w1, 0, laneoff)),
                    (int)lds_u32(lb, lut_addr<LR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w1, 2, laneoff))};
-        B[2] = v4i{(int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff)), (int)digit0_word(w1), 0, 0};
+        B[2] = v4i{(int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
     };
-    float acc[T];
-#pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = 0.0f;
-    auto finish = [&](uint32_t dbits, const v4i* A, const v4i* B, const uint4& SQ) {
+    int ct = s0 % Tt, cv = s0 / Tt;              // compute cursor: tile, block step
+    uint32_t pofs = (uint32_t)s0 * T * 64;        // item slot offset (bytes)
+    v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
+    // item in ring slot u; `next`: item + 1 is in the run (its operands are read here)
+    auto body = [&](auto uc, bool next) {
+        constexpr int u = decltype(uc)::value;
+        if (next) decode(wl[(u + 1) % D], wh[(u + 1) % D], (u & 1) ? B0 : B1);
+        const v4i* B = (u & 1) ? B1 : B0;
         v4i Dm = {0, 0, 0, 0};
 #pragma unroll
         for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], Dm, 0, 0, 0);
-        const float d = half_bits_to_float(dbits >> 16);
-        const uint32_t sq[4] = {SQ.x, SQ.y, SQ.z, SQ.w};
+        float d = half_bits_to_float(wh[u] >> 16);
+        if (PAD && 4 * cv + kq >= nb) d = 0.0f;
+        float* dst = (float*)(pbase + diag * pofs);
 #pragma unroll
-        for (int t = 0; t < T; t++) {
-            const int v = Dm[2 * t] * 256 + Dm[2 * t + 1] - (int)sq[2 * t + 1];
-            acc[t] += (d * __builtin_bit_cast(float, sq[2 * t])) * (float)v;
+        for (int t = 0; t < T; t++) dst[16 * t] = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[t]);
+        pofs += T * 64;
+        if (++ct == Tt) {
+            ct = 0;
+            ++cv;
+            if (next) load_a(cv);
         }
     };
-
-    // compute cursor: step cc of the current tile, `left` steps of it remain in this run's
-    // view of the tile, cs = tile slot (0 = the run's first tile)
-    int cc = c0, left = nq - c0, cs = 0;
-    auto flush_if_done = [&]() {
-        if (--left == 0) {
-            if (sum_lane) {
-#pragma unroll
-                for (int t = 0; t < T; t++) my_part[(cs * T + t) * 16] = acc[t];
-            }
-#pragma unroll
-            for (int t = 0; t < T; t++) acc[t] = 0.0f;
-            ++cs;
-            left = nq;
-            cc = 0;
-        } else {
-            ++cc;
-        }
-    };
-    if (n > 0) issue(cc, wl[0], wh[0], A0, B0, SQ0);
-    // One loop over passes of the ring: every slot is reloaded after use (also past the
-    // run's end), so the loads do not depend on the branches and their waits stay exact.
-    for (int j = 0; j < n; j += D) {
-#pragma unroll
-        for (int u = 0; u < D; u++) {
-            if (j + u < n) {
-                const int cn = left == 1 ? 0 : cc + 1;
-                if (j + u + 1 < n) {
-                    if (u & 1) issue(cn, wl[(u + 1) % D], wh[(u + 1) % D], A0, B0, SQ0);
-                    else issue(cn, wl[(u + 1) % D], wh[(u + 1) % D], A1, B1, SQ1);
-                }
-                if (u & 1) finish(wh[u], A1, B1, SQ1);
-                else finish(wh[u], A0, B0, SQ0);
-                flush_if_done();
-            }
-            load_next(u);
-        }
+    if (n > 0) {
+        load_a(cv);
+        decode(wl[0], wh[0], B0);
     }
-    if (left != nq) {                            // the run ended inside a tile: store it
-        left = 1;
-        flush_if_done();
+    int j = 0;
+    for (; j + D < n; j += D) {                  // full passes: every item has a successor
+        static_for<D>([&](auto uc) {
+            body(uc, true);
+            load_next(decltype(uc)::value);
+        });
     }
+    static_for<D>([&](auto uc) {                 // the last 1..D items
+        constexpr int u = decltype(uc)::value;
+        if (j + u < n) body(uc, j + u + 1 < n);
+    });
     __syncthreads();
 
-    // tile sums: every wave whose run touches the tile, in wave order, quarters in order
-    for (int o = tid; o < (wt1 - wt0) * 4 * T; o += 1024) {
+    // row sums: output (tile tl, row rr, token t) adds its item slots over c ascending and
+    // quarters ascending, 16 lanes per output (lane sub takes c = sub, sub + 16, ...), then
+    // a fixed-order DPP reduction over the 16 lanes
+    for (int o16 = tid; o16 < Tt * 4 * T * 16; o16 += 1024) {
+        const int o = o16 >> 4, sub = o16 & 15;
         const int tl = o / (4 * T), rr = (o / T) & 3, t = o % T;
         float sum = 0.0f;
+        for (int c = sub; c < nq; c += 16) {
+            const float* p = part + ((c * Tt + tl) * T + t) * 16 + rr;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; w2++) {
-            const int f = run_tiles[w2].x, l = run_tiles[w2].y;
-            if (tl >= f && tl <= l) {
-                const float* p = part + ((size_t)(w2 * slots + tl - f) * T + t) * 16 + rr;
-#pragma unroll
-                for (int q = 0; q < 4; q++) sum += p[4 * q];
-            }
+            for (int q = 0; q < 4; q++) sum += p[4 * q];
         }
+        sum = row16_fsum(sum);
         const int row = (wt0 + tl) * 4 + rr;
-        if (row < N) y[(size_t)t * N + row] = sum;
+        if (sub == 0 && row < N) y[(size_t)t * N + row] = sum;
     }
 }
 
@@ -402,42 +502,19 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ 
 // steps (of 4 blocks) per tile; blocks past K are zero padding
 static int gemv_nq(int K) { return (K / kGroup + 3) / 4; }
 
-XprepLayout xprep_layout(int K, int T) {
-    const size_t nbv = 4 * (size_t)gemv_nq(K);
-    XprepLayout L;
-    L.off_s = 0;
-    L.off_a = ((nbv * T * 8) + 255) & ~(size_t)255;
-    L.bytes = L.off_a + nbv * kAImageBytes * 2 * (size_t)T;
-    return L;
-}
-
-hipError_t launch_gemv_prep(const void* x, int x_dtype, int x_layout, uint8_t* xprep, int K, int T,
-                            hipStream_t s) {
-    const XprepLayout L = xprep_layout(K, T);
-    const int nq = gemv_nq(K);
-    const dim3 grid(4 * nq), block(128);
-    if (T == 1)
-        hipLaunchKernelGGL(k_gemv_prep<1>, grid, block, 0, s, x, x_dtype, x_layout, xprep, K, nq, L.off_a);
-    else
-        hipLaunchKernelGGL(k_gemv_prep<2>, grid, block, 0, s, x, x_dtype, x_layout, xprep, K, nq, L.off_a);
-    return hipGetLastError();
-}
-
 constexpr int kLdsMax = 160 * 1024;
 
-constexpr int kRing = 12;    // weight steps in flight per wave
+// Weight items in flight per wave.  A deeper ring only stalls the wave at load issue once
+// the CU's vector-memory queue is full (16 waves x 4 items x 512 B = 32 KB per CU in
+// flight already keep HBM busy), which delays the prologue and the loop.
+constexpr int kRing = 4;
 
-// tile slots a wave's run can touch when a workgroup owns tpw tiles
-static int gemv_slots(int nq, int tpw) {
-    const int run = (tpw * nq + kWaves - 1) / kWaves;
-    return (run + nq - 1) / nq + 1;
-}
-
-// LDS of a GEMV launch (the static digit table, then the dynamic part): digit table + A image + scales/sums + per-wave tile sums
-static int gemv_lds_bytes(int K, int T, int LR, int slots) {
-    const int nbv = 4 * gemv_nq(K);
-    return gemv_static_lds_bytes(LR) + gemv_a_lds_bytes(gemv_nq(K) * kAImageBytes * 2 * T) + gemv_s_lds_bytes(nbv, T) +
-           kWaves * slots * T * 16 * 4;
+// LDS of a GEMV launch: trit table + A image + scales + the larger of the item sums for
+// tpw tiles and (xbytes > 0) the staged raw activation, whole 1 KB DMA chunks
+static int gemv_lds_bytes(int K, int T, int LR, int tpw, int xbytes) {
+    const int nq = gemv_nq(K);
+    return gemv_static_lds_bytes(LR) + gemv_a_lds_bytes(nq * kAImageBytes * 2 * T) + gemv_s_lds_bytes(4 * nq, T) + 1536 +
+           std::max(nq * tpw * T * 16 * 4, (xbytes + 1023) & ~1023);
 }
 
 static int device_cus() {
@@ -451,12 +528,12 @@ static int device_cus() {
     return n_cu;
 }
 
-template <int T, int LR>
-static hipError_t launch_gemv_cfg(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int tpw,
-                                  hipStream_t s, const XprepLayout& L) {
+template <int T, int LR, bool PAD, bool XS>
+static hipError_t launch_gemv_cfg(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N,
+                                  int tpw, int lds, hipStream_t s) {
     static bool attr_done = false;
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            kLdsMax - gemv_static_lds_bytes(LR));
         if (e != hipSuccess) return e;
@@ -464,39 +541,70 @@ static hipError_t launch_gemv_cfg(const uint8_t* W, const uint8_t* xprep, float*
     }
     const int tiles = (N + 3) / 4, nq = gemv_nq(K);
     const int grid = (tiles + tpw - 1) / tpw;
-    const int slots = gemv_slots(nq, tpw);
-    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing>), dim3(grid), dim3(1024), gemv_lds_bytes(K, T, LR, slots) - gemv_static_lds_bytes(LR), s, W,
-                       xprep, y, K, N, nq, tpw, slots, L.off_a);
+    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS>), dim3(grid), dim3(1024), lds - gemv_static_lds_bytes(LR), s,
+                       W, x, x_dtype, x_layout, y, K, N, nq, tpw);
     return hipGetLastError();
 }
 
-// One workgroup per CU when its tile sums fit in LDS beside the table and activation, else
-// smaller tile ranges (more workgroups).  Table: 64 replicas (one v_perm per lookup) when
-// there is room, else 16.
+template <int T, int LR, bool XS>
+static hipError_t launch_gemv_pad(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N,
+                                  int tpw, int lds, hipStream_t s) {
+    return (K / kGroup) % 4 ? launch_gemv_cfg<T, LR, true, XS>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s)
+                            : launch_gemv_cfg<T, LR, false, XS>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+}
+
+// Configuration choice, first that fits 160 KB of LDS: one workgroup per CU, else smaller
+// tile ranges (more workgroups); the staged activation (XS) before per-thread loads; a
+// 64-replica trit table (one v_perm per lookup) before a 16-replica one.
 template <int T>
-static hipError_t launch_gemv_t(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, hipStream_t s,
-                                const XprepLayout& L) {
-    const int tiles = (N + 3) / 4, nq = gemv_nq(K), cus = device_cus();
+static hipError_t launch_gemv_t(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N,
+                                hipStream_t s) {
+    const int tiles = (N + 3) / 4, cus = device_cus();
+    const int xbytes = T * K * (x_dtype == 1 ? 2 : 4);
+    const bool regs_ok = K <= kChunkMax * 8 * 1024;
     for (int wgs = cus;; wgs *= 2) {
         const int tpw = (tiles + wgs - 1) / wgs;
-        const int slots = gemv_slots(nq, tpw);
-        if (gemv_lds_bytes(K, T, 6, slots) <= kLdsMax) return launch_gemv_cfg<T, 6>(W, xprep, y, K, N, tpw, s, L);
-        if (gemv_lds_bytes(K, T, 4, slots) <= kLdsMax) return launch_gemv_cfg<T, 4>(W, xprep, y, K, N, tpw, s, L);
+        int lds;
+        if ((lds = gemv_lds_bytes(K, T, 6, tpw, xbytes)) <= kLdsMax)
+            return launch_gemv_pad<T, 6, true>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+        if ((lds = gemv_lds_bytes(K, T, 4, tpw, xbytes)) <= kLdsMax)
+            return launch_gemv_pad<T, 4, true>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+        if (regs_ok && (lds = gemv_lds_bytes(K, T, 6, tpw, 0)) <= kLdsMax)
+            return launch_gemv_pad<T, 6, false>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+        if (regs_ok && (lds = gemv_lds_bytes(K, T, 4, tpw, 0)) <= kLdsMax)
+            return launch_gemv_pad<T, 4, false>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
         if (tpw == 1) return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_gemv_ptq1(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int T,
+// Matrices whose byte size does not fit the 32-bit buffer offsets run as row chunks.
+hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                             hipStream_t s) {
-    const XprepLayout L = xprep_layout(K, T);
-    return T == 1 ? launch_gemv_t<1>(W, xprep, y, K, N, s, L) : launch_gemv_t<2>(W, xprep, y, K, N, s, L);
+    const size_t row_bytes = (size_t)(K / kGroup) * kBlockBytes;
+    const int chunk = (int)std::min<size_t>((size_t)N, ((size_t)1 << 31) / row_bytes / 4 * 4);
+    for (int n0 = 0; n0 < N; n0 += chunk) {
+        const int nn = std::min(chunk, N - n0);
+        const uint8_t* Wc = W + (size_t)n0 * row_bytes;
+        float* yc = y + n0;
+        // y is [T][N]: the chunk's rows of token t start at t*N + n0; T = 2 chunks write
+        // through a [2][nn] view only when nn == N
+        if (T == 2 && nn != N) return hipErrorInvalidValue;
+        const hipError_t e = T == 1 ? launch_gemv_t<1>(Wc, x, x_dtype, x_layout, yc, K, nn, s)
+                                    : launch_gemv_t<2>(Wc, x, x_dtype, x_layout, yc, K, nn, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
+// Largest K some configuration fits for fp32 activations (fp16 ones never need more LDS).
 int gemv_max_k(int T) {
-    int K = kGroup;
-    while (gemv_lds_bytes(K + kGroup, T, 4, gemv_slots(gemv_nq(K + kGroup), 1)) <= kLdsMax) K += kGroup;
+    auto fits = [T](int K) {
+        return gemv_lds_bytes(K, T, 4, 1, T * K * 4) <= kLdsMax ||
+               (K <= kChunkMax * 8 * 1024 && gemv_lds_bytes(K, T, 4, 1, 0) <= kLdsMax);
+    };
+    int K = 0;
+    while (fits(K + kGroup)) K += kGroup;
     return K;
 }
-
 
 }  // namespace kata

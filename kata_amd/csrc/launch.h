@@ -7,16 +7,10 @@
 
 namespace kata {
 
-// ---- PTQ1_0 GEMV (gemv_ptq1.hip)
-struct XprepLayout {
-    size_t off_s, off_a, bytes;   // (scale, sum) pairs, A image, total
-};
-XprepLayout xprep_layout(int K, int T);
-hipError_t launch_gemv_prep(const void* x, int x_dtype, int x_layout, uint8_t* xprep, int K, int T,
+// ---- PTQ1_0 GEMV (gemv_ptq1.hip); x 16-byte aligned, rows [T][K] or half2 [K][2] (T = 2)
+hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                             hipStream_t s);
-hipError_t launch_gemv_ptq1(const uint8_t* W, const uint8_t* xprep, float* y, int K, int N, int T,
-                            hipStream_t s);
-int gemv_max_k(int T);   // largest K whose prepared activation fits the GEMV's LDS
+int gemv_max_k(int T);   // largest K the PTQ1_0 GEMV accepts (its activation image lives in LDS)
 
 // ---- Q8_0 GEMV (gemv_q8.hip)
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,

@@ -50,28 +50,6 @@ def gemv_ptq1(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1, half
     return y
 
 
-def xprep_bytes(K: int, T: int) -> int:
-    return int(lib().kata_gemv_ptq1_xprep_bytes(K, T))
-
-
-def gemv_ptq1_prep(x: torch.Tensor, K: int, T: int = 1, half2: bool = False,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
-    _need_gpu(x)
-    nbytes = xprep_bytes(K, T)
-    xp = out if out is not None else torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-    check(lib().kata_gemv_ptq1_prep(_ptr(x), _xdtype(x), KATA_X_HALF2 if half2 else KATA_X_ROWS,
-                                    _ptr(xp), K, T, _stream(x)))
-    return xp
-
-
-def gemv_ptq1_prepped(W: torch.Tensor, xprep: torch.Tensor, K: int, N: int, T: int = 1,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
-    _need_gpu(W, xprep)
-    y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
-    check(lib().kata_gemv_ptq1_prepped(_ptr(W), _ptr(xprep), _ptr(y), K, N, T, _stream(W)))
-    return y
-
-
 def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
             out: torch.Tensor | None = None) -> torch.Tensor:
     _need_gpu(W, x)

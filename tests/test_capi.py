@@ -23,7 +23,7 @@ def header_symbols():
 
 def test_library_exports_every_header_symbol():
     syms = header_symbols()
-    assert len(syms) >= 20
+    assert len(syms) >= 19
     lib = L.lib()
     for s in syms:
         assert hasattr(lib, s), s
@@ -73,13 +73,11 @@ def test_other_entry_points_reject_bad_shapes():
     assert lib.kata_gemm_ptq1_f16(FAKE, 136, FAKE, FAKE, 0, 8, 4, 136, 8, None) == KATA_EINVAL   # K % 128
     assert lib.kata_quant_rows_i8(FAKE, FAKE, FAKE, 4, 128, 2, None) == KATA_EINVAL            # ldS < M
     assert lib.kata_gemm_ptq1_i8(FAKE, FAKE, 4, FAKE, FAKE, 0, 4, 4, 128, 8, None) == KATA_EINVAL  # ldc < N
-    assert lib.kata_gemv_ptq1_prep(FAKE, 0, 0, ctypes.c_void_p(0x10004), 128, 1, None) == KATA_EINVAL  # xprep align
-    assert lib.kata_gemv_ptq1_xprep_bytes(100, 1) == 0
+    assert lib.kata_gemv_ptq1(FAKE, ctypes.c_void_p(0x10008), 1, 0, FAKE, 128, 8, 1, None) == KATA_EINVAL  # x align
     # the 27B shapes (K up to 17408) must fit for both T
     assert lib.kata_gemv_ptq1_max_k(1) >= 17408 and lib.kata_gemv_ptq1_max_k(2) >= 17408
     assert lib.kata_gemv_ptq1_max_k(1) % 128 == 0 and lib.kata_gemv_ptq1_max_k(2) % 128 == 0
     assert lib.kata_gemv_ptq1_max_k(3) == 0
-    assert lib.kata_gemv_ptq1_xprep_bytes(5120, 1) >= 5120 // 128 * (384 + 8)   # A image + scales/sums
 
 
 def test_host_pack_matches_oracle_and_golden(golden):

@@ -67,16 +67,17 @@ def test_half2_layout_matches_rows(dev):
     assert np.array_equal(y_rows, y_ilv)
 
 
-def test_prepped_equals_one_shot(dev):
-    K, N, T = 5120, 256, 2
+def test_t2_rows_equal_t1(dev):
+    """Each token of a T=2 call is quantised and reduced exactly as a T=1 call on it."""
+    K, N = 5120, 256
     W_np, _, _ = orc.synth_ptq1(N, K, 5)
-    x = torch.from_numpy(orc.synth_x(T, K, 6)).to(dev)
+    x = torch.from_numpy(orc.synth_x(2, K, 6)).to(dev)
     W = torch.from_numpy(W_np).to(dev)
-    y1 = ops.gemv_ptq1(W, x, K, N, T)
-    xp = ops.gemv_ptq1_prep(x, K, T)
-    y2 = ops.gemv_ptq1_prepped(W, xp, K, N, T)
-    torch.cuda.synchronize()
-    assert torch.equal(y1, y2)
+    y2 = ops.gemv_ptq1(W, x, K, N, 2)
+    for t in range(2):
+        y1 = ops.gemv_ptq1(W, x[t:t + 1].contiguous(), K, N, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(y1[0], y2[t])
 
 
 def test_special_inputs(dev):
