@@ -55,7 +55,8 @@ int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, f
 int kata_gemv_ptq1_max_k(int T);
 
 /* Q8_0 GEMV for the MTP head: y[t][n] = sum_b d[n,b] * sum_i q[n,b,i] * x[t][32b+i].
- * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16, y [T][N] fp32.
+ * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16 (16-byte aligned), y [T][N] fp32.
+ * W is 2-byte aligned (the block layout's granularity).
  * Replaces the `gq` lambda of Engine::mtpRows (src/engine.cpp:351; k_gemv_q8_t1/_t2,
  * shaders/mtp.metal:5-22). */
 int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,

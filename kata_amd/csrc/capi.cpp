@@ -76,7 +76,7 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
     if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
     if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
     if (!aligned(W, 2)) return fail(KATA_EINVAL, "W must be 2-byte aligned");
-    if (!aligned(x, x_dtype == KATA_F16 ? 2 : 4)) return fail(KATA_EINVAL, "x misaligned");
+    if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
     return check_launch(kata::launch_gemv_q8(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv q8_0");
 }
 

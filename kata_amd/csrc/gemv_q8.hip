@@ -3,11 +3,13 @@
 // Semantics (shaders/mtp.metal:5-20): y[t][n] = sum_b d[n,b] * (sum_i q[n,b,i] * x[t][32b+i]),
 // per block the int8 x activation dot in fp32, then acc += d * s.
 //
-// Design: HBM-bound (1.0625 bytes per weight), so plain VALU fp32 FMAs have ample headroom.
-// Each wave owns 4 rows and walks pairs of blocks (68 bytes, dword aligned whenever the row
-// holds an even number of blocks, i.e. K % 64 == 0): one lane loads a pair as 17 dwords per
-// row and reuses its 64 activations across the 4 rows.  Rows with an odd block count use a
-// per-block kernel with 16-bit loads.
+// Design: HBM-bound (1.0625 bytes per weight); plain VALU fp32 FMAs keep up.  A lane owns
+// whole 34-byte blocks and consecutive lanes own consecutive blocks of a row, so each load
+// instruction of a wave covers 2176 contiguous bytes.  A block is read from its
+// dword-aligned start as two 16-byte loads, one dword and one 16-bit load (blocks sit at
+// 2-byte granularity) and realigned with v_alignbyte.  A wave owns R = 4 rows and one of KS slices of K, and reuses each block's
+// activations (loaded once into registers) for its 4 rows; the KS waves of a workgroup
+// that share rows add their partial sums through LDS in a fixed order (deterministic).
 #include "common.h"
 #include "launch.h"
 
@@ -15,129 +17,155 @@ namespace kata {
 
 namespace {
 
+constexpr int kRowsPerWave = 4;
+
 __device__ inline float byte_s8(uint32_t w, int k) { return (float)(int8_t)(uint8_t)(w >> (8 * k)); }
 
+// 32 activations x[t][32b .. 32b+31] as floats (fp16 or fp32 rows)
 template <int T, bool XH>
-__device__ inline float load_x(const void* x, size_t idx) {
-    if (XH) return (float)((const _Float16*)x)[idx];
-    return ((const float*)x)[idx];
+__device__ inline void load_x32(const void* x, int K, int b, float (&xv)[T][32]) {
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        if (XH) {
+            const uint4* p = (const uint4*)((const _Float16*)x + (size_t)t * K + (size_t)b * 32);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint4 u = p[c];
+                const uint32_t ws[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const v2h hh = __builtin_bit_cast(v2h, ws[h]);
+                    xv[t][c * 8 + 2 * h] = (float)hh[0];
+                    xv[t][c * 8 + 2 * h + 1] = (float)hh[1];
+                }
+            }
+        } else {
+            const float4* p = (const float4*)((const float*)x + (size_t)t * K + (size_t)b * 32);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const float4 u = p[c];
+                xv[t][4 * c] = u.x;
+                xv[t][4 * c + 1] = u.y;
+                xv[t][4 * c + 2] = u.z;
+                xv[t][4 * c + 3] = u.w;
+            }
+        }
+    }
 }
 
-template <int T, bool XH>
-__global__ __launch_bounds__(256) void k_gemv_q8_pair(const uint8_t* __restrict__ W, const void* __restrict__ x,
-                                                      float* __restrict__ y, int K, int N) {
-    constexpr int R = 4;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * 4 + wave) * R;
-    const int nb = K / kQ8Group, np = nb >> 1;
+// Workgroup = 4 waves = (4 / KS) row groups x KS slices of the row's blocks.
+template <int T, bool XH, int KS>
+__global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t* __restrict__ W, uint32_t w_off, uint32_t w_bytes,
+                                                 const void* __restrict__ x, float* __restrict__ y, int K, int N) {
+    constexpr int R = kRowsPerWave;
+    constexpr int GROUPS = 4 / KS;
+    __shared__ float red[4][T][R];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave / KS, ks = wave % KS;
+    const int row0 = (blockIdx.x * GROUPS + grp) * R;
+    const int nb = K / kQ8Group;
+    const int b0 = (ks * nb) / KS, b1 = ((ks + 1) * nb) / KS;
+    const uint32_t row_bytes = (uint32_t)nb * kQ8BlockBytes;
+    // W as a raw buffer from its dword-aligned base (w_off = W & 3); exact bounds
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(W - w_off), 0, (int)w_bytes, 0x00020000);
+
     float acc[T][R];
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
         for (int r = 0; r < R; r++) acc[t][r] = 0.0f;
 
-    for (int p = lane; p < np; p += 64) {
-        float xv[T][64];
-#pragma unroll
-        for (int t = 0; t < T; t++) {
-            if (XH) {
-                const uint4* xp = (const uint4*)((const _Float16*)x + (size_t)t * K + (size_t)p * 64);
-#pragma unroll
-                for (int c = 0; c < 8; c++) {
-                    const uint4 u = xp[c];
-                    const uint32_t ws[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                    for (int h = 0; h < 4; h++) {
-                        xv[t][c * 8 + 2 * h] = half_bits_to_float(ws[h] & 0xffffu);
-                        xv[t][c * 8 + 2 * h + 1] = half_bits_to_float(ws[h] >> 16);
-                    }
-                }
-            } else {
-                const float4* xp = (const float4*)((const float*)x + (size_t)t * K + (size_t)p * 64);
-#pragma unroll
-                for (int c = 0; c < 16; c++) {
-                    const float4 u = xp[c];
-                    xv[t][4 * c] = u.x; xv[t][4 * c + 1] = u.y; xv[t][4 * c + 2] = u.z; xv[t][4 * c + 3] = u.w;
-                }
-            }
-        }
+    // all loads of a block step (4 rows) are issued before its arithmetic
+    for (int b = b0 + lane; b < b1; b += 64) {
+        uint32_t s[R][9];
+        float d[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int row = min(row0 + r, N - 1);
-            const uint32_t* q = (const uint32_t*)(W + ((size_t)row * nb + 2 * (size_t)p) * kQ8BlockBytes);
-            uint32_t wd[17];
+            const uint32_t base = w_off + (uint32_t)row * row_bytes + (uint32_t)b * kQ8BlockBytes;
+            const uint32_t sh = base & 3u, a0 = base - sh;
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)a0, 0, 0));
+            const u32x4 hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(a0 + 16), 0, 0));
+            // block bytes 30..33: the dword at a0 + 32 ends at the block's end when sh = 2
+            // (with sh = 0 it would pass it, and past the matrix for the last block: the
+            // bounds check returns zeros there, and bytes 32..33 come from a 16-bit load)
+            const uint32_t w8 = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)(a0 + 32), 0, 0);
+            const uint32_t h16 = __builtin_amdgcn_raw_buffer_load_b16(rsrc, (int)(base + 32), 0, 0);
+            const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            // stream s[i] = block bytes 4i .. 4i+3: s[0] = {d, d, q0, q1}, s[i] = q(4i-2) ..,
+            // s[8] = {q30, q31}
 #pragma unroll
-            for (int i = 0; i < 17; i++) wd[i] = q[i];
-            // byte at position pb of the 68-byte pair
-#define QB(pb) byte_s8(wd[(pb) >> 2], (pb) & 3)
-            const float d0 = half_bits_to_float(wd[0] & 0xffffu);
-            const float d1 = half_bits_to_float(wd[8] >> 16);
+            for (int i = 0; i < 7; i++) s[r][i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+            s[r][7] = __builtin_amdgcn_alignbyte(w8, w[7], sh);
+            s[r][8] = h16;
+        }
+        float xv[T][32];
+        load_x32<T, XH>(x, K, b, xv);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            d[r] = half_bits_to_float(s[r][0] & 0xffffu);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                float s0 = 0.0f, s1 = 0.0f;
+                float sum = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 32; i++) s0 += QB(2 + i) * xv[t][i];
-#pragma unroll
-                for (int i = 0; i < 32; i++) s1 += QB(36 + i) * xv[t][32 + i];
-                acc[t][r] += d0 * s0;
-                acc[t][r] += d1 * s1;
+                for (int k = 0; k < 32; k++) sum += byte_s8(s[r][(k + 2) >> 2], (k + 2) & 3) * xv[t][k];
+                acc[t][r] += d[r] * sum;
             }
-#undef QB
         }
     }
+    // wave sums (fixed butterfly), then the KS slices in slice order
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float v = acc[t][r];
+#pragma unroll
             for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-            if (lane == 0 && row0 + r < N) y[(size_t)t * N + row0 + r] = v;
+            acc[t][r] = v;
         }
-}
-
-// Rows of an odd number of blocks are only 2-byte aligned: one block per lane, 16-bit loads.
-template <int T, bool XH>
-__global__ __launch_bounds__(256) void k_gemv_q8_block(const uint8_t* __restrict__ W, const void* __restrict__ x,
-                                                       float* __restrict__ y, int K, int N) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * 4 + wave;
-    if (row >= N) return;
-    const int nb = K / kQ8Group;
-    float acc[T];
+    if (KS == 1) {
+        if (lane < T * R) {
+            const int t = lane / R, r = lane % R;
+            float v = 0.0f;
 #pragma unroll
-    for (int t = 0; t < T; t++) acc[t] = 0.0f;
-    for (int b = lane; b < nb; b += 64) {
-        const uint16_t* q = (const uint16_t*)(W + ((size_t)row * nb + b) * kQ8BlockBytes);
-        const float d = half_bits_to_float(q[0]);
-        float s[T];
+            for (int tt = 0; tt < T; tt++)
 #pragma unroll
-        for (int t = 0; t < T; t++) s[t] = 0.0f;
-        for (int i = 0; i < 16; i++) {
-            const uint32_t w = q[1 + i];
-#pragma unroll
-            for (int t = 0; t < T; t++) {
-                s[t] += byte_s8(w, 0) * load_x<T, XH>(x, (size_t)t * K + 32 * (size_t)b + 2 * i);
-                s[t] += byte_s8(w, 1) * load_x<T, XH>(x, (size_t)t * K + 32 * (size_t)b + 2 * i + 1);
-            }
+                for (int rr = 0; rr < R; rr++)
+                    if (tt == t && rr == r) v = acc[tt][rr];
+            if (row0 + r < N) y[(size_t)t * N + row0 + r] = v;
         }
-#pragma unroll
-        for (int t = 0; t < T; t++) acc[t] += d * s[t];
+        return;
     }
+    if (lane == 0) {
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-        float v = acc[t];
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-        if (lane == 0) y[(size_t)t * N + row] = v;
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int r = 0; r < R; r++) red[wave][t][r] = acc[t][r];
+    }
+    __syncthreads();
+    if (ks == 0 && lane < T * R) {
+        const int t = lane / R, r = lane % R;
+        float v = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < KS; k2++) v += red[wave + k2][t][r];
+        if (row0 + r < N) y[(size_t)t * N + row0 + r] = v;
     }
 }
 
 template <int T, bool XH>
 hipError_t launch_q8_t(const uint8_t* W, const void* x, float* y, int K, int N, hipStream_t s) {
     const int nb = K / kQ8Group;
-    if ((nb & 1) == 0 && (((uintptr_t)W) & 3) == 0)
-        hipLaunchKernelGGL((k_gemv_q8_pair<T, XH>), dim3((N + 15) / 16), dim3(256), 0, s, W, x, y, K, N);
-    else
-        hipLaunchKernelGGL((k_gemv_q8_block<T, XH>), dim3((N + 3) / 4), dim3(256), 0, s, W, x, y, K, N);
+    const uint32_t w_off = (uint32_t)((uintptr_t)W & 3);
+    const uint32_t w_bytes = w_off + (uint32_t)N * (uint32_t)nb * kQ8BlockBytes;
+    const int groups = (N + kRowsPerWave - 1) / kRowsPerWave;
+    // long rows: four waves share a row group (one K slice each); short rows: one each
+    if (nb >= 256) {
+        hipLaunchKernelGGL((k_gemv_q8<T, XH, 4>), dim3(groups), dim3(256), 0, s, W, w_off, w_bytes, x, y, K, N);
+    } else {
+        hipLaunchKernelGGL((k_gemv_q8<T, XH, 1>), dim3((groups + 3) / 4), dim3(256), 0, s, W, w_off, w_bytes, x, y, K,
+                           N);
+    }
     return hipGetLastError();
 }
 
@@ -145,6 +173,7 @@ hipError_t launch_q8_t(const uint8_t* W, const void* x, float* y, int K, int N, 
 
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                           hipStream_t s) {
+    if ((size_t)N * (size_t)(K / kQ8Group) * kQ8BlockBytes + 4 > 0x7fffffffu) return hipErrorInvalidValue;
     if (T == 1) return x_dtype == 1 ? launch_q8_t<1, true>(W, x, y, K, N, s) : launch_q8_t<1, false>(W, x, y, K, N, s);
     return x_dtype == 1 ? launch_q8_t<2, true>(W, x, y, K, N, s) : launch_q8_t<2, false>(W, x, y, K, N, s);
 }

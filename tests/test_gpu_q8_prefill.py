@@ -37,6 +37,20 @@ def test_q8_random(dev, K, N, T, dtype):
     assert rel_l2(y, ref).max() < 1e-5
 
 
+@pytest.mark.parametrize("K,N,T", [(64, 5, 1), (8192, 9, 2), (96, 3, 1)])
+def test_q8_unaligned_weight_base(dev, K, N, T):
+    """Weights at a 2-byte (not 4-byte) aligned address: every block changes alignment."""
+    W_np, _, _ = orc.synth_q8(N, K, 7 * K + N)
+    buf = torch.zeros(W_np.size + 16, dtype=torch.uint8, device=dev)
+    W = buf[2:2 + W_np.size]
+    W.copy_(torch.from_numpy(W_np.reshape(-1)))
+    assert W.data_ptr() % 4 == 2
+    x_np = orc.synth_x(T, K, K + 3, np.float16)
+    y = ops.gemv_q8(W, torch.from_numpy(x_np).to(dev), K, N, T).cpu().numpy()
+    ref = orc.gemv_q8(W_np, x_np.astype(np.float32), K, N, T)
+    assert rel_l2(y, ref).max() < 1e-5
+
+
 # ----------------------------------------------------------------------------- expansions
 def test_expand_bit_exact(dev, golden):
     K, N = int(golden["ptq1_K"]), int(golden["ptq1_N"])
