@@ -6,8 +6,10 @@
 Workload (the batch-1 decode sweep): one step is the T=1 decode
 GEMV of every ternary matrix of one layer of each kind at the 27B shapes —
 GDN qkv 5120->10240, z 5120->6144, ssm_out 6144->5120; GQA q 5120->12288, k/v 5120->1024,
-o 6144->5120; FFN gate/up 5120->17408, down 17408->5120 — one kernel launch each (the
-activation is quantised inside the GEMV kernel).  Weights are seeded
+o 6144->5120; FFN gate/up 5120->17408, down 17408->5120.  The matrices that multiply the
+same input run as one launch (kata_gemv_ptq1_batch: qkv+z, q+k+v, gate+up; ssm_out, o and
+down alone), 6 launches per step; the activation is quantised inside the GEMV kernel.
+Weights are seeded
 synthetic PTQ1_0 (trits iid on {-1,0,1}, fp16 scales |N(0,0.02)|), activations fp16
 N(0,1).  Steps rotate over enough distinct weight copies (>= 512 MB) that no matrix is
 served from the 256 MB Infinity Cache.  `value` = packed weight bytes of all GEMVs of the
@@ -17,7 +19,8 @@ Also reported (same JSON line):
   roofline     dominant kernel k_gemv_ptq1<1>: algorithmic bytes per launch (the packed
                weight bytes, averaged over the sweep's matrices) / its average launch
                duration, vs 8 TB/s HBM;
-  per_matrix   GB/s of each matrix kind alone (200 repeats over rotating copies);
+  per_matrix   GB/s of each matrix kind alone (200 repeats over rotating copies, replayed
+               from one HIP graph so that the host's launch cost is not what is timed);
   verify_t2    config 3: the T=2 verify GEMV on the FFN and attention shapes;
   q8_0_t1      config 3: the Q8_0 MTP-head GEMV, 17408x5120 and 5120x17408;
   prefill_gemm pp512 exact fp16 GEMM TFLOPS (M=512, 5120->17408 and 17408->5120),
@@ -126,7 +129,18 @@ def main():
                                    .astype(np.float16)).to(dev)
     ys = [torch.empty((1, N), dtype=torch.float32, device=dev) for _, _, N, _ in SWEEP]
 
+    groups = {}
+    for j, (name, K, N, grp) in enumerate(SWEEP):
+        groups.setdefault(grp, []).append(j)
+    group_list = [(grp, idx, SWEEP[idx[0]][1]) for grp, idx in groups.items()]
+
     def step(i):
+        ws = copies[i % ncopies]
+        for grp, idx, K in group_list:
+            ops.gemv_ptq1_batch([ws[j] for j in idx], xs[grp], K, [SWEEP[j][2] for j in idx], 1,
+                                outs=[ys[j] for j in idx])
+
+    def step_single(i):
         ws = copies[i % ncopies]
         for j, (name, K, N, grp) in enumerate(SWEEP):
             ops.gemv_ptq1(ws[j], xs[grp], K, N, 1, out=ys[j])
@@ -136,7 +150,7 @@ def main():
     use_graph = args.graph
     cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
     runners = {}
-    for fname, fn in (("step", step),):
+    for fname, fn in (("step", step), ("single", step_single)):
         for i in range(2):
             fn(i)                                 # first calls set kernel attributes
         torch.cuda.synchronize()
@@ -169,34 +183,36 @@ def main():
     ms_step = ms_total / args.steps
     value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
 
-    # ---- dominant kernel: a step is nothing but its 10 GEMV launches
-    gemv_launch_us = ms_total * 1e3 / (args.steps * len(SWEEP))
-    bytes_per_launch = set_bytes / len(SWEEP)
+    # ---- dominant kernel: a step is nothing but its GEMV launches
+    launches = len(group_list)
+    gemv_launch_us = ms_total * 1e3 / (args.steps * launches)
+    ms_single = timed("single", args.steps)
+    bytes_per_launch = set_bytes / launches
     achieved = bytes_per_launch / (gemv_launch_us * 1e-6) / 1e9
 
     # ---- per matrix kind (config 2: 200 repeats each over rotating copies)
     per_matrix = {}
     def time_reps(fn, nrep):
+        """us per call of fn(r), r = 0..nrep-1, captured once into a graph and replayed: the
+        host's per-launch cost (a Python call each) stays out of the timed region."""
         for r in range(3):
             fn(r)
         torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap_stream):
+            for r in range(nrep):
+                fn(r)
+        g.replay()
+        torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        for r in range(nrep):
-            fn(r)
+        g.replay()
         b.record(stream)
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1e3 / nrep
 
     for j, (name, K, N, grp) in enumerate(SWEEP):
-        nrep = args.reps
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for r in range(nrep):
-            ops.gemv_ptq1(copies[r % ncopies][j], xs[grp], K, N, 1, out=ys[j])
-        b.record(stream)
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / nrep
+        us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], xs[grp], K, N, 1, out=ys[j]), args.reps)
         per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
                             "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
 
@@ -285,12 +301,14 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded trits/scales/activations)",
         "config": {"workload": "BASELINE configs[1]: bs=1 decode GEMV sweep, one layer of each kind "
-                               "(10 matrices, one GEMV launch each)",
+                               "(10 matrices in 6 launches, matrices sharing an input batched)",
                    "weight_copies": ncopies, "bytes_per_step": set_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_ptq1<1>", "avg_launch_us": round(gemv_launch_us, 3),
                      "bytes_per_launch": bytes_per_launch},
+        "one_launch_per_matrix": {"ms_per_step": round(ms_single / args.steps, 5),
+                                  "GBps": round(set_bytes * args.steps / (ms_single * 1e-3) / 1e9, 1)},
         "per_matrix": per_matrix,
         "verify_t2": verify_t2,
         "q8_0_t1": q8,

@@ -54,6 +54,16 @@ int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, f
 /* Largest K the PTQ1_0 GEMV accepts for T tokens (its activation image lives in LDS). */
 int kata_gemv_ptq1_max_k(int T);
 
+/* The same GEMV for 1..4 matrices that multiply one activation (same K), in one launch:
+ * y[i][t][n] for W[i] with N[i] rows.  W, y and N are HOST arrays of count device
+ * pointers / row counts.  The activation is read and quantised once per launch instead
+ * of once per matrix.  No counterpart function in the reference, which issues one
+ * dGemvPtq1 per matrix; this batches the calls of Engine::step that share an input —
+ * qkv + z, q + k + v, gate + up (src/engine.cpp:150-191) — and the matching `gv` calls of
+ * verify2 (src/engine.cpp:458-492). */
+int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, const int* N,
+                         const void* x, int x_dtype, int x_layout, int K, int T, void* stream);
+
 /* Q8_0 GEMV for the MTP head: y[t][n] = sum_b d[n,b] * sum_i q[n,b,i] * x[t][32b+i].
  * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16 (16-byte aligned), y [T][N] fp32.
  * W is 2-byte aligned (the block layout's granularity).

@@ -36,6 +36,7 @@ SIGNATURES = {
     "kata_version": (ctypes.c_char_p, []),
     "kata_gemv_ptq1": (I, [P, P, I, I, P, I, I, I, P]),
     "kata_gemv_ptq1_max_k": (I, [I]),
+    "kata_gemv_ptq1_batch": (I, [I, P, P, P, P, I, I, I, I, P]),
     "kata_gemv_q8_0": (I, [P, P, I, P, I, I, I, P]),
     "kata_gemm_ptq1_f16": (I, [P, I, P, P, I, I, I, I, I, P]),
     "kata_quant_rows_i8": (I, [P, P, P, I, I, I, P]),

@@ -68,6 +68,18 @@ int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, f
                         "gemv ptq1");
 }
 
+int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x, int x_dtype,
+                         int x_layout, int K, int T, void* stream) {
+    if (count < 1 || count > kata::gemv_max_mats()) return fail(KATA_EINVAL, "count=%d must be 1..%d", count, kata::gemv_max_mats());
+    if (!W || !y || !N) return fail(KATA_EINVAL, "null array argument");
+    for (int i = 0; i < count; i++) {
+        int rc = check_gemv_args(W[i], x, x_dtype, x_layout, y[i], K, N[i], T);
+        if (rc) return rc;
+    }
+    return check_launch(kata::launch_gemv_ptq1_multi(count, W, y, N, x, x_dtype, x_layout, K, T, (hipStream_t)stream),
+                        "gemv ptq1 batch");
+}
+
 // ------------------------------------------------------------------ Q8_0 GEMV
 int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, void* stream) {
     if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");

@@ -39,6 +39,20 @@ constexpr int kMfmaPerBlock = 3;
 constexpr int kAImageBytes = kMfmaPerBlock * 4 * 16;   // per block and A row (token, limb)
 constexpr int kWaves = 16;
 constexpr int kChunkMax = 3;   // 8-element activation chunks per thread: K <= 3 * 8 * 1024
+constexpr int kMaxMats = 4;    // matrices sharing one activation in one launch
+
+// The matrices of one launch (same K, same activation): matrix i is W[i] (N[i] rows), its
+// output rows go to y[i][t * ldy[i] + row], and workgroups [wg0[i], wg0[i+1]) serve it with
+// tpw[i] tiles of 4 rows each.
+struct GemvMats {
+    const uint8_t* W[kMaxMats];
+    float* y[kMaxMats];
+    int N[kMaxMats];
+    int tpw[kMaxMats];
+    int ldy[kMaxMats];
+    int wg0[kMaxMats + 1];
+    int count;
+};
 
 // A block is read as four 8-byte segments starting at bytes 20, 0, 8, 16 (segment 3 uses
 // only bytes 16..19; bytes 20..23 belong to segment 0).  Segment 0 carries the scale.
@@ -242,16 +256,16 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
 }
 
 // Work split ("activation-stationary").  One 1024-thread workgroup (16 waves) per CU owns
-// the contiguous tile range [wt0, wt0 + Tt) (4 rows per tile).  Its work items (c, tile) —
-// 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered c-major,
-// s = c * Tt + tile, and cut into 16 equal contiguous runs, one per wave, so a wave keeps
-// the A operand of one block step c in registers across many tiles and reloads it from
-// LDS only when c changes.  Lane x + 16*g: B column x = (row r = x & 3, block 4c + kq with
-// kq = x >> 2), A row x = (block 4c + (x >> 2), token (x >> 1) & 1, limb x & 1); result
-// rows 4g..4g+3 belong to block 4c + g, so lane 20*q + r holds row r's sum over block
-// 4c + q.  Those 16 lanes store their scaled sums to the item's LDS slot (the other lanes
-// store to a scratch slot: no exec-mask changes in the loop); at the end each output row
-// adds its nq * 4 slots in a fixed order (deterministic, no atomics).
+// the contiguous tile range [wt0, wt0 + Tt) (4 rows per tile) of one matrix.  Its work
+// items (c, tile) — 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered
+// c-major, s = c * Tt + tile, and cut into 16 equal contiguous runs, one per wave, so a wave
+// keeps the A operand of one block step c in registers across many tiles and reloads it
+// from LDS only when c changes.  Lane x + 16*g: B column x = (row r = x & 3, block 4c + kq
+// with kq = x >> 2), A row x = (block 4c + (x >> 2), token (x >> 1) & 1, limb x & 1);
+// result rows 4g..4g+3 belong to block 4c + g, so lane 20*q + r holds row r's sum over
+// block 4c + q.  Those 16 lanes store their scaled sums to the item's LDS slot (the other
+// lanes store to a scratch slot: no exec-mask changes in the loop); at the end each
+// output row adds its nq * 4 slots in a fixed order (deterministic, no atomics).
 //
 // Timeline.  (1) Wave 0 (the first wave of the workgroup to launch) copies the scatter
 // offsets and (XS) the raw activation into LDS by DMA before any weight load is queued on
@@ -265,10 +279,9 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
 // Dynamic LDS: A image (384*T B per virtual block, quarters 64 B apart), (scale, 0)
 // pairs [vb][t], the scatter offsets (1 KB), a scratch slot for the off-diagonal lanes
 // (512 B), then item sums [S][T][16] floats, which with XS first hold the raw activation.
-template <int T, int LR, int D, bool PAD, bool XS>
-__global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ W, const void* __restrict__ x,
-                                                    int x_dtype, int x_layout, float* __restrict__ y, int K, int N,
-                                                    int nq, int tpw) {
+template <int T, int LR, int D, bool PAD, bool XS, bool MULTI>
+__global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __restrict__ x, int x_dtype, int x_layout,
+                                                    int K, int nq) {
     static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by item parity");
     constexpr int ASTRIDE = 4 * 2 * T * 16;      // A image bytes per (virtual block, MFMA)
     constexpr int BLK = kMfmaPerBlock * ASTRIDE;  // A image bytes per virtual block
@@ -281,8 +294,41 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ 
     const int x_ = lane & 15, g = lane >> 4;
     const int r = x_ & 3, kq = x_ >> 2;
     const int nb = K >> 7, nbv = 4 * nq;
+    // this workgroup's matrix (workgroups [wg0[i], wg0[i+1]) serve matrix i) and tile range
+    // One matrix (MULTI false): only entry 0 is read, the kernel arguments span one cache
+    // line less.  Several: every field is read before any is selected (the empty asm takes
+    // them all as inputs); otherwise the compiler turns the selection into branches around
+    // dependent argument loads, a chain of memory latencies at kernel start.
+    const uint8_t* __restrict__ W = P.W[0];
+    float* __restrict__ y = P.y[0];
+    int N = P.N[0], tpw = P.tpw[0], ldy = P.ldy[0], wg0 = 0;
+    if constexpr (MULTI) {
+        const uint8_t* Wv[kMaxMats] = {P.W[0], P.W[1], P.W[2], P.W[3]};
+        float* yv[kMaxMats] = {P.y[0], P.y[1], P.y[2], P.y[3]};
+        int Nv[kMaxMats] = {P.N[0], P.N[1], P.N[2], P.N[3]};
+        int tv[kMaxMats] = {P.tpw[0], P.tpw[1], P.tpw[2], P.tpw[3]};
+        int lv[kMaxMats] = {P.ldy[0], P.ldy[1], P.ldy[2], P.ldy[3]};
+        int gv[kMaxMats] = {P.wg0[0], P.wg0[1], P.wg0[2], P.wg0[3]};
+        const int cnt = P.count;
+        asm volatile("" ::"s"(Wv[0]), "s"(Wv[1]), "s"(Wv[2]), "s"(Wv[3]), "s"(yv[0]), "s"(yv[1]), "s"(yv[2]), "s"(yv[3]));
+        asm volatile("" ::"s"(Nv[0]), "s"(Nv[1]), "s"(Nv[2]), "s"(Nv[3]), "s"(tv[0]), "s"(tv[1]), "s"(tv[2]), "s"(tv[3]));
+        asm volatile("" ::"s"(lv[0]), "s"(lv[1]), "s"(lv[2]), "s"(lv[3]), "s"(gv[1]), "s"(gv[2]), "s"(gv[3]), "s"(cnt));
+        int mi = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxMats; i++) mi = (i < cnt && (int)blockIdx.x >= gv[i]) ? i : mi;
+        wg0 = gv[0];
+#pragma unroll
+        for (int i = 1; i < kMaxMats; i++) {
+            W = mi == i ? Wv[i] : W;
+            y = mi == i ? yv[i] : y;
+            N = mi == i ? Nv[i] : N;
+            tpw = mi == i ? tv[i] : tpw;
+            ldy = mi == i ? lv[i] : ldy;
+            wg0 = mi == i ? gv[i] : wg0;
+        }
+    }
     const int tiles = (N + 3) >> 2;
-    const int wt0 = blockIdx.x * tpw;
+    const int wt0 = ((int)blockIdx.x - wg0) * tpw;
     const int Tt = min(tiles, wt0 + tpw) - wt0;
     const int S = nq * Tt;
     const int s0 = (wave * S) / kWaves, s1 = ((wave + 1) * S) / kWaves;
@@ -493,7 +539,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(const uint8_t* __restrict__ 
         }
         sum = row16_fsum(sum);
         const int row = (wt0 + tl) * 4 + rr;
-        if (sub == 0 && row < N) y[(size_t)t * N + row] = sum;
+        if (sub == 0 && row < N) y[(size_t)t * ldy + row] = sum;
     }
 }
 
@@ -528,73 +574,98 @@ static int device_cus() {
     return n_cu;
 }
 
-template <int T, int LR, bool PAD, bool XS>
-static hipError_t launch_gemv_cfg(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N,
-                                  int tpw, int lds, hipStream_t s) {
+template <int T, int LR, bool PAD, bool XS, bool MULTI>
+static hipError_t launch_gemv_cfg(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
+                                  hipStream_t s) {
     static bool attr_done = false;
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            kLdsMax - gemv_static_lds_bytes(LR));
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    const int tiles = (N + 3) / 4, nq = gemv_nq(K);
-    const int grid = (tiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS>), dim3(grid), dim3(1024), lds - gemv_static_lds_bytes(LR), s,
-                       W, x, x_dtype, x_layout, y, K, N, nq, tpw);
+    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI>), dim3(P.wg0[P.count]), dim3(1024),
+                       lds - gemv_static_lds_bytes(LR), s, P, x, x_dtype, x_layout, K, gemv_nq(K));
     return hipGetLastError();
 }
 
 template <int T, int LR, bool XS>
-static hipError_t launch_gemv_pad(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N,
-                                  int tpw, int lds, hipStream_t s) {
-    return (K / kGroup) % 4 ? launch_gemv_cfg<T, LR, true, XS>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s)
-                            : launch_gemv_cfg<T, LR, false, XS>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+static hipError_t launch_gemv_pad(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
+                                  hipStream_t s) {
+    if (P.count > 1)
+        return (K / kGroup) % 4 ? launch_gemv_cfg<T, LR, true, XS, true>(P, x, x_dtype, x_layout, K, lds, s)
+                                : launch_gemv_cfg<T, LR, false, XS, true>(P, x, x_dtype, x_layout, K, lds, s);
+    return (K / kGroup) % 4 ? launch_gemv_cfg<T, LR, true, XS, false>(P, x, x_dtype, x_layout, K, lds, s)
+                            : launch_gemv_cfg<T, LR, false, XS, false>(P, x, x_dtype, x_layout, K, lds, s);
 }
 
-// Configuration choice, first that fits 160 KB of LDS: one workgroup per CU, else smaller
-// tile ranges (more workgroups); the staged activation (XS) before per-thread loads; a
-// 64-replica trit table (one v_perm per lookup) before a 16-replica one.
+// Split `wgs` workgroups over the matrices in proportion to their tiles (at least one
+// each); returns the largest tiles-per-workgroup.
+static int gemv_split(GemvMats& P, int wgs) {
+    int total = 0, tmax = 0;
+    for (int i = 0; i < P.count; i++) total += (P.N[i] + 3) / 4;
+    P.wg0[0] = 0;
+    for (int i = 0; i < P.count; i++) {
+        const int tiles = (P.N[i] + 3) / 4;
+        const int w = std::max(1, (int)(((long long)tiles * wgs + total - 1) / total));
+        P.tpw[i] = (tiles + w - 1) / w;
+        P.wg0[i + 1] = P.wg0[i] + (tiles + P.tpw[i] - 1) / P.tpw[i];
+        tmax = std::max(tmax, P.tpw[i]);
+    }
+    for (int i = P.count; i < kMaxMats; i++) P.wg0[i + 1] = P.wg0[P.count];
+    return tmax;
+}
+
+// Configuration choice, first that fits 160 KB of LDS: about one workgroup per CU, else
+// smaller tile ranges (more workgroups); the staged activation (XS) before per-thread
+// loads; a 64-replica trit table (one v_perm per lookup) before a 16-replica one.
 template <int T>
-static hipError_t launch_gemv_t(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N,
-                                hipStream_t s) {
-    const int tiles = (N + 3) / 4, cus = device_cus();
+static hipError_t launch_gemv_t(GemvMats& P, const void* x, int x_dtype, int x_layout, int K, hipStream_t s) {
+    const int cus = device_cus();
     const int xbytes = T * K * (x_dtype == 1 ? 2 : 4);
     const bool regs_ok = K <= kChunkMax * 8 * 1024;
     for (int wgs = cus;; wgs *= 2) {
-        const int tpw = (tiles + wgs - 1) / wgs;
+        const int tpw = gemv_split(P, wgs);
         int lds;
         if ((lds = gemv_lds_bytes(K, T, 6, tpw, xbytes)) <= kLdsMax)
-            return launch_gemv_pad<T, 6, true>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+            return launch_gemv_pad<T, 6, true>(P, x, x_dtype, x_layout, K, lds, s);
         if ((lds = gemv_lds_bytes(K, T, 4, tpw, xbytes)) <= kLdsMax)
-            return launch_gemv_pad<T, 4, true>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+            return launch_gemv_pad<T, 4, true>(P, x, x_dtype, x_layout, K, lds, s);
         if (regs_ok && (lds = gemv_lds_bytes(K, T, 6, tpw, 0)) <= kLdsMax)
-            return launch_gemv_pad<T, 6, false>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+            return launch_gemv_pad<T, 6, false>(P, x, x_dtype, x_layout, K, lds, s);
         if (regs_ok && (lds = gemv_lds_bytes(K, T, 4, tpw, 0)) <= kLdsMax)
-            return launch_gemv_pad<T, 4, false>(W, x, x_dtype, x_layout, y, K, N, tpw, lds, s);
+            return launch_gemv_pad<T, 4, false>(P, x, x_dtype, x_layout, K, lds, s);
         if (tpw == 1) return hipErrorInvalidValue;
     }
 }
 
-// Matrices whose byte size does not fit the 32-bit buffer offsets run as row chunks.
+// count matrices of N[i] rows sharing x, one launch.  A matrix whose byte size does not fit
+// the 32-bit buffer offsets is split into row chunks (separate entries).
+hipError_t launch_gemv_ptq1_multi(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                  int x_dtype, int x_layout, int K, int T, hipStream_t s) {
+    const size_t row_bytes = (size_t)(K / kGroup) * kBlockBytes;
+    const int chunk = (int)std::min<size_t>((size_t)1 << 30, ((size_t)1 << 31) / row_bytes / 4 * 4);
+    GemvMats P{};
+    for (int i = 0; i < count; i++) {
+        for (int n0 = 0; n0 < N[i]; n0 += chunk) {
+            if (P.count == kMaxMats) return hipErrorInvalidValue;
+            P.W[P.count] = W[i] + (size_t)n0 * row_bytes;
+            P.y[P.count] = y[i] + n0;
+            P.N[P.count] = std::min(chunk, N[i] - n0);
+            P.ldy[P.count] = N[i];
+            ++P.count;
+        }
+    }
+    return T == 1 ? launch_gemv_t<1>(P, x, x_dtype, x_layout, K, s) : launch_gemv_t<2>(P, x, x_dtype, x_layout, K, s);
+}
+
 hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                             hipStream_t s) {
-    const size_t row_bytes = (size_t)(K / kGroup) * kBlockBytes;
-    const int chunk = (int)std::min<size_t>((size_t)N, ((size_t)1 << 31) / row_bytes / 4 * 4);
-    for (int n0 = 0; n0 < N; n0 += chunk) {
-        const int nn = std::min(chunk, N - n0);
-        const uint8_t* Wc = W + (size_t)n0 * row_bytes;
-        float* yc = y + n0;
-        // y is [T][N]: the chunk's rows of token t start at t*N + n0; T = 2 chunks write
-        // through a [2][nn] view only when nn == N
-        if (T == 2 && nn != N) return hipErrorInvalidValue;
-        const hipError_t e = T == 1 ? launch_gemv_t<1>(Wc, x, x_dtype, x_layout, yc, K, nn, s)
-                                    : launch_gemv_t<2>(Wc, x, x_dtype, x_layout, yc, K, nn, s);
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
+    return launch_gemv_ptq1_multi(1, &W, &y, &N, x, x_dtype, x_layout, K, T, s);
 }
+
+int gemv_max_mats() { return kMaxMats; }
 
 // Largest K some configuration fits for fp32 activations (fp16 ones never need more LDS).
 int gemv_max_k(int T) {

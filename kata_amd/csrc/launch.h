@@ -10,7 +10,10 @@ namespace kata {
 // ---- PTQ1_0 GEMV (gemv_ptq1.hip); x 16-byte aligned, rows [T][K] or half2 [K][2] (T = 2)
 hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                             hipStream_t s);
+hipError_t launch_gemv_ptq1_multi(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                  int x_dtype, int x_layout, int K, int T, hipStream_t s);
 int gemv_max_k(int T);   // largest K the PTQ1_0 GEMV accepts (its activation image lives in LDS)
+int gemv_max_mats();     // most matrices one launch takes
 
 // ---- Q8_0 GEMV (gemv_q8.hip)
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,

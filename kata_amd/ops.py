@@ -50,6 +50,19 @@ def gemv_ptq1(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1, half
     return y
 
 
+def gemv_ptq1_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, half2: bool = False, outs=None):
+    """PTQ1_0 GEMVs of up to 4 matrices sharing the activation x, one launch: returns [y_i]."""
+    _need_gpu(x, *Ws)
+    n = len(Ws)
+    ys = outs if outs is not None else [torch.empty((T, N), dtype=torch.float32, device=x.device) for N in Ns]
+    Wa = (ctypes.c_void_p * n)(*[W.data_ptr() for W in Ws])
+    ya = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    Na = (ctypes.c_int * n)(*Ns)
+    check(lib().kata_gemv_ptq1_batch(n, Wa, ya, Na, _ptr(x), _xdtype(x), KATA_X_HALF2 if half2 else KATA_X_ROWS,
+                                     K, T, _stream(x)))
+    return ys
+
+
 def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
             out: torch.Tensor | None = None) -> torch.Tensor:
     _need_gpu(W, x)

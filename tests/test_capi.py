@@ -68,6 +68,12 @@ def test_other_entry_points_reject_bad_shapes():
     lib = L.lib()
     assert lib.kata_gemv_ptq1(None, FAKE, 0, 0, FAKE, 128, 8, 1, None) == KATA_EINVAL
     assert lib.kata_gemv_q8_0(FAKE, FAKE, 0, FAKE, 48, 8, 1, None) == KATA_EINVAL
+    Wa = (ctypes.c_void_p * 5)(*([0x10000] * 5))
+    Na = (ctypes.c_int * 5)(*([8] * 5))
+    for count in (0, 5):                                   # 1..4 matrices per launch
+        assert lib.kata_gemv_ptq1_batch(count, Wa, Wa, Na, FAKE, 0, 0, 128, 1, None) == KATA_EINVAL
+    Na[1] = 0                                              # every N must be positive
+    assert lib.kata_gemv_ptq1_batch(2, Wa, Wa, Na, FAKE, 0, 0, 128, 1, None) == KATA_EINVAL
     assert lib.kata_gemm_ptq1_f16(FAKE, 120, FAKE, FAKE, 0, 8, 4, 128, 8, None) == KATA_EINVAL   # lda < K
     assert lib.kata_gemm_ptq1_f16(FAKE, 128, FAKE, FAKE, 0, 4, 4, 128, 8, None) == KATA_EINVAL   # ldc < N
     assert lib.kata_gemm_ptq1_f16(FAKE, 136, FAKE, FAKE, 0, 8, 4, 136, 8, None) == KATA_EINVAL   # K % 128

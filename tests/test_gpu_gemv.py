@@ -117,3 +117,22 @@ def test_full_shape_17408x5120(dev):
         sub = np.ascontiguousarray(W_np[rows])
         ref_o = orc.gemv_ptq1(sub, x_np[:T].astype(np.float32), K, len(rows), T)
         assert rel_l2(y.cpu().numpy()[:, rows], ref_o).max() < TIGHT
+
+
+@pytest.mark.parametrize("K,Ns,T,half2", [
+    (5120, (96, 8, 8), 1, False), (6144, (40, 13), 2, True), (1024, (5, 64, 3, 17), 2, False),
+    (17408, (20,), 1, False),
+])
+def test_batch_equals_single_calls(dev, K, Ns, T, half2):
+    """One launch over several matrices sharing x gives exactly the per-matrix results."""
+    Ws_np = [orc.synth_ptq1(N, K, 100 + i)[0] for i, N in enumerate(Ns)]
+    x_np = orc.synth_x(T, K, 99)
+    x = torch.from_numpy(np.ascontiguousarray(x_np.T) if half2 else x_np).to(dev)
+    Ws = [torch.from_numpy(w).to(dev) for w in Ws_np]
+    ys = ops.gemv_ptq1_batch(Ws, x, K, list(Ns), T, half2=half2)
+    for W, W_np, N, yb in zip(Ws, Ws_np, Ns, ys):
+        y1 = ops.gemv_ptq1(W, x, K, N, T, half2=half2)
+        torch.cuda.synchronize()
+        assert torch.equal(yb, y1)
+        ref = orc.gemv_ptq1(W_np, x_np.astype(np.float32), K, N, T)
+        assert rel_l2(yb.cpu().numpy(), ref).max() < TIGHT
