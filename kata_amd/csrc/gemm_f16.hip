@@ -6,25 +6,30 @@
 // summation order differs (tolerance-based parity).
 //
 // Design (MI355X-first; the reference expands every matrix to a 178 MB fp16 stage first):
-//  * A workgroup (4 waves) computes a 128 x 16U tile of C, U = 1..18 column units of 16
-//    chosen per problem so the grid is close to a multiple of the CU count (pp512 gate/up:
-//    128 x 272 -> exactly 256 tiles).  Wave (wm, wn) owns rows 64wm..64wm+63 and about
-//    half of the units; each 16x16 output tile is accumulated by v_mfma_f32_16x16x32_f16.
-//  * K advances in stages of 64 (half a PTQ1_0 block) through a two-stage LDS pipeline:
-//    while the matrix cores consume stage s, the workgroup stores stage s+1's A tile (from
-//    registers loaded a stage earlier) and decodes stage s+1's weights straight from the
-//    packed bytes into fp16, and the loads for stage s+2 are in flight.  No fp16 weight
-//    copy ever touches HBM.
+//  * Work is cut into tiles of 256 rows of A / C by 128 columns (8 units of 16).  Tiles are
+//    taken whole by one workgroup each for as many full rounds of the CU count as there
+//    are; the tiles left over are split along K into pieces, one workgroup each, so the
+//    last round fills the chip too.  A piece writes its fp32 partial tile to a workspace
+//    and a second kernel adds the pieces of each tile in piece order (deterministic).
+//    256-row tiles halve the weight decoding per flop against 128-row ones.  K advances in
+//    stages of 64 (half a PTQ1_0 block).
+//  * 8 waves, two per SIMD.  Waves 0..3 are consumers: wave w owns rows 64w..64w+63 and all
+//    128 columns, 2 x 4 tiles of v_mfma_f32_32x32x16_f16, with the A and B fragments of a
+//    16-k step loaded from LDS before the MFMAs of the step before it.  Waves 4..7 are producers:
+//    they copy A tiles into LDS by DMA two stages ahead (three A buffers) and decode the
+//    next stage's ternary weights from the packed bytes (copied into LDS by DMA two blocks
+//    ahead) into fp16 LDS tiles (two B buffers).  No fp16 weight copy ever touches HBM.
 //  * Decode: a group is 4 consecutive k of one row from the 4 bytes of one packed dword
-//    and one base-3 digit.  The bytes go to 16-bit lanes (b0,b2) and (b1,b3); the digit is
+//    and one base-3 digit; the bytes go to 16-bit lanes (b0,b2) and (b1,b3), the digit is
 //    ((b * 3^n) mod 256) * 3 >> 8 with packed 16-bit multiplies, and v_perm_b32 picks the
-//    fp16 value -d, 0 or +d for it from one register pair.  Within each group of 4 k the
-//    LDS tiles hold the order (k0, k2, k1, k3) - the same permutation for A and for the
-//    weights, so the dot products are unchanged - which lets each 16-bit-lane pair be
-//    stored as it is.  Wave i of the workgroup decodes the same 4 groups of every row.
+//    fp16 value -d, 0 or +d.  Within each group of 4 k the B tiles hold the order
+//    (k0, k2, k1, k3); the consumers apply the same permutation to their A fragments after
+//    reading them (A is copied to LDS unpermuted), so the dot products are unchanged.
+//    A producer lane decodes half of one weight row (8 of its 16 groups per stage).
 //  * LDS rows are 64 halves (128 B) of 8 chunks of 16 B; chunk c of row r is stored at
-//    c ^ ((r >> 1) & 7), so the MFMA operand reads and the decode stores spread evenly
-//    over the LDS banks.
+//    c ^ ((r >> 1) & 7).
+//  * Workgroups are numbered so that the ones on one XCD (dispatched round robin) share
+//    row tiles, and with them the A rows in that XCD's L2.
 #include "common.h"
 #include "launch.h"
 
@@ -35,27 +40,44 @@ namespace kata {
 
 namespace {
 
-constexpr int BM = 128;          // rows of A / C per workgroup
+constexpr int BM = 256;          // rows of A / C per workgroup
 constexpr int BKS = 64;          // k per stage (halves)
-constexpr int kMaxUnits = 18;    // 16-column units per workgroup
 constexpr int ROWB = BKS * 2;    // LDS bytes per tile row
+constexpr int NT = 4;            // 32-column MFMA tiles per workgroup
+constexpr int BN = 32 * NT;      // columns per tile (128)
+constexpr int kABuf = 3;         // A stage buffers (DMA two stages ahead)
+constexpr int kWStage = BN * 32;    // staged packed bytes of one block of the tile rows, 32 B per row
+constexpr int kLdsBytes = kABuf * BM * ROWB + 2 * BN * ROWB + 2 * kWStage;
+constexpr int kMaxPieces = 16;   // K pieces of one split tile
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// chunk c of row r lives at slot c ^ ((r >> 1) & 7): with the row's parity that gives 16
-// distinct 16-byte bank positions over any 16 consecutive rows (MFMA operand reads: 16
-// rows x 4 chunks) and over 64 consecutive rows at one chunk (decode stores)
 __device__ inline uint32_t swz(int row, int chunk) { return (uint32_t)(row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4)); }
 
-// (h0..h7) -> (h0,h2,h1,h3, h4,h6,h5,h7): the within-4 k order of the LDS tiles
-__device__ inline uint4 permute_k4(uint4 v) {
+// (h0..h7) -> (h0,h2,h1,h3, h4,h6,h5,h7): the within-4 k order of the B tiles
+__device__ inline v8h permute_k4(v8h a) {
+    const uint4 v = __builtin_bit_cast(uint4, a);
     uint4 o;
     o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
     o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
     o.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
     o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
-    return o;
+    return __builtin_bit_cast(v8h, o);
+}
+
+// LDS DMA, 16 bytes per lane to lds + 16*lane (lds wave-uniform); issued through inline
+// assembly so that the compiler does not make later LDS accesses wait for every load in
+// flight; the kernel waits for these copies explicitly.  M0 is restored.
+__device__ inline void dma16(const void* g, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(lds)
+                 : "memory");
+}
+__device__ inline uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p);
 }
 
 // fp16 of (digit_n(b) - 1) * d for bytes in 16-bit lanes (b_lo, b_hi); lo = (-d, 0),
@@ -68,121 +90,160 @@ __device__ inline uint32_t decode_pair(u16x2 b, uint32_t p3n, uint32_t lo, uint3
     return __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, sel));
 }
 
-// group: bytes of w, digit n -> LDS (b0, b2, b1, b3) at k..k+3 of the row
-__device__ inline void decode_group(uint8_t* brow, int row, int k, uint32_t w, uint32_t p3n, uint32_t lo, uint32_t hi) {
-    const u16x2 e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
-    const u16x2 o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00ff00ffu);
-    uint2 v;
-    v.x = decode_pair(e, p3n, lo, hi);
-    v.y = decode_pair(o, p3n, lo, hi);
-    *(uint2*)(brow + swz(row, k >> 3) + (k & 7) * 2) = v;
+// the two 16-bit-lane halves of a dword's bytes: (b0, b2), (b1, b3)
+__device__ inline void split(uint32_t w, u16x2& e, u16x2& o) {
+    e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
+    o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00ff00ffu);
+}
+
+// group: bytes of w, digit n -> 4 fp16 (b0, b2, b1, b3) as two dwords
+__device__ inline uint2 group_vals(uint32_t w, uint32_t p3n, uint32_t lo, uint32_t hi) {
+    u16x2 e, o;
+    split(w, e, o);
+    return make_uint2(decode_pair(e, p3n, lo, hi), decode_pair(o, p3n, lo, hi));
 }
 
 __host__ __device__ constexpr uint32_t p3x2(int n) {
     return n == 0 ? 0x00010001u : n == 1 ? 0x00030003u : n == 2 ? 0x00090009u : n == 3 ? 0x001b001bu : 0x00510051u;
 }
 
-// Decode groups (e = element of the block, dword j = bytes 4j..4j+3, k = stage-relative
-// position = e - 64h).  A row has 16 groups per stage:
-//   h=0: dword i, digit n at e = 16n + 4i                         (i, n = 0..3)
-//   h=1: dword i digit 4 at e = 64 + 4i; dword 4+i digit n at e = 80 + 4i + 8n (n = 0..4);
-//        qh at e = 120..123 and 124..127
-// For the extra rows (256..) each wave takes 4 of a row's 16 groups:
-//   h=0: dword `wave`, digits 0..3
-//   h=1: wave 0: dw0 d4 @64, dw4 d0 @80, dw4 d1 @88, dw4 d2 @96
-//        wave 1: dw1 d4 @68, dw4 d3 @104, dw4 d4 @112, dw5 d0 @84
-//        wave 2: dw2 d4 @72, dw5 d1 @92, dw5 d2 @100, dw5 d3 @108
-//        wave 3: dw3 d4 @76, dw5 d4 @116, qh @120..123, qh @124..127
-// weight-tile rows in LDS: 2 waves x 5 tiles of 32 columns (rows past the tile's R are
-// read by the MFMAs but never stored)
-constexpr int BROWS = 320;
-constexpr int kLdsBytes = 2 * BM * ROWB + 2 * BROWS * ROWB;
+// Decode groups of a stage (e = element of the block, dword j = bytes 4j..4j+3, stage
+// k = e - 64h; each group covers 4 consecutive k):
+//   h=0: dword i, digit n at k = 16n + 4i                        (i, n = 0..3)
+//   h=1: dword i digit 4 at k = 4i; dword 4+i digit n at k = 16 + 4i + 8n (n = 0..4);
+//        qh bytes (qh0, qh1, qh0, qh1) digits (a, a+1) at k = 56 (a = 0) and 60 (a = 2)
+// Producer half-rows (half q of the row): a 16-byte LDS chunk holds two groups:
+//   h=0: chunk 2n + q = dwords 2q, 2q+1 at digit n (n = 0..3)
+//   h=1: q=0: chunk 0 = digit 4 of dwords 0,1; chunks 2,3,4 = digits 0,1,2 of dwords 4,5
+//        q=1: chunk 1 = digit 4 of dwords 2,3; chunks 5,6 = digits 3,4 of dwords 4,5;
+//             chunk 7 = the two qh groups
+// Job of workgroup b (the launch's schedule, see launch_gemm_f16): b < n_full is whole
+// tile b; otherwise piece (b - n_full) % S of split tile n_full + (b - n_full) / S.  Tile t
+// is row tile t / G, column group t % G (columns 128 g ..).
+struct GemmJobs {
+    int G;        // column groups
+    int n_full;   // whole tiles
+    int S;        // pieces per split tile
+    int n_jobs;   // workgroups
+};
 
-// Workgroup = 8 waves, two per SIMD: waves 0..3 are consumers (MFMAs over the LDS stage;
-// wave (wm, wn) owns rows 64wm.. and about half of the column units), waves 4..7 are
-// producers (A tile stores, weight decode and all global loads for the next stages).  The
-// SIMD interleaves a consumer's MFMAs with a producer's decode VALU work.  One barrier per
-// stage, preceded by an LDS-only wait: the producers' global prefetches stay in flight.
-template <bool C_F16, int NWU>
+template <bool C_F16>
 __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restrict__ A, int lda,
                                                        const uint8_t* __restrict__ W, void* __restrict__ C,
-                                                       int ldc, int M, int K, int N, int G) {
+                                                       int ldc, float* __restrict__ ws, int M, int K, int N,
+                                                       GemmJobs J) {
     extern __shared__ __align__(16) uint8_t smem[];
     auto As = [&](int buf) { return smem + buf * (BM * ROWB); };
-    auto Bs = [&](int buf) { return smem + 2 * BM * ROWB + buf * (BROWS * ROWB); };
+    auto Bs = [&](int buf) { return smem + kABuf * BM * ROWB + buf * (BN * ROWB); };
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool consumer = wave < 4;
-    const int nb = K >> 7;
-    const int m0 = blockIdx.y * BM;
-    // column units of this workgroup
-    const int U = (N + 15) >> 4;
-    const int u0 = (int)(((long)blockIdx.x * U) / G), u1 = (int)(((long)(blockIdx.x + 1) * U) / G);
-    const int nu = u1 - u0, n0 = u0 * 16, R = nu * 16;
+    // workgroups are dispatched round robin over 8 XCDs: within the whole-tile jobs and
+    // within the pieces, consecutive jobs are placed on one XCD
+    int job = blockIdx.x;
+    {
+        const int lo = job < J.n_full ? 0 : J.n_full;
+        const int n = job < J.n_full ? J.n_full : J.n_jobs - J.n_full;
+        const int i = job - lo;
+        if (n % 8 == 0 && lo % 8 == 0) job = lo + (i % 8) * (n / 8) + i / 8;
+    }
+    const int nbk = K >> 7;
+    int tile, kb0, nb;
+    if (job < J.n_full) {
+        tile = job;
+        kb0 = 0;
+        nb = nbk;
+    } else {
+        const int j = job - J.n_full, piece = j % J.S;
+        tile = J.n_full + j / J.S;
+        kb0 = (int)(((long)piece * nbk) / J.S);
+        nb = (int)(((long)(piece + 1) * nbk) / J.S) - kb0;
+    }
+    const int m0 = (tile / J.G) * BM;
+    const int n0 = (tile % J.G) * BN;
+    const int R = min(BN, N - n0);              // columns of this tile
+    const int nst = 2 * nb;                      // stages
+    const uint32_t row_bytes = (uint32_t)nbk * kBlockBytes;
+    A += (size_t)kb0 * 128;
     auto barrier = [&]() {
         __builtin_amdgcn_s_waitcnt((15 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
     };
 
-    if (consumer) {
-        // 32x32x16 MFMAs (the 16x16x32 form issues at half the rate on gfx950): wave (wm, wn)
-        // owns rows 64wm..64wm+63 (two 32-row tiles) and 32-column tiles [wt0, wt0 + nwt)
-        // of the workgroup's ceil(nu / 2); the last tile may include 16 columns past R,
-        // computed from LDS rows that are never stored.
-        const int wm = wave >> 1, wn = wave & 1;
+    if (wave < 4) {
+        // ================= consumers =================
         const int l32 = lane & 31, lh = lane >> 5;
-        const int T = (nu + 1) >> 1;
-        const int wt0 = wn ? (T + 1) >> 1 : 0;
-        const int nwt = wn ? T >> 1 : (T + 1) >> 1;
-        v16f acc[2][NWU];
+        v16f acc[2][NT];
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < NWU; j++)
+            for (int j = 0; j < NT; j++)
 #pragma unroll
                 for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
-        // all NWU tiles (a wave with fewer computes tiles it never stores; the LDS weight
-        // tile has BROWS >= 2 * 32 * NWU rows)
-        auto compute = [&](int buf) {
-            const uint8_t* at = As(buf);
-            const uint8_t* bt = Bs(buf);
+        // lane l reads row / column l % 32 of each 32-row tile at k = 16 kk + 8 (l / 32) .. +7,
+        // chunk 2 kk + l / 32; every tile row of this lane has the same swizzle term
+        const int xs = (l32 >> 1) & 7;
+        const uint32_t a_row = (uint32_t)(wave * 64 + l32) * ROWB, b_row = (uint32_t)l32 * ROWB;
+        auto load_frags = [&](int st, int kk, v8h (&af)[2], v8h (&bf)[NT]) {
+            const uint32_t c = (uint32_t)(((2 * kk + lh) ^ xs) << 4);
+            const uint8_t* at = As(st % kABuf) + a_row + c;
+            const uint8_t* bt = Bs(st & 1) + b_row + c;
 #pragma unroll
-            for (int kk = 0; kk < BKS / 16; kk++) {
-                // lane l: row / column l % 32, k = 16 kk + 8 (l / 32) .. +7 = chunk 2kk + l/32
-                v8h af[2], bfs[NWU];
+            for (int i = 0; i < 2; i++) af[i] = *(const v8h*)(at + i * 32 * ROWB);
 #pragma unroll
-                for (int i = 0; i < 2; i++) af[i] = *(const v8h*)(at + swz(wm * 64 + i * 32 + l32, 2 * kk + lh));
-#pragma unroll
-                for (int j = 0; j < NWU; j++) bfs[j] = *(const v8h*)(bt + swz((wt0 + j) * 32 + l32, 2 * kk + lh));
-#pragma unroll
-                for (int j = 0; j < NWU; j++)
-#pragma unroll
-                    for (int i = 0; i < 2; i++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfs[j], acc[i][j], 0, 0, 0);
-            }
+            for (int j = 0; j < NT; j++) bf[j] = *(const v8h*)(bt + j * 32 * ROWB);
         };
-        barrier();                                       // stage 0 produced
-        for (int b = 0; b < nb; b++) {
-            compute(0);
-            barrier();
-            compute(1);
-            barrier();
+        auto mfmas = [&](v8h (&af)[2], v8h (&bf)[NT]) {
+            v8h ap[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) ap[i] = permute_k4(af[i]);
+#pragma unroll
+            for (int j = 0; j < NT; j++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap[i], bf[j], acc[i][j], 0, 0, 0);
+        };
+        // fragments are loaded one k step ahead of the MFMAs that use them; the last step
+        // of a stage is loaded before the barrier that releases the stage's buffers
+        v8h a0[2], b0[NT], a1[2], b1[NT];
+        barrier();                               // the producers' first copies landed
+        barrier();                               // stage 0 produced
+        load_frags(0, 0, a0, b0);
+        for (int st = 0; st < nst; st++) {
+            load_frags(st, 1, a1, b1);
+            mfmas(a0, b0);
+            load_frags(st, 2, a0, b0);
+            mfmas(a1, b1);
+            load_frags(st, 3, a1, b1);
+            mfmas(a0, b0);
+            barrier();                           // stage st + 1 produced; stage st's buffers free
+            if (st + 1 < nst) load_frags(st + 1, 0, a0, b0);
+            mfmas(a1, b1);
         }
-        // ---- store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
+        // store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
+        if (job >= J.n_full) {
+            // piece: the whole fp32 tile, [256][128], into the job's workspace slot
+            float* P = ws + (size_t)(job - J.n_full) * (BM * BN);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < NT; j++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++)
+                        P[(wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3)) * BN + j * 32 + l32] = acc[i][j][q];
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < NWU; j++) {
-                if (j < nwt) {
-                    const int gc = (wt0 + j) * 32 + l32;            // tile column
-                    const int gn = n0 + gc;
+            for (int j = 0; j < NT; j++) {
+                const int gc = j * 32 + l32;     // tile column
+                const int gn = n0 + gc;
 #pragma unroll
-                    for (int q = 0; q < 16; q++) {
-                        const int gm = m0 + wm * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
-                        if (gm < M && gc < R && gn < N) {
-                            if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][q];
-                            else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][q];
-                        }
+                for (int q = 0; q < 16; q++) {
+                    const int gm = m0 + wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
+                    if (gm < M && gc < R) {
+                        if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][q];
+                        else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][q];
                     }
                 }
             }
@@ -190,221 +251,215 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
     }
 
     // ================= producers =================
-    const int pw = wave - 4, ptid = tid - 256;
-    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
-    // ---- A: thread -> row ptid/2, chunks 4*(ptid&1) .. +3; stage t's A is loaded into
-    // register set t & 1 two stages before it is stored (index clamped to the last stage)
-    const int arow = ptid >> 1, achunk = (ptid & 1) * 4;
-    const _Float16* a_src = A + (size_t)min(m0 + arow, M - 1) * lda + achunk * 8;
-    uint4 areg[2][4];
-    const int last_stage = 2 * nb - 1;
-    auto load_a = [&](auto set_c, int st) {
-        constexpr int set = decltype(set_c)::value;
-        const int s2 = min(st, last_stage);
+    const int pw = wave - 4;
+    // ---- A: DMA instruction i of producer pw copies LDS bytes [1024 (4i + pw), +1024) of
+    // the stage's A tile: lane l -> tile row r = 8 (4i + pw) + l / 8, LDS slot l % 8, which
+    // holds global chunk (l % 8) ^ ((r >> 1) & 7) of that row (rows >= M read row M - 1)
+    const int ar_lo = 8 * pw + (lane >> 3);      // row for i = 0; + 32 i
+    const int aslot = lane & 7;
+    auto issue_a = [&](int st) {
+        const int s2 = min(st, nst - 1);         // stages past the end copy the last one
+        const int buf = st % kABuf;
+        const uint32_t base = lds_addr(As(buf)) + 1024 * pw;
 #pragma unroll
-        for (int c = 0; c < 4; c++) areg[set][c] = *(const uint4*)(a_src + (size_t)s2 * BKS + c * 8);
-    };
-    auto store_a = [&](auto set_c, int buf) {
-        constexpr int set = decltype(set_c)::value;
-#pragma unroll
-        for (int c = 0; c < 4; c++) *(uint4*)(As(buf) + swz(arow, achunk + c)) = permute_k4(areg[set][c]);
-    };
-
-    // ---- weight bytes: raw buffer loads, 32-bit row offsets, block offset in soffset.
-    // Rows 0..255 of the tile: lane `lane` of producer pw owns row 64pw + lane and loads its
-    // whole 28-byte block (one x4 and one x3 load, so a load instruction touches one line
-    // per row) and decodes all 16 groups of the row per stage.  Rows 256.. (R <= 288): each
-    // producer decodes 4 of the 16 groups of row 256 + lane (schedule in the table above).
-    const __amdgpu_buffer_rsrc_t wrsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
-    const int rowM = 64 * pw + lane, rowX = 256 + lane;
-    const uint32_t offM = (uint32_t)min(n0 + min(rowM, R - 1), N - 1) * row_bytes;
-    const uint32_t offX = (uint32_t)min(n0 + min(rowX, R - 1), N - 1) * row_bytes;
-    const bool has_x = R > 256;                  // workgroup-uniform
-    uint32_t wm_cur[7], wm_nxt[7];               // main row: block being decoded / next
-    uint32_t x_cur[4], x_nxt[4];                 // extra row: dword pw, dwb, dword 5, dword 6
-    const int dwb = pw < 2 ? 4 : 5;
-    auto load_blk = [&](uint32_t* wm7, uint32_t* x4, int blk) {
-        const int so = min(blk, nb - 1) * kBlockBytes;
-        const uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)offM, so, 0));
-        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-        const u32x3 v1 = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(wrsrc, (int)offM + 16, so, 0));
-        wm7[0] = v0.x; wm7[1] = v0.y; wm7[2] = v0.z; wm7[3] = v0.w;
-        wm7[4] = v1.x; wm7[5] = v1.y; wm7[6] = v1.z;
-        x4[0] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * pw), so, 0);
-        x4[1] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 4 * dwb), so, 0);
-        x4[2] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 20), so, 0);
-        x4[3] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(offX + 24), so, 0);
-    };
-    // Per-producer schedule of the extra row at h=1 as scalars: k (stage-relative) and
-    // multiplier pair of groups q = 1..3; group 0 is digit 4 of dword pw at k = 4 * pw.
-    // Source: dwb, except producer 1 q3 (dword 5) and producer 3 q2/q3 (the qh bytes as
-    // (qh0, qh1, qh0, qh1), digits a, a+1 per lane half).
-    const uint32_t k1 = (0x341c2810u >> (8 * pw)) & 0xffu;       // 16, 40, 28, 52
-    const uint32_t k2 = (0x38243018u >> (8 * pw)) & 0xffu;       // 24, 48, 36, 56
-    const uint32_t k3 = (0x3c2c1420u >> (8 * pw)) & 0xffu;       // 32, 20, 44, 60
-    const uint32_t m1 = pw == 0 ? p3x2(0) : pw == 1 ? p3x2(3) : pw == 2 ? p3x2(1) : p3x2(4);
-    const uint32_t m2 = pw == 0 ? p3x2(1) : pw == 1 ? p3x2(4) : pw == 2 ? p3x2(2) : 0x00030001u;
-    const uint32_t m3 = pw == 0 ? p3x2(2) : pw == 1 ? p3x2(0) : pw == 2 ? p3x2(3) : 0x001b0009u;
-    // Main row decode, batched over the 8 independent byte pairs of 4 dwords (the 16-bit
-    // lanes (b0,b2), (b1,b3) of each) so the dependent digit chains interleave.  Digits are
-    // iterated: t = 3m, digit = t >> 8, next m = t mod 256 (m0 = b); the h=0 stage leaves
-    // the pairs' remainders after digit 3 in mrem for digit 4 at h=1.
-    u16x2 mrem[8];
-    auto emit = [&](uint8_t* bt, int k, u16x2 te, u16x2 to, uint32_t lo, uint32_t hi) {
-        const u16x2 se = (te >> (u16x2){8, 8}) * (u16x2){0x0202, 0x0202} + (u16x2){0x0100, 0x0100};
-        const u16x2 so = (to >> (u16x2){8, 8}) * (u16x2){0x0202, 0x0202} + (u16x2){0x0100, 0x0100};
-        uint2 v;
-        v.x = __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, se));
-        v.y = __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, so));
-        *(uint2*)(bt + swz(rowM, k >> 3) + (k & 7) * 2) = v;
-    };
-    auto split = [&](uint32_t w, u16x2& e, u16x2& o) {
-        e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
-        o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00ff00ffu);
-    };
-    // stage h of the current block into buffer buf: the main row's 16 groups, then the
-    // extra row's 4
-    auto decode = [&](auto h_c, int buf) {
-        constexpr int h = decltype(h_c)::value;
-        uint8_t* bt = Bs(buf);
-        {
-            const uint32_t dbits = wm_cur[6] >> 16;
-            const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
-            if (h == 0) {
-                u16x2 m[8];
-#pragma unroll
-                for (int i = 0; i < 4; i++) split(wm_cur[i], m[2 * i], m[2 * i + 1]);
-#pragma unroll
-                for (int n = 0; n < 4; n++) {
-                    u16x2 t[8];
-#pragma unroll
-                    for (int p = 0; p < 8; p++) t[p] = m[p] * (u16x2){3, 3};
-#pragma unroll
-                    for (int i = 0; i < 4; i++) emit(bt, 16 * n + 4 * i, t[2 * i], t[2 * i + 1], lo, hi);
-#pragma unroll
-                    for (int p = 0; p < 8; p++) m[p] = t[p] & (u16x2){0xff, 0xff};
-                }
-#pragma unroll
-                for (int p = 0; p < 8; p++) mrem[p] = m[p];
-            } else {
-                // digit 4 of dwords 0..3 at k = 4i
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    emit(bt, 4 * i, mrem[2 * i] * (u16x2){3, 3}, mrem[2 * i + 1] * (u16x2){3, 3}, lo, hi);
-                // dwords 4, 5: digits 0..4 at k = 16 + 4i + 8n
-                u16x2 m[4];
-                split(wm_cur[4], m[0], m[1]);
-                split(wm_cur[5], m[2], m[3]);
-#pragma unroll
-                for (int n = 0; n < 5; n++) {
-                    u16x2 t[4];
-#pragma unroll
-                    for (int p = 0; p < 4; p++) t[p] = m[p] * (u16x2){3, 3};
-#pragma unroll
-                    for (int i = 0; i < 2; i++) emit(bt, 16 + 4 * i + 8 * n, t[2 * i], t[2 * i + 1], lo, hi);
-#pragma unroll
-                    for (int p = 0; p < 4; p++) m[p] = t[p] & (u16x2){0xff, 0xff};
-                }
-                const uint32_t qh = __builtin_amdgcn_perm(0u, wm_cur[6], 0x01000100u);
-                decode_group(bt, rowM, 56, qh, 0x00030001u, lo, hi);
-                decode_group(bt, rowM, 60, qh, 0x001b0009u, lo, hi);
-            }
+        for (int i = 0; i < 8; i++) {
+            const int r = ar_lo + 32 * i;
+            const int chunk = aslot ^ ((r >> 1) & 7);
+            const _Float16* src = A + (size_t)min(m0 + r, M - 1) * lda + (size_t)s2 * BKS + chunk * 8;
+            dma16(src, base + 4096 * i);
         }
-        if (has_x) {
-            const uint32_t dbits = x_cur[3] >> 16;
-            const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
-            if (h == 0) {
+    };
+    // ---- weights: lane `lane` of producer pw decodes half q = pw & 1 of tile row
+    // 64 (pw >> 1) + lane (q wave-uniform: no divergence).  The packed bytes of a block of
+    // the tile's rows are copied into LDS by DMA (two 16-byte pieces per row, bytes 0..15
+    // and 12..27, so no copy reads past the row's block), two blocks ahead; a lane reads
+    // its dwords back when it starts the block.  Staging slot layout [piece][BN rows][16 B]:
+    // producer pw copies piece pw & 1 of rows 64 (pw >> 1) .. +63.
+    const int wrow = 64 * (pw >> 1) + lane, q = pw & 1;
+    const bool wactive = wrow < R;
+    uint8_t* Ws = smem + kABuf * BM * ROWB + 2 * BN * ROWB;      // [2 slots][2][BN][16 B]
+    const uint8_t* wsrc = W + (size_t)min(n0 + min(wrow, R - 1), N - 1) * row_bytes + (size_t)kb0 * kBlockBytes + 12 * q;
+    auto issue_w = [&](int blk) {
+        dma16(wsrc + (size_t)min(blk, nb - 1) * kBlockBytes,
+              lds_addr(Ws + (blk & 1) * kWStage + q * (BN * 16) + (pw >> 1) * 1024));
+    };
+    uint32_t w_cur[5];
+    auto read_w = [&](int blk) {
+        const uint8_t* slot = Ws + (blk & 1) * kWStage;
+        const uint2 a = *(const uint2*)(slot + wrow * 16 + 8 * q);                  // dwords 2q, 2q+1
+        const uint4 c = *(const uint4*)(slot + BN * 16 + wrow * 16);               // bytes 12..27
+        w_cur[0] = a.x;
+        w_cur[1] = a.y;
+        w_cur[2] = c.y;                                                            // dword 4
+        w_cur[3] = c.z;                                                            // dword 5
+        w_cur[4] = c.w;                                                            // dword 6
+    };
+    auto decode_w = [&](auto h_c, int buf) {
+        constexpr int h = decltype(h_c)::value;
+        if (!wactive) return;
+        uint8_t* bt = Bs(buf);
+        const uint32_t dbits = w_cur[4] >> 16;
+        const uint32_t lo = dbits ^ 0x8000u, hi = dbits | (dbits << 16);
+        auto put = [&](int chunk, uint2 a, uint2 b) {
+            *(uint4*)(bt + swz(wrow, chunk)) = make_uint4(a.x, a.y, b.x, b.y);
+        };
+        if (h == 0) {
 #pragma unroll
-                for (int q = 0; q < 4; q++) decode_group(bt, rowX, 16 * q + 4 * pw, x_cur[0], p3x2(q), lo, hi);
-            } else {
-                decode_group(bt, rowX, 4 * pw, x_cur[0], p3x2(4), lo, hi);
-                const uint32_t qh = __builtin_amdgcn_perm(0u, x_cur[3], 0x01000100u);
-                const uint32_t w23 = pw == 3 ? qh : x_cur[1];
-                decode_group(bt, rowX, (int)k1, x_cur[1], m1, lo, hi);
-                decode_group(bt, rowX, (int)k2, w23, m2, lo, hi);
-                decode_group(bt, rowX, (int)k3, pw == 1 ? x_cur[2] : w23, m3, lo, hi);
-            }
+            for (int n = 0; n < 4; n++)
+                put(2 * n + q, group_vals(w_cur[0], p3x2(n), lo, hi), group_vals(w_cur[1], p3x2(n), lo, hi));
+        } else if (q == 0) {
+            put(0, group_vals(w_cur[0], p3x2(4), lo, hi), group_vals(w_cur[1], p3x2(4), lo, hi));
+#pragma unroll
+            for (int n = 0; n < 3; n++)
+                put(2 + n, group_vals(w_cur[2], p3x2(n), lo, hi), group_vals(w_cur[3], p3x2(n), lo, hi));
+        } else {
+            put(1, group_vals(w_cur[0], p3x2(4), lo, hi), group_vals(w_cur[1], p3x2(4), lo, hi));
+#pragma unroll
+            for (int n = 3; n < 5; n++)
+                put(2 + n, group_vals(w_cur[2], p3x2(n), lo, hi), group_vals(w_cur[3], p3x2(n), lo, hi));
+            const uint32_t qh = __builtin_amdgcn_perm(0u, w_cur[4], 0x01000100u);
+            put(7, group_vals(qh, 0x00030001u, lo, hi), group_vals(qh, 0x001b0009u, lo, hi));
         }
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    // ---- prologue: stage 0 into buffer 0; stage 1's A, block 1's bytes in flight.  All
-    // loads below are unconditional (indices clamped) so the wait counts stay exact.
-    load_blk(wm_cur, x_cur, 0);
-    load_a(I0(), 0);
-    load_a(I1(), 1);
-    load_blk(wm_nxt, x_nxt, 1);
-    store_a(I0(), 0);
-    load_a(I0(), 2);
-    decode(I0(), 0);
+    // Vector-memory order of a producer (all its loads are LDS copies, which the compiler
+    // cannot count, so the waits below do): before the barrier that releases stage s, A
+    // batch s (8 copies) must have landed while the copies issued after it may still be in
+    // flight; a block's weight copy (1) goes after the A batch of its slot.
+    // prologue: weight blocks 0 and 1, A stages 0 and 1
+    issue_w(0);
+    issue_w(1);
+    issue_a(0);
+    issue_a(1);
+    // blocks 0, 1 and batch 0; a row's two weight pieces come from two waves
+    __builtin_amdgcn_s_waitcnt((8 & 15) | ((8 >> 4) << 14) | (7 << 4) | (15 << 8));
+    barrier();
+    read_w(0);
+    decode_w(I0(), 0);
     barrier();
     for (int b = 0; b < nb; b++) {
-        // consumers on stage 2b (buffer 0); produce stage 2b+1 = h1 of block b into buffer 1
-        store_a(I1(), 1);
-        load_a(I1(), 2 * b + 3);
-        decode(I1(), 1);
+        // consumers on stage 2b; produce stage 2b+1 (h=1 of block b) into B buffer 1
+        issue_a(2 * b + 2);
+        decode_w(I1(), 1);
+        __builtin_amdgcn_s_waitcnt((8 & 15) | ((8 >> 4) << 14) | (7 << 4) | (15 << 8));    // batch 2b+1, block b+1
         barrier();
-        // consumers on stage 2b+1 (buffer 1); produce stage 2b+2 = h0 of block b+1
-#pragma unroll
-        for (int i = 0; i < 7; i++) wm_cur[i] = wm_nxt[i];
-#pragma unroll
-        for (int i = 0; i < 4; i++) x_cur[i] = x_nxt[i];
-        load_blk(wm_nxt, x_nxt, b + 2);
-        store_a(I0(), 0);
-        load_a(I0(), 2 * b + 4);
-        decode(I0(), 0);
+        // consumers on stage 2b+1; produce stage 2b+2 (h=0 of block b+1) into B buffer 0
+        if (b + 1 < nb) read_w(b + 1);
+        issue_a(2 * b + 3);
+        issue_w(b + 2);                          // into the staging slot block b freed
+        if (b + 1 < nb) decode_w(I0(), 0);
+        __builtin_amdgcn_s_waitcnt((9 & 15) | ((9 >> 4) << 14) | (7 << 4) | (15 << 8));    // batch 2b+2
         barrier();
+    }
+}
+
+// C[m][n] for the split tiles: the sum of the tile's pieces in piece order.  One thread
+// per 4 consecutive columns of a tile row.
+template <bool C_F16>
+__global__ __launch_bounds__(256) void k_gemm_pieces_sum(const float* __restrict__ ws, void* __restrict__ C, int ldc,
+                                                         int M, int N, GemmJobs J) {
+    const int t = J.n_full + blockIdx.y;                    // split tile
+    const int e = blockIdx.x * 256 + threadIdx.x;           // quad of the tile, < BM * BN / 4
+    const int r = e / (BN / 4), c4 = (e % (BN / 4)) * 4;
+    const int gm = (t / J.G) * BM + r, gn0 = (t % J.G) * BN + c4;
+    if (gm >= M) return;
+    const float* P = ws + (size_t)blockIdx.y * J.S * (BM * BN) + r * BN + c4;
+    float4 s = *(const float4*)P;
+    for (int p = 1; p < J.S; p++) {
+        const float4 v = *(const float4*)(P + (size_t)p * (BM * BN));
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    }
+    const float v[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (gn0 + i < N) {
+            if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn0 + i] = (_Float16)v[i];
+            else ((float*)C)[(size_t)gm * ldc + gn0 + i] = v[i];
+        }
     }
 }
 
 }  // namespace
 
-// Column groups: about (CUs / row tiles) groups of at most kMaxUnits units; the wave
-// unit count selects the kernel instance.
-template <int NWU>
-static hipError_t launch_nwu(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M,
-                             int K, int N, int G, dim3 grid, hipStream_t s) {
-    static bool attr_done = false;
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true, NWU>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false, NWU>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
-    if (c_dtype == 1)
-        hipLaunchKernelGGL((k_gemm_ptq1_f16<true, NWU>), grid, dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W, C,
-                           ldc, M, K, N, G);
-    else
-        hipLaunchKernelGGL((k_gemm_ptq1_f16<false, NWU>), grid, dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W,
-                           C, ldc, M, K, N, G);
-    return hipGetLastError();
+namespace {
+
+struct DeviceWs {
+    int n_cu = 0;
+    float* ws = nullptr;                         // n_cu fp32 tiles of split-tile pieces
+    bool attr_done = false;
+};
+
+DeviceWs& device_ws(int dev) {
+    static DeviceWs tab[64];
+    return tab[dev & 63];
 }
 
+}  // namespace
+
+// The schedule: T tiles; the whole rounds of n_cu tiles go to one workgroup each, the
+// remaining r tiles are split into S = min(n_cu / r, kMaxPieces, blocks) pieces each.  The
+// pieces' workspace (at most n_cu fp32 tiles, 128 KB each) is allocated on a device's
+// first call and kept; calls on one device share it and must not overlap in time.
 hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
                            int M, int K, int N, hipStream_t s) {
-    static int n_cu = 0;
-    if (!n_cu) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-            n_cu = 256;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    DeviceWs& D = device_ws(dev);
+    if (!D.n_cu) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        D.n_cu = n > 0 ? n : 256;
+    }
+    if (!D.attr_done) {
+        e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    kLdsBytes);
+        if (e != hipSuccess) return e;
+        D.attr_done = true;
     }
     const int mt = (M + BM - 1) / BM;
-    const int U = (N + 15) / 16;
-    int G = std::max(1, n_cu / mt);
-    G = std::max(G, (U + kMaxUnits - 1) / kMaxUnits);
-    G = std::min(G, U);
-    const int umax = (U + G - 1) / G;                   // units of the widest workgroup
-    const int tmax = ((umax + 1) / 2 + 1) / 2;          // 32-column tiles of its wider wave
-    const dim3 grid(G, mt);
-    if (tmax <= 1) return launch_nwu<1>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
-    if (tmax <= 2) return launch_nwu<2>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
-    if (tmax <= 3) return launch_nwu<3>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
-    return launch_nwu<5>(A, lda, W, C, c_dtype, ldc, M, K, N, G, grid, s);
+    GemmJobs J;
+    J.G = (N + BN - 1) / BN;
+    const long T = (long)mt * J.G;
+    const int nbk = K / 128;
+    long rem = T % D.n_cu;
+    int S = rem ? std::min(std::min(D.n_cu / (int)rem, kMaxPieces), nbk) : 1;
+    if (S < 2) {
+        S = 1;
+        rem = 0;
+    }
+    J.n_full = (int)(T - rem);
+    J.S = S;
+    J.n_jobs = (int)(J.n_full + rem * S);
+    if (rem && !D.ws) {
+        e = hipMalloc((void**)&D.ws, (size_t)D.n_cu * BM * BN * sizeof(float));
+        if (e != hipSuccess) {
+            D.ws = nullptr;
+            return e;
+        }
+    }
+    if (c_dtype == 1)
+        hipLaunchKernelGGL(k_gemm_ptq1_f16<true>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W,
+                           C, ldc, D.ws, M, K, N, J);
+    else
+        hipLaunchKernelGGL(k_gemm_ptq1_f16<false>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, (const _Float16*)A, lda,
+                           W, C, ldc, D.ws, M, K, N, J);
+    e = hipGetLastError();
+    if (e != hipSuccess || !rem) return e;
+    const dim3 grid(BM * BN / 4 / 256, (unsigned)rem);
+    if (c_dtype == 1)
+        hipLaunchKernelGGL(k_gemm_pieces_sum<true>, grid, dim3(256), 0, s, D.ws, C, ldc, M, N, J);
+    else
+        hipLaunchKernelGGL(k_gemm_pieces_sum<false>, grid, dim3(256), 0, s, D.ws, C, ldc, M, N, J);
+    return hipGetLastError();
 }
 
 }  // namespace kata

@@ -113,6 +113,23 @@ def test_gemm_f16_pp512_full_shape(dev, K, N):
     assert rel_l2(C.cpu().numpy()[rows, :64], ref_o).max() < 1e-5
 
 
+def test_gemm_f16_tile_schedules(dev):
+    """Whole-tile rounds, split tiles (pieces summed from the workspace) and both together,
+    called back to back so the workspace is reused with a different piece count; every
+    output vs torch fp32 on the bit-exact expanded weights."""
+    cases = [(256, 128, 128 * 256),      # 256 tiles: whole tiles only (one round on 256 CUs)
+             (256, 256, 128 * 257 - 5),  # one round + 1 split tile of 2 pieces, ragged N
+             (70, 1280, 200),            # 2 tiles split 10 ways
+             (513, 384, 130)]            # 3 x 2 tiles, 3 pieces, ragged M and N
+    for M, K, N in cases:
+        W_np, _, _ = orc.synth_ptq1(N, K, M * 7 + K + N)
+        A = torch.from_numpy(orc.synth_x(M, K, M + 3)).to(dev)
+        W = torch.from_numpy(W_np).to(dev)
+        C = ops.gemm_ptq1_f16(A, W, K, N)
+        ref = A.float() @ ops.expand_f16(W, K, N).float().T
+        assert rel_l2(C.cpu().numpy(), ref.cpu().numpy()).max() < 5e-5, (M, K, N)
+
+
 # ----------------------------------------------------------------------------- int8 path
 def test_quant_rows_bit_exact(dev, golden):
     Q, SX = ops.quant_rows(torch.from_numpy(golden["qr_X"]).to(dev))
