@@ -20,11 +20,9 @@
 //    next stage's ternary weights from the packed bytes (copied into LDS by DMA two blocks
 //    ahead) into fp16 LDS tiles (two B buffers).  No fp16 weight copy ever touches HBM.
 //  * Decode: a group is 4 consecutive k of one row from the 4 bytes of one packed dword
-//    and one base-3 digit; the bytes go to 16-bit lanes (b0,b2) and (b1,b3), the digit is
+//    and one base-3 digit; the bytes go to 16-bit lanes (b0,b1) and (b2,b3), the digit is
 //    ((b * 3^n) mod 256) * 3 >> 8 with packed 16-bit multiplies, and v_perm_b32 picks the
-//    fp16 value -d, 0 or +d.  Within each group of 4 k the B tiles hold the order
-//    (k0, k2, k1, k3); the consumers apply the same permutation to their A fragments after
-//    reading them (A is copied to LDS unpermuted), so the dot products are unchanged.
+//    fp16 value -d, 0 or +d.
 //    A producer lane decodes half of one weight row (8 of its 16 groups per stage).
 //  * LDS rows are 64 halves (128 B) of 8 chunks of 16 B; chunk c of row r is stored at
 //    c ^ ((r >> 1) & 7).
@@ -55,17 +53,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 __device__ inline uint32_t swz(int row, int chunk) { return (uint32_t)(row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4)); }
 
-// (h0..h7) -> (h0,h2,h1,h3, h4,h6,h5,h7): the within-4 k order of the B tiles
-__device__ inline v8h permute_k4(v8h a) {
-    const uint4 v = __builtin_bit_cast(uint4, a);
-    uint4 o;
-    o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
-    o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
-    o.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
-    o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
-    return __builtin_bit_cast(v8h, o);
-}
-
 // LDS DMA, 16 bytes per lane to lds + 16*lane (lds wave-uniform); issued through inline
 // assembly so that the compiler does not make later LDS accesses wait for every load in
 // flight; the kernel waits for these copies explicitly.  M0 is restored.
@@ -90,17 +77,16 @@ __device__ inline uint32_t decode_pair(u16x2 b, uint32_t p3n, uint32_t lo, uint3
     return __builtin_amdgcn_perm(hi, lo, __builtin_bit_cast(uint32_t, sel));
 }
 
-// the two 16-bit-lane halves of a dword's bytes: (b0, b2), (b1, b3)
-__device__ inline void split(uint32_t w, u16x2& e, u16x2& o) {
-    e = __builtin_bit_cast(u16x2, w & 0x00ff00ffu);
-    o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00ff00ffu);
+// group: bytes (b0, b1, b2, b3) of w -> 4 fp16 in that order as two dwords, digit n of
+// b0, b1 by the multipliers p3lo and of b2, b3 by p3hi; the bytes go to 16-bit lanes
+// (b0, b1) and (b2, b3) (v_perm selector 0x0c is a zero byte)
+__device__ inline uint2 group_vals(uint32_t w, uint32_t p3lo, uint32_t p3hi, uint32_t lo, uint32_t hi) {
+    const u16x2 e = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c010c00u));
+    const u16x2 o = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c030c02u));
+    return make_uint2(decode_pair(e, p3lo, lo, hi), decode_pair(o, p3hi, lo, hi));
 }
-
-// group: bytes of w, digit n -> 4 fp16 (b0, b2, b1, b3) as two dwords
 __device__ inline uint2 group_vals(uint32_t w, uint32_t p3n, uint32_t lo, uint32_t hi) {
-    u16x2 e, o;
-    split(w, e, o);
-    return make_uint2(decode_pair(e, p3n, lo, hi), decode_pair(o, p3n, lo, hi));
+    return group_vals(w, p3n, p3n, lo, hi);
 }
 
 __host__ __device__ constexpr uint32_t p3x2(int n) {
@@ -111,7 +97,7 @@ __host__ __device__ constexpr uint32_t p3x2(int n) {
 // k = e - 64h; each group covers 4 consecutive k):
 //   h=0: dword i, digit n at k = 16n + 4i                        (i, n = 0..3)
 //   h=1: dword i digit 4 at k = 4i; dword 4+i digit n at k = 16 + 4i + 8n (n = 0..4);
-//        qh bytes (qh0, qh1, qh0, qh1) digits (a, a+1) at k = 56 (a = 0) and 60 (a = 2)
+//        qh bytes (qh0, qh1, qh0, qh1) at digits (a, a, a+1, a+1) at k = 56 (a = 0) and 60 (a = 2)
 // Producer half-rows (half q of the row): a 16-byte LDS chunk holds two groups:
 //   h=0: chunk 2n + q = dwords 2q, 2q+1 at digit n (n = 0..3)
 //   h=1: q=0: chunk 0 = digit 4 of dwords 0,1; chunks 2,3,4 = digits 0,1,2 of dwords 4,5
@@ -193,14 +179,11 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
             for (int j = 0; j < NT; j++) bf[j] = *(const v8h*)(bt + j * 32 * ROWB);
         };
         auto mfmas = [&](v8h (&af)[2], v8h (&bf)[NT]) {
-            v8h ap[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) ap[i] = permute_k4(af[i]);
 #pragma unroll
             for (int j = 0; j < NT; j++)
 #pragma unroll
                 for (int i = 0; i < 2; i++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         };
         // fragments are loaded one k step ahead of the MFMAs that use them; the last step
         // of a stage is loaded before the barrier that releases the stage's buffers
@@ -318,7 +301,7 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
             for (int n = 3; n < 5; n++)
                 put(2 + n, group_vals(w_cur[2], p3x2(n), lo, hi), group_vals(w_cur[3], p3x2(n), lo, hi));
             const uint32_t qh = __builtin_amdgcn_perm(0u, w_cur[4], 0x01000100u);
-            put(7, group_vals(qh, 0x00030001u, lo, hi), group_vals(qh, 0x001b0009u, lo, hi));
+            put(7, group_vals(qh, p3x2(0), p3x2(1), lo, hi), group_vals(qh, p3x2(2), p3x2(3), lo, hi));
         }
     };
     using I0 = std::integral_constant<int, 0>;
