@@ -13,7 +13,9 @@ Weights are seeded
 synthetic PTQ1_0 (trits iid on {-1,0,1}, fp16 scales |N(0,0.02)|), activations fp16
 N(0,1).  Steps rotate over enough distinct weight copies (>= 512 MB) that no matrix is
 served from the 256 MB Infinity Cache.  `value` = packed weight bytes of all GEMVs of the
-timed steps / wall time of those steps (events on the launch stream), in GB/s.
+timed steps / wall time of those steps (events on the launch stream), in GB/s; a step's 6
+launches are issued from Python (--graph replays a HIP graph of them instead, which measures
+slower here: a graph launch costs more than the host's lead over the GPU).
 
 Also reported (same JSON line):
   roofline     dominant kernel k_gemv_ptq1<1>: algorithmic bytes per launch (the packed
@@ -80,6 +82,32 @@ def cpu_baseline(sample_rows: int, threads: int):
     return total_bytes / total_t / 1e9, total_bytes
 
 
+def run_gemm(torch, ops, dev, stream, copies, ncopies):
+    """pp512 exact fp16 prefill GEMM (config 4): us and TFLOPS per shape, 10 calls over
+    rotating weight copies between two events."""
+    gemm = {}
+    M = 512
+    A = {K: torch.from_numpy(np.random.default_rng(K).standard_normal((M, K)).astype(np.float16)).to(dev)
+         for K in (5120, 17408)}
+    for name, K, N, j in (("ffn_gate", 5120, 17408, 7), ("ffn_down", 17408, 5120, 9)):
+        C = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for r in range(3):
+            ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
+        torch.cuda.synchronize()
+        nrep = 10
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for r in range(nrep):
+            ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / nrep
+        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        gemm[name] = {"M": M, "K": K, "N": N, "us": round(us, 1), "TFLOPS": round(tflops, 1),
+                      "frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+    return gemm
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -88,7 +116,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=2048)
-    ap.add_argument("--graph", action="store_true", help="replay per-step HIP graphs instead of eager launches")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay each step's HIP graph instead of launching its GEMVs from Python")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the pp512 prefill GEMMs (for counter runs), then exit")
+    ap.add_argument("--step-only", action="store_true",
+                    help="only the timed decode-sweep steps (for counter runs), then print value and exit")
     ap.add_argument("--reps", type=int, default=200, help="repeats per matrix for the per-matrix tables")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
                     help="only run 20 plain torch copies of MB MiB (HBM-counter calibration) and exit")
@@ -129,6 +162,10 @@ def main():
                                    .astype(np.float16)).to(dev)
     ys = [torch.empty((1, N), dtype=torch.float32, device=dev) for _, _, N, _ in SWEEP]
 
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": run_gemm(torch, ops, dev, stream, copies, ncopies)}))
+        return
+
     groups = {}
     for j, (name, K, N, grp) in enumerate(SWEEP):
         groups.setdefault(grp, []).append(j)
@@ -150,7 +187,7 @@ def main():
     use_graph = args.graph
     cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
     runners = {}
-    for fname, fn in (("step", step), ("single", step_single)):
+    for fname, fn in (("step", step),) if args.step_only else (("step", step), ("single", step_single)):
         for i in range(2):
             fn(i)                                 # first calls set kernel attributes
         torch.cuda.synchronize()
@@ -182,6 +219,9 @@ def main():
     ms_total = timed("step", args.steps)
     ms_step = ms_total / args.steps
     value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
+    if args.step_only:
+        print(json.dumps({"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms_step, 5)}))
+        return
 
     # ---- dominant kernel: a step is nothing but its GEMV launches
     launches = len(group_list)
@@ -246,28 +286,7 @@ def main():
         del Wqs, Wq
 
     # ---- pp512 prefill GEMM (config 4), fp16 exact path
-    gemm = None
-    if not args.no_gemm:
-        gemm = {}
-        M = 512
-        A = {K: torch.from_numpy(np.random.default_rng(K).standard_normal((M, K)).astype(np.float16)).to(dev)
-             for K in (5120, 17408)}
-        for name, K, N, j in (("ffn_gate", 5120, 17408, 7), ("ffn_down", 17408, 5120, 9)):
-            C = torch.empty((M, N), dtype=torch.float16, device=dev)
-            for r in range(3):
-                ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
-            torch.cuda.synchronize()
-            nrep = 10
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for r in range(nrep):
-                ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
-            b.record(stream)
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / nrep
-            tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-            gemm[name] = {"M": M, "K": K, "N": N, "us": round(us, 1), "TFLOPS": round(tflops, 1),
-                          "frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+    gemm = None if args.no_gemm else run_gemm(torch, ops, dev, stream, copies, ncopies)
 
     # ---- CPU baseline (reference host arithmetic, bounded sample)
     cpu = None

@@ -600,16 +600,33 @@ static hipError_t launch_gemv_pad(const GemvMats& P, const void* x, int x_dtype,
                             : launch_gemv_cfg<T, LR, false, XS, false>(P, x, x_dtype, x_layout, K, lds, s);
 }
 
-// Split `wgs` workgroups over the matrices in proportion to their tiles (at least one
-// each); returns the largest tiles-per-workgroup.
+// Split at most `wgs` workgroups over the matrices in proportion to their tiles (at least
+// one each; a launch of more workgroups than CUs would run its last ones as a second
+// round), the spare ones to the matrix with the most tiles per workgroup; returns the
+// largest tiles-per-workgroup.
 static int gemv_split(GemvMats& P, int wgs) {
-    int total = 0, tmax = 0;
+    int total = 0;
+    int w[kMaxMats];
     for (int i = 0; i < P.count; i++) total += (P.N[i] + 3) / 4;
+    int used = 0;
+    for (int i = 0; i < P.count; i++) {
+        w[i] = std::max(1, (int)((long long)((P.N[i] + 3) / 4) * wgs / total));
+        used += w[i];
+    }
+    auto tpw_of = [&](int i) { return ((P.N[i] + 3) / 4 + w[i] - 1) / w[i]; };
+    while (used < wgs) {
+        int best = 0;
+        for (int i = 1; i < P.count; i++)
+            if (tpw_of(i) > tpw_of(best)) best = i;
+        if (tpw_of(best) == 1) break;
+        ++w[best];
+        ++used;
+    }
+    int tmax = 0;
     P.wg0[0] = 0;
     for (int i = 0; i < P.count; i++) {
         const int tiles = (P.N[i] + 3) / 4;
-        const int w = std::max(1, (int)(((long long)tiles * wgs + total - 1) / total));
-        P.tpw[i] = (tiles + w - 1) / w;
+        P.tpw[i] = tpw_of(i);
         P.wg0[i + 1] = P.wg0[i] + (tiles + P.tpw[i] - 1) / P.tpw[i];
         tmax = std::max(tmax, P.tpw[i]);
     }
