@@ -77,6 +77,9 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
  * C[m][n] = sum_k A[m][k] * half(trit[n][k] * d[n][k/128]), fp32 accumulation.
  * A is fp16 [M][lda] (lda >= K), C is [M][ldc] of c_dtype (KATA_F32 or KATA_F16).
  * K % 128 == 0; any M >= 1, N >= 1.
+ * The K-pieces of the last round of tiles use a per-device workspace (at most one fp32
+ * 256x128 tile per CU), allocated on the device's first call that needs it and kept: calls
+ * on one device must not overlap in time, and that first call must not be captured.
  * Replaces Engine::dExpandGemm's fp16 path (src/engine.cpp:208-219: k_expand_ptq1_v2 into
  * a 178 MB stage, then Engine::dGemm / k_gemm_f16, shaders/prefill.metal:31-41). */
 int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
