@@ -43,6 +43,7 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
 
 # (name, K, N, input) of one layer of each kind; matrices of one input share its activation
 SWEEP = [
@@ -105,6 +106,26 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
         tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
         gemm[name] = {"M": M, "K": K, "N": N, "us": round(us, 1), "TFLOPS": round(tflops, 1),
                       "frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+        # the int8 FFN variant (config 5): activation quantisation + int8 GEMM
+        Q, SX = ops.quant_rows(A[K])
+        for r in range(3):
+            ops.gemm_ptq1_i8(Q, SX, copies[r % ncopies][j], K, N, out=C)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for r in range(nrep):
+            ops.quant_rows(A[K])
+        b.record(stream)
+        torch.cuda.synchronize()
+        us_q = a.elapsed_time(b) * 1e3 / nrep
+        a.record(stream)
+        for r in range(nrep):
+            ops.gemm_ptq1_i8(Q, SX, copies[r % ncopies][j], K, N, out=C)
+        b.record(stream)
+        torch.cuda.synchronize()
+        us_i = a.elapsed_time(b) * 1e3 / nrep
+        tops = 2.0 * M * N * K / (us_i * 1e-6) / 1e12
+        gemm[name + "_i8"] = {"M": M, "K": K, "N": N, "quant_us": round(us_q, 1), "us": round(us_i, 1),
+                              "TOPS": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
     return gemm
 
 

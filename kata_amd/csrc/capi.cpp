@@ -125,7 +125,7 @@ int kata_gemm_ptq1_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t*
     if (ldc < N) return fail(KATA_EINVAL, "ldc=%d < N=%d", ldc, N);
     if (c_dtype != KATA_F32 && c_dtype != KATA_F16) return fail(KATA_EINVAL, "c_dtype=%d", c_dtype);
     if (!aligned(A8, 16)) return fail(KATA_EINVAL, "A8 must be 16-byte aligned");
-    if (!aligned(W, 2)) return fail(KATA_EINVAL, "W must be 2-byte aligned");
+    if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
     return check_launch(kata::launch_gemm_i8(A8, SX, ldS, W, C, c_dtype, ldc, M, K, N, (hipStream_t)stream),
                         "gemm ptq1 i8");
 }

@@ -39,6 +39,27 @@ __global__ __launch_bounds__(256) void k_quant_rows(const _Float16* __restrict__
     }
 }
 
+// digit multipliers 3^n in both 16-bit lanes
+__host__ __device__ constexpr uint32_t p3x2(int n) {
+    return n == 0 ? 0x00010001u : n == 1 ? 0x00030003u : n == 2 ? 0x00090009u : n == 3 ? 0x001b001bu : 0x00510051u;
+}
+
+// int8 trits (digit - 1) of the 4 bytes of w, in byte order: bytes 0, 1 at the digit of
+// multiplier p3lo, bytes 2, 3 at p3hi.  The bytes go to 16-bit lanes (v_perm selector 0x0c is
+// a zero byte); ((b * 3^n) mod 256) * 3 has the digit in its high byte; a v_perm table maps
+// digits 0, 1, 2 to the bytes 0xff, 0x00, 0x01.
+__device__ inline uint32_t trits4(uint32_t w, uint32_t p3lo, uint32_t p3hi) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 e = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c010c00u));
+    u16x2 o = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c030c02u));
+    e = (e * __builtin_bit_cast(u16x2, p3lo)) & (u16x2){0xff, 0xff};
+    o = (o * __builtin_bit_cast(u16x2, p3hi)) & (u16x2){0xff, 0xff};
+    e = e * (u16x2){3, 3};
+    o = o * (u16x2){3, 3};
+    const uint32_t dg = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, o), __builtin_bit_cast(uint32_t, e), 0x07050301u);
+    return __builtin_amdgcn_perm(0u, 0x000100ffu, dg);
+}
+
 constexpr int BM = 128, BN = 128, BK = 128;
 constexpr int LDB_S = BK + 16;   // bytes per LDS row
 
@@ -78,32 +99,36 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__
             }
             if (tid < BM) sxs[tid] = (m0 + tid < M) ? SX[(size_t)kb * ldS + m0 + tid] : 0.0f;
         }
-        for (int idx = tid; idx < BN * 13; idx += 256) {
-            const int r = idx / 13, pr = idx - r * 13;
-            const int gn = n0 + r;
-            const int p = 2 * pr;
-            uint16_t* brow = (uint16_t*)(Bs + r * LDB_S);
+        // B tile: thread -> 4 of the 8 16-byte chunks (16 k each) of tile row tid / 2
+        {
+            const int r = tid >> 1, gn = n0 + r;
+            uint4* brow = (uint4*)(Bs + r * LDB_S);
             if (gn < N) {
                 const uint8_t* blk = W + ((size_t)gn * nb + kb) * kBlockBytes;
-                const uint32_t bb = *(const uint16_t*)(blk + p);
-                const uint32_t b0 = bb & 0xffu, b1 = bb >> 8;
-                const int nd = p < 24 ? 5 : 4;
+                const uint32_t* bw = (const uint32_t*)blk;   // blocks are 4-byte aligned (W is, 28 = 4 * 7)
+                const uint32_t w0 = bw[0], w1 = bw[1], w2 = bw[2], w3 = bw[3], w4 = bw[4], w5 = bw[5], w6 = bw[6];
+                if ((tid & 1) == 0) {
+                    // chunks 0..3: dwords 0..3 at digit c
 #pragma unroll
-                for (int n = 0; n < 5; n++) {
-                    if (n < nd) {
-                        const uint32_t t0 = (uint32_t)(uint8_t)(int8_t)((int)ptq1_digit(b0, n) - 1);
-                        const uint32_t t1 = (uint32_t)(uint8_t)(int8_t)((int)ptq1_digit(b1, n) - 1);
-                        brow[ptq1_slot_elem(p, n) >> 1] = (uint16_t)(t0 | (t1 << 8));
-                    }
+                    for (int c = 0; c < 4; c++)
+                        brow[c] = make_uint4(trits4(w0, p3x2(c), p3x2(c)), trits4(w1, p3x2(c), p3x2(c)),
+                                             trits4(w2, p3x2(c), p3x2(c)), trits4(w3, p3x2(c), p3x2(c)));
+                } else {
+                    brow[4] = make_uint4(trits4(w0, p3x2(4), p3x2(4)), trits4(w1, p3x2(4), p3x2(4)),
+                                         trits4(w2, p3x2(4), p3x2(4)), trits4(w3, p3x2(4), p3x2(4)));
+                    brow[5] = make_uint4(trits4(w4, p3x2(0), p3x2(0)), trits4(w5, p3x2(0), p3x2(0)),
+                                         trits4(w4, p3x2(1), p3x2(1)), trits4(w5, p3x2(1), p3x2(1)));
+                    brow[6] = make_uint4(trits4(w4, p3x2(2), p3x2(2)), trits4(w5, p3x2(2), p3x2(2)),
+                                         trits4(w4, p3x2(3), p3x2(3)), trits4(w5, p3x2(3), p3x2(3)));
+                    const uint32_t qh = __builtin_amdgcn_perm(0u, w6, 0x01000100u);   // (qh0, qh1, qh0, qh1)
+                    brow[7] = make_uint4(trits4(w4, p3x2(4), p3x2(4)), trits4(w5, p3x2(4), p3x2(4)),
+                                         trits4(qh, p3x2(0), p3x2(1)), trits4(qh, p3x2(2), p3x2(3)));
                 }
-                if (pr == 0) sws[r] = half_bits_to_float(*(const uint16_t*)(blk + 26));
+                if ((tid & 1) == 0) sws[r] = half_bits_to_float(w6 >> 16);
             } else {
 #pragma unroll
-                for (int n = 0; n < 5; n++) {
-                    const int e = ptq1_slot_elem(p, n);
-                    if (e >= 0) brow[e >> 1] = 0;
-                }
-                if (pr == 0) sws[r] = 0.0f;
+                for (int c = 0; c < 4; c++) brow[4 * (tid & 1) + c] = make_uint4(0, 0, 0, 0);
+                if ((tid & 1) == 0) sws[r] = 0.0f;
             }
         }
         __syncthreads();
