@@ -113,7 +113,7 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
         torch.cuda.synchronize()
         a.record(stream)
         for r in range(nrep):
-            ops.quant_rows(A[K])
+            ops.quant_rows(A[K], out=(Q, SX))
         b.record(stream)
         torch.cuda.synchronize()
         us_q = a.elapsed_time(b) * 1e3 / nrep

@@ -87,7 +87,8 @@ int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, in
 
 /* Activation quantisation for the int8 prefill path: per (token m, 128-group g)
  * scale = amax > 0 ? amax/127 : 1, Q = clamp(rint(x/scale), +-127), SX[g*ldS + m] = scale.
- * X fp16 [M][K], Q int8 [M][K], SX fp32 [K/128][ldS], ldS >= M.
+ * X fp16 [M][K] (16-byte aligned), Q int8 [M][K] (8-byte aligned), SX fp32 [K/128][ldS],
+ * ldS >= M.
  * Replaces k_quant_rows (shaders/prefill.metal:369-381; dispatched src/engine.cpp:230). */
 int kata_quant_rows_i8(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS, void* stream);
 

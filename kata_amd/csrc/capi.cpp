@@ -112,7 +112,7 @@ int kata_quant_rows_i8(const uint16_t* X, int8_t* Q, float* SX, int M, int K, in
     if (M <= 0) return fail(KATA_EINVAL, "M=%d must be positive", M);
     if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
     if (ldS < M) return fail(KATA_EINVAL, "ldS=%d < M=%d", ldS, M);
-    if (!aligned(X, 4) || !aligned(Q, 2)) return fail(KATA_EINVAL, "X/Q misaligned");
+    if (!aligned(X, 16) || !aligned(Q, 8)) return fail(KATA_EINVAL, "X must be 16-byte and Q 8-byte aligned");
     return check_launch(kata::launch_quant_rows(X, Q, SX, M, K, ldS, (hipStream_t)stream), "quant rows");
 }
 

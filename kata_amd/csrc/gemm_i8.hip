@@ -18,25 +18,47 @@ namespace kata {
 
 namespace {
 
+// max over the 16 lanes of a DPP row
+__device__ inline float row16_max(float a) {
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xb1, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4e, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x141, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x140, 0xf, 0xf, false)));
+    return a;
+}
+
+// One (token, group) per 16 lanes (a DPP row), 8 elements per lane from one 16-byte load;
+// groups numbered token-major, 16 per 256-thread workgroup.
 __global__ __launch_bounds__(256) void k_quant_rows(const _Float16* __restrict__ X, int8_t* __restrict__ Q,
-                                                    float* __restrict__ SX, int K, int ldS) {
-    const int m = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+                                                    float* __restrict__ SX, int M, int K, int ldS) {
     const int G = K / kGroup;
-    const _Float16* xr = X + (size_t)m * K;
-    int8_t* qr = Q + (size_t)m * K;
-    for (int g = wave; g < G; g += 4) {
-        const v2h v = *(const v2h*)(xr + g * kGroup + 2 * lane);
-        const float a = (float)v[0], b = (float)v[1];
-        float mx = fmaxf(fabsf(a), fabsf(b));
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float scale = mx > 0.0f ? mx / 127.0f : 1.0f;
-        const float inv = 1.0f / scale;
-        const float qa = fminf(fmaxf(rintf(a * inv), -127.0f), 127.0f);
-        const float qb = fminf(fmaxf(rintf(b * inv), -127.0f), 127.0f);
-        const uint16_t pk = (uint16_t)((uint8_t)(int8_t)qa | ((uint16_t)(uint8_t)(int8_t)qb << 8));
-        *(uint16_t*)(qr + g * kGroup + 2 * lane) = pk;
-        if (lane == 0) SX[(size_t)g * ldS + m] = scale;
+    const int gi = blockIdx.x * 16 + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+    if (gi >= M * G) return;                     // whole DPP rows drop out together
+    const int m = gi / G, g = gi - m * G;
+    const size_t o = (size_t)m * K + (size_t)g * kGroup + 8 * sub;
+    const uint4 raw = *(const uint4*)(X + o);
+    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const v2h h = __builtin_bit_cast(v2h, rw[i]);
+        v[2 * i] = (float)h[0];
+        v[2 * i + 1] = (float)h[1];
     }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[i]));
+    mx = row16_max(mx);
+    const float scale = mx > 0.0f ? mx / 127.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    uint32_t q[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float qf = fminf(fmaxf(rintf(v[i] * inv), -127.0f), 127.0f);
+        q[i >> 2] |= (uint32_t)(uint8_t)(int8_t)qf << (8 * (i & 3));
+    }
+    *(uint2*)(Q + o) = make_uint2(q[0], q[1]);
+    if (sub == 0) SX[(size_t)g * ldS + m] = scale;
 }
 
 // digit multipliers 3^n in both 16-bit lanes
@@ -179,7 +201,9 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__
 }  // namespace
 
 hipError_t launch_quant_rows(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS, hipStream_t s) {
-    hipLaunchKernelGGL(k_quant_rows, dim3(M), dim3(256), 0, s, (const _Float16*)X, Q, SX, K, ldS);
+    const long groups = (long)M * (K / kGroup);
+    hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((groups + 15) / 16)), dim3(256), 0, s, (const _Float16*)X, Q, SX,
+                       M, K, ldS);
     return hipGetLastError();
 }
 

@@ -84,12 +84,16 @@ def gemm_ptq1_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=to
     return C
 
 
-def quant_rows(X: torch.Tensor, ldS: int | None = None):
+def quant_rows(X: torch.Tensor, ldS: int | None = None, out=None):
+    """int8 rows and group scales of X; `out` = (Q, SX) to write into existing tensors."""
     _need_gpu(X)
     M, K = X.shape
     ldS = M if ldS is None else ldS
-    Q = torch.empty((M, K), dtype=torch.int8, device=X.device)
-    SX = torch.zeros((K // GROUP, ldS), dtype=torch.float32, device=X.device)
+    if out is not None:
+        Q, SX = out
+    else:
+        Q = torch.empty((M, K), dtype=torch.int8, device=X.device)
+        SX = torch.zeros((K // GROUP, ldS), dtype=torch.float32, device=X.device)
     check(lib().kata_quant_rows_i8(_ptr(X), _ptr(Q), _ptr(SX), M, K, ldS, _stream(X)))
     return Q, SX
 
