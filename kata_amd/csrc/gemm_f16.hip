@@ -30,6 +30,7 @@
 //    row tiles, and with them the A rows in that XCD's L2.
 #include "common.h"
 #include "launch.h"
+#include "gemm_sched.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -46,7 +47,6 @@ constexpr int BN = 32 * NT;      // columns per tile (128)
 constexpr int kABuf = 3;         // A stage buffers (DMA two stages ahead)
 constexpr int kWStage = BN * 32;    // staged packed bytes of one block of the tile rows, 32 B per row
 constexpr int kLdsBytes = kABuf * BM * ROWB + 2 * BN * ROWB + 2 * kWStage;
-constexpr int kMaxPieces = 16;   // K pieces of one split tile
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -103,16 +103,6 @@ __host__ __device__ constexpr uint32_t p3x2(int n) {
 //   h=1: q=0: chunk 0 = digit 4 of dwords 0,1; chunks 2,3,4 = digits 0,1,2 of dwords 4,5
 //        q=1: chunk 1 = digit 4 of dwords 2,3; chunks 5,6 = digits 3,4 of dwords 4,5;
 //             chunk 7 = the two qh groups
-// Job of workgroup b (the launch's schedule, see launch_gemm_f16): b < n_full is whole
-// tile b; otherwise piece (b - n_full) % S of split tile n_full + (b - n_full) / S.  Tile t
-// is row tile t / G, column group t % G (columns 128 g ..).
-struct GemmJobs {
-    int G;        // column groups
-    int n_full;   // whole tiles
-    int S;        // pieces per split tile
-    int n_jobs;   // workgroups
-};
-
 template <bool C_F16>
 __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restrict__ A, int lda,
                                                        const uint8_t* __restrict__ W, void* __restrict__ C,
@@ -123,27 +113,9 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
     auto Bs = [&](int buf) { return smem + kABuf * BM * ROWB + buf * (BN * ROWB); };
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // workgroups are dispatched round robin over 8 XCDs: within the whole-tile jobs and
-    // within the pieces, consecutive jobs are placed on one XCD
-    int job = blockIdx.x;
-    {
-        const int lo = job < J.n_full ? 0 : J.n_full;
-        const int n = job < J.n_full ? J.n_full : J.n_jobs - J.n_full;
-        const int i = job - lo;
-        if (n % 8 == 0 && lo % 8 == 0) job = lo + (i % 8) * (n / 8) + i / 8;
-    }
     const int nbk = K >> 7;
-    int tile, kb0, nb;
-    if (job < J.n_full) {
-        tile = job;
-        kb0 = 0;
-        nb = nbk;
-    } else {
-        const int j = job - J.n_full, piece = j % J.S;
-        tile = J.n_full + j / J.S;
-        kb0 = (int)(((long)piece * nbk) / J.S);
-        nb = (int)(((long)(piece + 1) * nbk) / J.S) - kb0;
-    }
+    int job, tile, kb0, nb;
+    gemm_job(J, nbk, job, tile, kb0, nb);
     const int m0 = (tile / J.G) * BM;
     const int n0 = (tile % J.G) * BN;
     const int R = min(BN, N - n0);              // columns of this tile
@@ -337,112 +309,63 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
     }
 }
 
-// C[m][n] for the split tiles: the sum of the tile's pieces in piece order.  One thread
-// per 4 consecutive columns of a tile row.
-template <bool C_F16>
-__global__ __launch_bounds__(256) void k_gemm_pieces_sum(const float* __restrict__ ws, void* __restrict__ C, int ldc,
-                                                         int M, int N, GemmJobs J) {
-    const int t = J.n_full + blockIdx.y;                    // split tile
-    const int e = blockIdx.x * 256 + threadIdx.x;           // quad of the tile, < BM * BN / 4
-    const int r = e / (BN / 4), c4 = (e % (BN / 4)) * 4;
-    const int gm = (t / J.G) * BM + r, gn0 = (t % J.G) * BN + c4;
-    if (gm >= M) return;
-    const float* P = ws + (size_t)blockIdx.y * J.S * (BM * BN) + r * BN + c4;
-    float4 s = *(const float4*)P;
-    for (int p = 1; p < J.S; p++) {
-        const float4 v = *(const float4*)(P + (size_t)p * (BM * BN));
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
-    }
-    const float v[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        if (gn0 + i < N) {
-            if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn0 + i] = (_Float16)v[i];
-            else ((float*)C)[(size_t)gm * ldc + gn0 + i] = v[i];
-        }
-    }
-}
-
 }  // namespace
 
-namespace {
-
-struct DeviceWs {
-    int n_cu = 0;
-    float* ws = nullptr;                         // n_cu fp32 tiles of split-tile pieces
-    bool attr_done = false;
-};
-
-DeviceWs& device_ws(int dev) {
-    static DeviceWs tab[64];
-    return tab[dev & 63];
-}
-
-}  // namespace
-
-// The schedule: T tiles; the whole rounds of n_cu tiles go to one workgroup each, the
-// remaining r tiles are split into S = min(n_cu / r, kMaxPieces, blocks) pieces each.  The
-// pieces' workspace (at most n_cu fp32 tiles, 128 KB each) is allocated on a device's
-// first call and kept; calls on one device share it and must not overlap in time.
-hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
-                           int M, int K, int N, hipStream_t s) {
+hipError_t gemm_device(bool need_ws, int* n_cu, float** ws) {
+    struct Dev {
+        int n_cu = 0;
+        float* ws = nullptr;
+    };
+    static Dev tab[64];
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    DeviceWs& D = device_ws(dev);
+    Dev& D = tab[dev & 63];
     if (!D.n_cu) {
         int n = 0;
         e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
         D.n_cu = n > 0 ? n : 256;
     }
-    if (!D.attr_done) {
-        e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kLdsBytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    kLdsBytes);
-        if (e != hipSuccess) return e;
-        D.attr_done = true;
-    }
-    const int mt = (M + BM - 1) / BM;
-    GemmJobs J;
-    J.G = (N + BN - 1) / BN;
-    const long T = (long)mt * J.G;
-    const int nbk = K / 128;
-    long rem = T % D.n_cu;
-    int S = rem ? std::min(std::min(D.n_cu / (int)rem, kMaxPieces), nbk) : 1;
-    if (S < 2) {
-        S = 1;
-        rem = 0;
-    }
-    J.n_full = (int)(T - rem);
-    J.S = S;
-    J.n_jobs = (int)(J.n_full + rem * S);
-    if (rem && !D.ws) {
-        e = hipMalloc((void**)&D.ws, (size_t)D.n_cu * BM * BN * sizeof(float));
+    if (need_ws && !D.ws) {
+        e = hipMalloc((void**)&D.ws, (size_t)D.n_cu * 256 * 128 * sizeof(float));
         if (e != hipSuccess) {
             D.ws = nullptr;
             return e;
         }
     }
+    *n_cu = D.n_cu;
+    *ws = D.ws;
+    return hipSuccess;
+}
+
+hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
+                           int M, int K, int N, hipStream_t s) {
+    static bool attr_done = false;
+    if (!attr_done) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    kLdsBytes);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    int n_cu = 0;
+    float* ws = nullptr;
+    hipError_t e = gemm_device(false, &n_cu, &ws);
+    if (e != hipSuccess) return e;
+    const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, n_cu);   // one workgroup per CU
+    if (J.n_jobs > J.n_full && (e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
         hipLaunchKernelGGL(k_gemm_ptq1_f16<true>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W,
-                           C, ldc, D.ws, M, K, N, J);
+                           C, ldc, ws, M, K, N, J);
     else
         hipLaunchKernelGGL(k_gemm_ptq1_f16<false>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, (const _Float16*)A, lda,
-                           W, C, ldc, D.ws, M, K, N, J);
+                           W, C, ldc, ws, M, K, N, J);
     e = hipGetLastError();
-    if (e != hipSuccess || !rem) return e;
-    const dim3 grid(BM * BN / 4 / 256, (unsigned)rem);
-    if (c_dtype == 1)
-        hipLaunchKernelGGL(k_gemm_pieces_sum<true>, grid, dim3(256), 0, s, D.ws, C, ldc, M, N, J);
-    else
-        hipLaunchKernelGGL(k_gemm_pieces_sum<false>, grid, dim3(256), 0, s, D.ws, C, ldc, M, N, J);
-    return hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_pieces_sum<BM, BN>(ws, C, c_dtype, ldc, M, N, J, s);
 }
 
 }  // namespace kata

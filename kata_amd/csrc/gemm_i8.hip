@@ -13,6 +13,7 @@
 // the group's int32 result into fp32 accumulators with the row/column scales.
 #include "common.h"
 #include "launch.h"
+#include "gemm_sched.h"
 
 namespace kata {
 
@@ -88,15 +89,18 @@ constexpr int LDB_S = BK + 16;   // bytes per LDS row
 template <bool C_F16>
 __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__ A8, const float* __restrict__ SX,
                                                       int ldS, const uint8_t* __restrict__ W, void* __restrict__ C,
-                                                      int ldc, int M, int K, int N) {
+                                                      int ldc, float* __restrict__ ws, int M, int K, int N,
+                                                      GemmJobs J) {
     __shared__ int8_t As[BM * LDB_S];
     __shared__ int8_t Bs[BN * LDB_S];
     __shared__ float sws[BN];
     __shared__ float sxs[BM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int nb = K / kGroup;
+    int job, tile, kb_lo, kb_n;
+    gemm_job(J, nb, job, tile, kb_lo, kb_n);
+    const int m0 = (tile / J.G) * BM, n0 = (tile % J.G) * BN;
     const int l16 = lane & 15, lg = lane >> 4;
 
     v4f acc[4][4];
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__
 #pragma unroll
         for (int jx = 0; jx < 4; jx++) acc[i][jx] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = 0; kb < nb; ++kb) {
+    for (int kb = kb_lo; kb < kb_lo + kb_n; ++kb) {
         __syncthreads();
         {
             const int r = tid >> 1, h = tid & 1;
@@ -182,6 +186,20 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__
                     acc[i][jx][r] += (float)ia[i][jx][r] * (sw * sxs[wm * 64 + i * 16 + lg * 4 + r]);
         }
     }
+    if (job >= J.n_full) {
+        // a piece: the whole fp32 tile, [128][128], into its workspace slot
+        float* P = ws + (size_t)(job - J.n_full) * (BM * BN);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jx = 0; jx < 4; jx++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float v = acc[i][jx][r];
+                    P[(wm * 64 + i * 16 + lg * 4 + r) * BN + wn * 64 + jx * 16 + l16] = v;
+                }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -207,14 +225,24 @@ hipError_t launch_quant_rows(const uint16_t* X, int8_t* Q, float* SX, int M, int
     return hipGetLastError();
 }
 
+// Two workgroups are resident per CU (their registers), so the schedule fills 2 n_cu slots.
 hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C, int c_dtype,
                           int ldc, int M, int K, int N, hipStream_t s) {
-    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM), block(256);
+    int n_cu = 0;
+    float* ws = nullptr;
+    hipError_t e = gemm_device(false, &n_cu, &ws);
+    if (e != hipSuccess) return e;
+    const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, 2 * n_cu);
+    if (J.n_jobs > J.n_full && (e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
-        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, grid, block, 0, s, A8, SX, ldS, W, C, ldc, M, K, N);
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, dim3(J.n_jobs), dim3(256), 0, s, A8, SX, ldS, W, C, ldc, ws, M, K, N,
+                           J);
     else
-        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, grid, block, 0, s, A8, SX, ldS, W, C, ldc, M, K, N);
-    return hipGetLastError();
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, dim3(J.n_jobs), dim3(256), 0, s, A8, SX, ldS, W, C, ldc, ws, M, K,
+                           N, J);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_pieces_sum<BM, BN>(ws, C, c_dtype, ldc, M, N, J, s);
 }
 
 }  // namespace kata

@@ -173,6 +173,18 @@ def test_gemm_i8_golden_and_random(dev, golden):
 
 
 # ----------------------------------------------------------------------------- dispatcher
+def test_gemm_i8_tile_schedules(dev):
+    """int8 GEMM over whole tiles plus K-pieces (513 tiles of 128x128 on 2 x 256 slots) and
+    pieces only, back to back; vs the oracle's int8 path."""
+    for M, K, N in ((128, 256, 128 * 513 - 7), (200, 1280, 300)):
+        W_np, _, _ = orc.synth_ptq1(N, K, M + K + N + 5)
+        A = torch.from_numpy(orc.synth_x(M, K, M + 9)).to(dev)
+        Q, SX = ops.quant_rows(A)
+        C = ops.gemm_ptq1_i8(Q, SX, torch.from_numpy(W_np).to(dev), K, N).cpu().numpy()
+        ref = orc.gemm_i8(Q.cpu().numpy(), SX.cpu().numpy(), W_np, M, K, N)
+        assert rel_l2(C, ref).max() < 1e-6, (M, K, N)
+
+
 def test_dispatch_offsets_and_i8_selection(dev):
     K, N = 1024, 64
     W1, _, _ = orc.synth_ptq1(N, K, 21)
