@@ -109,36 +109,44 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__
 #pragma unroll
         for (int jx = 0; jx < 4; jx++) acc[i][jx] = v4f{0.f, 0.f, 0.f, 0.f};
 
+    // the operands of the next group are loaded into registers while the matrix cores work
+    // on the current one: thread -> 64 bytes of A row tid / 2 and the 7 dwords of W row
+    // tid / 2's block (thread tid < BM also the row scale of A row tid)
+    const int lr = tid >> 1, lh = tid & 1;
+    const bool a_ok = m0 + lr < M, w_ok = n0 + lr < N, s_ok = tid < BM && m0 + tid < M;
+    const uint4* asrc = (const uint4*)(A8 + (size_t)min(m0 + lr, M - 1) * K + lh * 64);
+    const uint32_t* wsrc = (const uint32_t*)(W + (size_t)min(n0 + lr, N - 1) * nb * kBlockBytes);   // 4-byte aligned
+    uint4 pa[4];
+    uint32_t pw[7];
+    float psx = 0.0f;
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) pa[c] = asrc[kb * (BK / 16) + c];
+#pragma unroll
+        for (int i = 0; i < 7; i++) pw[i] = wsrc[kb * 7 + i];
+        if (tid < BM) psx = SX[(size_t)kb * ldS + min(m0 + tid, M - 1)];
+    };
+    fetch(kb_lo);
     for (int kb = kb_lo; kb < kb_lo + kb_n; ++kb) {
-        __syncthreads();
+        __syncthreads();                         // the previous group's LDS tiles are consumed
         {
-            const int r = tid >> 1, h = tid & 1;
-            const int gm = m0 + r;
-            uint4* dst = (uint4*)(As + r * LDB_S + h * 64);
-            if (gm < M) {
-                const uint4* src = (const uint4*)(A8 + (size_t)gm * K + (size_t)kb * BK + h * 64);
+            uint4* dst = (uint4*)(As + lr * LDB_S + lh * 64);
 #pragma unroll
-                for (int c = 0; c < 4; c++) dst[c] = src[c];
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; c++) dst[c] = make_uint4(0, 0, 0, 0);
-            }
-            if (tid < BM) sxs[tid] = (m0 + tid < M) ? SX[(size_t)kb * ldS + m0 + tid] : 0.0f;
+            for (int c = 0; c < 4; c++) dst[c] = a_ok ? pa[c] : make_uint4(0, 0, 0, 0);
+            if (tid < BM) sxs[tid] = s_ok ? psx : 0.0f;
         }
         // B tile: thread -> 4 of the 8 16-byte chunks (16 k each) of tile row tid / 2
         {
-            const int r = tid >> 1, gn = n0 + r;
-            uint4* brow = (uint4*)(Bs + r * LDB_S);
-            if (gn < N) {
-                const uint8_t* blk = W + ((size_t)gn * nb + kb) * kBlockBytes;
-                const uint32_t* bw = (const uint32_t*)blk;   // blocks are 4-byte aligned (W is, 28 = 4 * 7)
-                const uint32_t w0 = bw[0], w1 = bw[1], w2 = bw[2], w3 = bw[3], w4 = bw[4], w5 = bw[5], w6 = bw[6];
-                if ((tid & 1) == 0) {
+            uint4* brow = (uint4*)(Bs + lr * LDB_S);
+            if (w_ok) {
+                const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[2], w3 = pw[3], w4 = pw[4], w5 = pw[5], w6 = pw[6];
+                if (lh == 0) {
                     // chunks 0..3: dwords 0..3 at digit c
 #pragma unroll
                     for (int c = 0; c < 4; c++)
                         brow[c] = make_uint4(trits4(w0, p3x2(c), p3x2(c)), trits4(w1, p3x2(c), p3x2(c)),
                                              trits4(w2, p3x2(c), p3x2(c)), trits4(w3, p3x2(c), p3x2(c)));
+                    sws[lr] = half_bits_to_float(w6 >> 16);
                 } else {
                     brow[4] = make_uint4(trits4(w0, p3x2(4), p3x2(4)), trits4(w1, p3x2(4), p3x2(4)),
                                          trits4(w2, p3x2(4), p3x2(4)), trits4(w3, p3x2(4), p3x2(4)));
@@ -150,13 +158,13 @@ __global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__
                     brow[7] = make_uint4(trits4(w4, p3x2(4), p3x2(4)), trits4(w5, p3x2(4), p3x2(4)),
                                          trits4(qh, p3x2(0), p3x2(1)), trits4(qh, p3x2(2), p3x2(3)));
                 }
-                if ((tid & 1) == 0) sws[r] = half_bits_to_float(w6 >> 16);
             } else {
 #pragma unroll
-                for (int c = 0; c < 4; c++) brow[4 * (tid & 1) + c] = make_uint4(0, 0, 0, 0);
-                if ((tid & 1) == 0) sws[r] = 0.0f;
+                for (int c = 0; c < 4; c++) brow[4 * lh + c] = make_uint4(0, 0, 0, 0);
+                if (lh == 0) sws[lr] = 0.0f;
             }
         }
+        if (kb + 1 < kb_lo + kb_n) fetch(kb + 1);
         __syncthreads();
         v4i ia[4][4];
 #pragma unroll
