@@ -130,6 +130,30 @@ def test_gemm_f16_tile_schedules(dev):
         assert rel_l2(C.cpu().numpy(), ref.cpu().numpy()).max() < 5e-5, (M, K, N)
 
 
+@pytest.mark.parametrize("M", [1024, 7300])
+def test_gemm_config5_prefill_shapes(dev, M):
+    """BASELINE config 5 prefill: a 7300-token prompt as one GEMM and as the reference's
+    1024-row chunk, gate shape, on the fp16 exact path and on the int8 FFN path.  References:
+    torch fp32 on the bit-exact expanded weights; for int8 the per-group integer sums come
+    from fp32 matmuls of integer values (exact below 2^24) and fold in ascending group order."""
+    K, N = 5120, 17408
+    W_np, _, _ = orc.synth_ptq1(N, K, 5005)
+    W = torch.from_numpy(W_np).to(dev)
+    A = torch.from_numpy(orc.synth_x(M, K, 5006)).to(dev)
+    C = ops.gemm_ptq1_f16(A, W, K, N)
+    ref = A.float() @ ops.expand_f16(W, K, N).float().T
+    assert rel_l2(C.cpu().numpy(), ref.cpu().numpy()).max() < 5e-5
+    del ref
+    Q, SX = ops.quant_rows(A)
+    C8 = ops.gemm_ptq1_i8(Q, SX, W, K, N)
+    T8, SW = ops.expand_i8(W, K, N)
+    ref8 = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    for g in range(K // 128):
+        I = Q[:, 128 * g:128 * (g + 1)].float() @ T8[:, 128 * g:128 * (g + 1)].float().T
+        ref8 += I * (SW[:, g][None, :] * SX[g, :M][:, None])
+    assert rel_l2(C8.cpu().numpy(), ref8.cpu().numpy()).max() < 1e-5
+
+
 # ----------------------------------------------------------------------------- int8 path
 def test_quant_rows_bit_exact(dev, golden):
     Q, SX = ops.quant_rows(torch.from_numpy(golden["qr_X"]).to(dev))
