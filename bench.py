@@ -67,6 +67,97 @@ def make_weights(torch, dev, K, N, seed, ops):
     return torch.from_numpy(ops.pack_ptq1(trits, scales)).to(dev)
 
 
+def device_weights(torch, dev, K, N, gen):
+    """A packed PTQ1_0 matrix drawn on the device with the same distribution: iid uniform
+    trits are iid uniform qs bytes in [0, 243) and qh bytes in [0, 81); d = fp16 |N(0, 0.02)|."""
+    nb = K // 128
+    blk = torch.empty((N, nb, 28), dtype=torch.uint8, device=dev)
+    blk[:, :, :24] = torch.randint(0, 243, (N, nb, 24), generator=gen, device=dev, dtype=torch.uint8)
+    blk[:, :, 24:26] = torch.randint(0, 81, (N, nb, 2), generator=gen, device=dev, dtype=torch.uint8)
+    d = (torch.randn((N, nb), generator=gen, device=dev) * 0.02).abs().half()
+    blk[:, :, 26:28] = d.view(torch.uint8).view(N, nb, 2)
+    return blk.view(N, nb * 28)
+
+
+# 64-layer trunk of the 27B model (48 gated-DeltaNet + 16 GQA layers, each with an FFN) and
+# the lm_head, as the decode step launches them (inputs shared by qkv+z, q+k+v, gate+up)
+GDN_LAUNCHES = [(5120, (10240, 6144)), (6144, (5120,)), (5120, (17408, 17408)), (17408, (5120,))]
+GQA_LAUNCHES = [(5120, (12288, 1024, 1024)), (6144, (5120,)), (5120, (17408, 17408)), (17408, (5120,))]
+LM_HEAD = (5120, (248320,))
+
+
+def run_config5(torch, ops, dev, stream):
+    """one bs=1 decode pass over all 64 layers + lm_head (5.6 GB of
+    ternary weights, far above the Infinity Cache) and the 7300-token prefill GEMMs (as one
+    GEMM and as 1024-row chunks), fp16 exact and int8 paths."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 900)
+    layers = [GDN_LAUNCHES] * 48 + [GQA_LAUNCHES] * 16
+    launches = [(K, [device_weights(torch, dev, K, N, gen) for N in Ns], Ns) for L in layers for K, Ns in L]
+    launches.append((LM_HEAD[0], [device_weights(torch, dev, LM_HEAD[0], LM_HEAD[1][0], gen)], LM_HEAD[1]))
+    total = sum(w.numel() for _, ws, _ in launches for w in ws)
+    xs = {K: torch.randn((1, K), generator=gen, device=dev).half() for K in (5120, 6144, 17408)}
+    ys = {N: torch.empty((1, N), dtype=torch.float32, device=dev) for N in (1024, 5120, 6144, 10240, 12288, 17408, 248320)}
+
+    def sweep():
+        for K, ws, Ns in launches:
+            if len(ws) == 1:
+                ops.gemv_ptq1(ws[0], xs[K], K, Ns[0], 1, out=ys[Ns[0]])
+            else:
+                ops.gemv_ptq1_batch(ws, xs[K], K, list(Ns), 1, outs=[ys[N] for N in Ns])
+    sweep()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        sweep()
+        b.record(stream)
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    ms = sorted(times)[len(times) // 2]
+    out = {"decode_64_layers": {"bytes": total, "launches": len(launches), "ms_median_of_5": round(ms, 3),
+                                "GBps": round(total / (ms * 1e-3) / 1e9, 1)}}
+    del launches
+    # 7300-token prefill, gate and down shapes
+    M = 7300
+    pre = {}
+    for name, K, N in (("ffn_gate", 5120, 17408), ("ffn_down", 17408, 5120)):
+        W = device_weights(torch, dev, K, N, gen)
+        A = torch.randn((M, K), generator=gen, device=dev).half()
+        C = torch.empty((M, N), dtype=torch.float16, device=dev)
+        Q = torch.empty((M, K), dtype=torch.int8, device=dev)
+        SX = torch.empty((K // 128, M), dtype=torch.float32, device=dev)
+
+        def timed(fn, nrep=5):
+            fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(nrep):
+                fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) * 1e3 / nrep
+
+        def chunks_f16():
+            for m0 in range(0, M, 1024):
+                ops.gemm_ptq1_f16(A[m0:m0 + 1024], W, K, N, out=C[m0:m0 + 1024])
+
+        us = timed(lambda: ops.gemm_ptq1_f16(A, W, K, N, out=C))
+        us_c = timed(chunks_f16)
+        ops.quant_rows(A, out=(Q, SX))
+        us_i8 = timed(lambda: ops.gemm_ptq1_i8(Q, SX, W, K, N, out=C))
+        fl = 2.0 * M * N * K
+        pre[name] = {"M": M, "K": K, "N": N, "f16_us": round(us, 1), "f16_TFLOPS": round(fl / (us * 1e-6) / 1e12, 1),
+                     "f16_1024_chunks_us": round(us_c, 1),
+                     "i8_us": round(us_i8, 1), "i8_TOPS": round(fl / (us_i8 * 1e-6) / 1e12, 1)}
+        del W, A, C, Q, SX
+    out["prefill_m7300"] = pre
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(sample_rows: int, threads: int):
     """Times the reference's host decode + fp32 dot on `sample_rows` rows of every sweep
     matrix (same shapes and distributions), returns GB/s of packed bytes."""
@@ -81,6 +172,22 @@ def cpu_baseline(sample_rows: int, threads: int):
         total_t += time.perf_counter() - t0
         total_bytes += packed_bytes(K, rows)
     return total_bytes / total_t / 1e9, total_bytes
+
+
+def cpu_gemm_baseline(threads: int, rows: int = 512):
+    """The pp512 gate GEMM on the host (decode each weight row to fp32 once, fp32 dots against
+    the 512 activation rows, OpenMP over weight rows) on its first `rows` weight rows."""
+    from oracle import oracle as orc
+    M, K, N = 512, 5120, 17408
+    W, _, _ = orc.synth_ptq1(rows, K, SEED + 3000)
+    A = orc.synth_x(M, K, SEED + 3001)
+    out = {"unit": "GFLOP/s", "sample": f"M={M}, K={K}, first {rows} of the N={N} gate rows"}
+    for key, th in (("value", threads), ("single_thread", 1)):
+        t0 = time.perf_counter()
+        orc.cpu_gemm_f32(A, W, M, K, rows, 0, rows, th)
+        out[key] = round(2.0 * M * K * rows / (time.perf_counter() - t0) / 1e9, 2)
+    out["cores"] = threads
+    return out
 
 
 def run_gemm(torch, ops, dev, stream, copies, ncopies):
@@ -139,6 +246,7 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=2048)
     ap.add_argument("--graph", action="store_true",
                     help="replay each step's HIP graph instead of launching its GEMVs from Python")
+    ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer sweep and the M=7300 GEMMs")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the pp512 prefill GEMMs (for counter runs), then exit")
     ap.add_argument("--step-only", action="store_true",
@@ -309,14 +417,24 @@ def main():
     # ---- pp512 prefill GEMM (config 4), fp16 exact path
     gemm = None if args.no_gemm else run_gemm(torch, ops, dev, stream, copies, ncopies)
 
+    # ---- config 5: full 64-layer decode pass, M=7300 prefill
+    cfg5 = None
+    if not args.no_config5:
+        cfg5 = run_config5(torch, ops, dev, stream)
+
     # ---- CPU baseline (reference host arithmetic, bounded sample)
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         gbs, nbytes = cpu_baseline(args.cpu_rows, threads)
+        gbs1, nbytes1 = cpu_baseline(max(64, args.cpu_rows // 8), 1)
         cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": f"first {args.cpu_rows} rows of each of the 10 sweep matrices "
-                         f"({nbytes/1e6:.1f} MB packed), fp32 decode+dot, OpenMP over rows"}
+                         f"({nbytes/1e6:.1f} MB packed), fp32 decode+dot, OpenMP over rows",
+               "single_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
+                                 "sample": f"first {max(64, args.cpu_rows // 8)} rows of each sweep matrix "
+                                           f"({nbytes1/1e6:.1f} MB)"},
+               "prefill_gemm": cpu_gemm_baseline(threads)}
 
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary
     traffic = None
@@ -353,6 +471,7 @@ def main():
         "verify_t2": verify_t2,
         "q8_0_t1": q8,
         "prefill_gemm": gemm,
+        "config5": cfg5,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -391,6 +391,55 @@ void orc_cpu_gemv_ptq1_f32(const uint8_t* W, const float* x, float* y, int K, in
     }
 }
 
+/* CPU baseline of the prefill GEMM (k_gemm_f16 semantics after k_expand_ptq1_v2,
+ * shaders/prefill.metal:31-41,472-479): each weight row n in [row0, row0+nrows) is decoded
+ * once to fp32 (half(t*d) is exact), then C[m][n] = sum_k A[m][k]*w[k] in fp32 for every A
+ * row.  OpenMP over weight rows; a bounded sample of columns can be timed.               */
+void orc_cpu_gemm_ptq1_f32(const uint16_t* A, const uint8_t* W, float* C, int M, int K, int N, int row0,
+                           int nrows, int nthreads) {
+    const int nb = K / ORC_GROUP;
+    float* af = (float*)malloc((size_t)M * K * 4);
+    for (size_t i = 0; i < (size_t)M * K; i++) af[i] = orc_half_to_float(A[i]);
+    const int nq = (nrows + 3) / 4;              /* quads of weight rows: each A row is read once per quad */
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        float* w = (float*)malloc((size_t)4 * K * 4);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int q = 0; q < nq; q++) {
+            const int n0 = row0 + 4 * q, nr = (4 < row0 + nrows - n0) ? 4 : row0 + nrows - n0;
+            for (int r = 0; r < 4; r++) {
+                const int n = n0 + (r < nr ? r : 0);
+                const uint8_t* row = W + (size_t)n * nb * ORC_BLOCK_BYTES;
+                for (int b = 0; b < nb; b++) {
+                    const uint8_t* blk = row + (size_t)b * ORC_BLOCK_BYTES;
+                    const float d = orc_ptq1_scale(blk);
+                    for (int e = 0; e < ORC_GROUP; e++)
+                        w[(size_t)r * K + b * ORC_GROUP + e] = (float)orc_ptq1_elem_trit(blk, e) * d;
+                }
+            }
+            for (int m = 0; m < M; m++) {
+                const float* ar = af + (size_t)m * K;
+                float acc[4][16] = {{0}};        /* 4 rows x 16 lanes: 8 vector accumulators */
+                for (int k = 0; k < K; k += 16)
+                    for (int r = 0; r < 4; r++)
+                        for (int j = 0; j < 16; j++) acc[r][j] += ar[k + j] * w[(size_t)r * K + k + j];
+                for (int r = 0; r < nr; r++) {
+                    float s = 0.0f;
+                    for (int j = 0; j < 16; j++) s += acc[r][j];
+                    C[(size_t)m * N + n0 + r] = s;
+                }
+            }
+        }
+        free(w);
+    }
+    free(af);
+}
+
 int orc_omp_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -56,6 +56,7 @@ def lib():
             "orc_expand_ptq1_i8": (None, [P, P, P, i, i]),
             "orc_gemm_i8": (None, [P, P, i, P, P, P, i, i, i]),
             "orc_cpu_gemv_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
+            "orc_cpu_gemm_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
             "orc_omp_max_threads": (i, []),
         }
         for name, (res, args) in sig.items():
@@ -163,6 +164,15 @@ def gemm_i8(A8, SX, W, M, K, N, want_group_sums=False):
     GS = np.empty((M, N, K // GROUP), np.int32) if want_group_sums else None
     lib().orc_gemm_i8(_p(A8), _p(SX), ldS, _p(W), _p(C), _p(GS) if GS is not None else None, M, K, N)
     return (C, GS) if want_group_sums else C
+
+
+def cpu_gemm_f32(A, W, M, K, N, row0, nrows, nthreads):
+    """CPU baseline GEMM (fp32) over weight rows [row0, row0 + nrows); C is [M][N]."""
+    A = np.ascontiguousarray(A, dtype=np.float16).view(np.uint16)
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    C = np.zeros((M, N), np.float32)
+    lib().orc_cpu_gemm_ptq1_f32(_p(A), _p(W), _p(C), M, K, N, row0, nrows, nthreads)
+    return C
 
 
 def cpu_gemv_f32(W, x, K, N, T, row0, nrows, nthreads):

@@ -205,3 +205,14 @@ def test_expand_i8_and_gemm_i8_golden(golden):
     want = (GS.astype(np.float64) * SW.astype(np.float64)[None, :, :]
             * golden["qr_SX"].T.astype(np.float64)[:, None, :]).sum(-1)
     np.testing.assert_allclose(C, want, rtol=1e-6, atol=1e-7)
+
+
+def test_cpu_baseline_gemm_matches_oracle_gemm():
+    """The bench's CPU GEMM baseline (fp32, tiled over weight rows) computes the same
+    products as the double-precision oracle GEMM, on a ragged row count."""
+    M, K, N = 37, 640, 23
+    W, _, _ = orc.synth_ptq1(N, K, 71)
+    A = orc.synth_x(M, K, 72)
+    C = orc.cpu_gemm_f32(A, W, M, K, N, 0, N, 2)
+    R = orc.gemm_f16(A, W, M, K, N)
+    assert np.abs(C - R).max() <= 1e-5 * np.abs(R).max()
