@@ -414,6 +414,23 @@ def main():
         q8[name] = {"K": K, "N": N, "us": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
         del Wqs, Wq
 
+    # ---- matmul input transform (residual add + RMSNorm + sign + FWHT), decode and prefill
+    xform = {}
+    for label, M in (("decode_m1", 1), ("prefill_m7300", 7300)):
+        W = 5120
+        xt = torch.randn((M, W), device=dev)
+        yt = torch.randn((M, W), device=dev)
+        gt = torch.sign(torch.randn(W, device=dev))
+        outt = torch.empty((M, W), dtype=torch.float16, device=dev)
+        xn = torch.empty_like(xt)
+
+        def xf(r, xt=xt, yt=yt, gt=gt, outt=outt, xn=xn, W=W, M=M):
+            ops.lib().kata_add_rms_fwht(ops._ptr(xt), ops._ptr(yt), ops._ptr(gt), ops._ptr(outt), 1, 0, ops._ptr(xn),
+                                        None, None, 0, W, M, ops._stream(xt))
+        us = time_reps(xf, 50 if M > 1 else args.reps)
+        nbytes = M * W * (4 + 4 + 4 + 2)              # x, y in; xnew fp32, out fp16 out
+        xform[label] = {"M": M, "W": W, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
     # ---- pp512 prefill GEMM (config 4), fp16 exact path
     gemm = None if args.no_gemm else run_gemm(torch, ops, dev, stream, copies, ncopies)
 
@@ -471,6 +488,7 @@ def main():
         "verify_t2": verify_t2,
         "q8_0_t1": q8,
         "prefill_gemm": gemm,
+        "input_transform": xform,
         "config5": cfg5,
         "cpu_baseline": cpu,
     }

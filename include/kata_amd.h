@@ -107,6 +107,26 @@ int kata_gemm_ptq1_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t*
 int kata_expand_ptq1_f16(const uint8_t* W, uint16_t* out, int K, int N, void* stream);
 int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, void* stream);
 
+/* ---------------------------------------------------------------- matmul input -------
+ * The transform every ternary matmul input goes through (the model's rotated basis), per
+ * token row m < M of width W (W % 1024 == 0), fp32 arithmetic:
+ *   v = x + y (y may be NULL), xnew = v (may be NULL), inv = 1/sqrt(mean(v^2) + 1e-6),
+ *   hout = v * inv * gamma (gamma and hout both NULL or both set; hout_dtype F32 or F16),
+ *   out[b][j] = (1/32) sum_k (-1)^popcount(j & k) * (v * inv * gs)[1024 b + k]
+ * (gs = the sign vector with the RMSNorm weight folded in).  out is fp32 or fp16 rows
+ * [M][W], or for M == 2 fp16 with the two tokens interleaved, [W][2] (KATA_X_HALF2, the
+ * half2 operand of the T = 2 GEMV).  All vectors 16-byte aligned.
+ * Replaces k_add_rms_fwht (shaders/ops.metal:86-106), k_add_rms_fwht_b and
+ * k_add_rms_fwht_t (shaders/prefill.metal:59-78,266-285). */
+int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out, int out_dtype, int out_layout,
+                      float* xnew, const float* gamma, void* hout, int hout_dtype, int W, int M, void* stream);
+/* The other input transforms, same out formats: mode 0 RMSNorm of src (as above, no
+ * residual), 1 SwiGLU v = silu(src) * src2, 2 src in the grouped GDN head order
+ * (v[128 t + h] = src[h + 128 (t/3 + 16 (t%3))], W == 6144), 3 v = src; out = H(v * gs).
+ * Replaces k_rms_fwht (shaders/ops.metal:30-54) and k_rms_fwht_b (shaders/prefill.metal:81-97). */
+int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype, int out_layout,
+                  int W, int M, int mode, void* stream);
+
 /* ---------------------------------------------------------------- HOST packers -------
  * HOST: quantize_row_ptq1_0_ref over nrow rows of k floats (k % 128 == 0)
  * (docs/reference/prism_ptq1_0_quant_dequant.c:4-52, quantize_ptq1_0 :86-96). */

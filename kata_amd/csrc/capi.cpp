@@ -144,6 +144,47 @@ int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, v
     return check_launch(kata::launch_expand_i8(W, T8, SW, K, N, (hipStream_t)stream), "expand i8");
 }
 
+// ------------------------------------------------------------------ matmul input transform
+static int check_fwht_out(const void* out, int out_dtype, int out_layout, int W, int M) {
+    if (out_dtype != KATA_F32 && out_dtype != KATA_F16) return fail(KATA_EINVAL, "out_dtype=%d", out_dtype);
+    if (out_layout != KATA_X_ROWS && out_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "out_layout=%d", out_layout);
+    if (out_layout == KATA_X_HALF2 && (out_dtype != KATA_F16 || M != 2))
+        return fail(KATA_EINVAL, "the half2 layout is fp16 with M == 2");
+    if (W <= 0 || W % 1024 != 0) return fail(KATA_EINVAL, "W=%d must be a positive multiple of 1024", W);
+    if (M <= 0 || M > 65535) return fail(KATA_EINVAL, "M=%d out of range", M);
+    if (!aligned(out, 16)) return fail(KATA_EINVAL, "out must be 16-byte aligned");
+    return KATA_OK;
+}
+
+int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out, int out_dtype, int out_layout,
+                      float* xnew, const float* gamma, void* hout, int hout_dtype, int W, int M, void* stream) {
+    if (!x || !gs || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (int rc = check_fwht_out(out, out_dtype, out_layout, W, M)) return rc;
+    if ((gamma == nullptr) != (hout == nullptr)) return fail(KATA_EINVAL, "gamma and hout go together");
+    if (hout && hout_dtype != KATA_F32 && hout_dtype != KATA_F16) return fail(KATA_EINVAL, "hout_dtype=%d", hout_dtype);
+    if (!aligned(x, 16) || (y && !aligned(y, 16)) || !aligned(gs, 16) || (xnew && !aligned(xnew, 16)) ||
+        (gamma && !aligned(gamma, 16)) || (hout && !aligned(hout, 16)))
+        return fail(KATA_EINVAL, "vectors must be 16-byte aligned");
+    const int flags = (y ? 1 : 0) | (xnew ? 2 : 0) | (hout ? 4 : 0) | (hout && hout_dtype == KATA_F16 ? 8 : 0);
+    return check_launch(kata::launch_norm_fwht(x, y, gs, out, out_dtype, out_layout, xnew, gamma, hout, flags, W, M, 0,
+                                               (hipStream_t)stream),
+                        "add_rms_fwht");
+}
+
+int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype, int out_layout,
+                  int W, int M, int mode, void* stream) {
+    if (!src || !gs || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (mode < 0 || mode > 3) return fail(KATA_EINVAL, "mode=%d", mode);
+    if (mode == 1 && !src2) return fail(KATA_EINVAL, "mode 1 needs src2");
+    if (mode == 2 && W != 6144) return fail(KATA_EINVAL, "mode 2 (GDN head order) needs W == 6144");
+    if (int rc = check_fwht_out(out, out_dtype, out_layout, W, M)) return rc;
+    if (!aligned(src, 16) || (src2 && !aligned(src2, 16)) || !aligned(gs, 16))
+        return fail(KATA_EINVAL, "vectors must be 16-byte aligned");
+    return check_launch(kata::launch_norm_fwht(src, mode == 1 ? src2 : nullptr, gs, out, out_dtype, out_layout, nullptr,
+                                               nullptr, nullptr, 0, W, M, mode, (hipStream_t)stream),
+                        "rms_fwht");
+}
+
 // ------------------------------------------------------------------ host packers
 // Byte encoding of the quantiser (docs/reference/prism_ptq1_0_quant_dequant.c:20-46):
 // stages of 16 and 8 bytes carry 5 digits each (most significant first, element

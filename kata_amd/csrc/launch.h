@@ -29,4 +29,10 @@ hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint
 hipError_t launch_expand_f16(const uint8_t* W, uint16_t* out, int K, int N, hipStream_t s);
 hipError_t launch_expand_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, hipStream_t s);
 
+// ---- matmul input transform (norm_fwht.hip); flags: 1 add src2 (mode 0), 2 write xnew,
+// 4 write hout, 8 hout fp16
+hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype,
+                            int out_layout, float* xnew, const float* gamma, void* hout, int flags, int W, int M,
+                            int mode, hipStream_t s);
+
 }  // namespace kata

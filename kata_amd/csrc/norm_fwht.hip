@@ -1,0 +1,198 @@
+// Input transform of every ternary matmul: (residual add +) RMSNorm / SwiGLU / GDN head
+// permutation, times the sign vector, then the normalised 1024-point Walsh-Hadamard
+// transform of each 1024-block (the model's rotated basis).
+//
+// Semantics (shaders/common.h:20-42, shaders/ops.metal:30-54,86-106,
+// shaders/prefill.metal:59-97,266-285), per token row m and element i < W:
+//   mode 0: v = x + y (y optional), xnew = v, inv = 1/sqrt(mean(v^2) + 1e-6),
+//           u = v * inv * gs, hout = v * inv * gamma (optional)
+//   mode 1: u = silu(src) * src2 * gs          mode 2: u = src[perm(i)] * gs (GDN heads)
+//   mode 3: u = src * gs
+//   out[block b][j] = (1/32) sum_k (-1)^popcount(j & k) u[1024 b + k]
+// fp32 arithmetic; out fp32 or fp16, rows [M][W] or (M = 2) the two tokens interleaved
+// per element, [W][2] (the half2 operand of the T = 2 verify GEMV).
+//
+// Design: a 256-thread workgroup per (1024-block, token) for few rows (more workgroups in
+// flight; each reads the row for its sum of squares, L2-resident after the first), per
+// token row for many (the row read once, held in registers).  Element k = 4 tid + r of a
+// block: bits 0-1 are a thread's registers, bits 2-7 its lane (butterflies by cross-lane
+// exchange), bits 8-9 its wave (one LDS transpose).  The sum of squares is reduced in a
+// fixed order: a butterfly across the wave's lanes, then the 4 waves through LDS.
+#include "common.h"
+#include "launch.h"
+
+namespace kata {
+
+namespace {
+
+constexpr float kRmsEps = 1e-6f;   // config/kata_m6.h:21
+
+__device__ inline float wave_sum(float a) {
+    // fixed-order butterfly over the 64 lanes
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+    return a;
+}
+
+// natural-order butterflies: for bit h the pair (k, k | h) becomes (a + b, a - b)
+__device__ inline void fwht1024(float (&v)[4], int tid, float* xs) {
+    const int lane = tid & 63;
+    float a = v[0] + v[1], b = v[0] - v[1], c = v[2] + v[3], d = v[2] - v[3];
+    v[0] = a + c;
+    v[1] = b + d;
+    v[2] = a - c;
+    v[3] = b - d;
+#pragma unroll
+    for (int k = 0; k < 6; k++) {
+        const int m = 1 << k;
+        const bool hi = lane & m;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = __shfl_xor(v[r], m);
+            v[r] = hi ? p - v[r] : v[r] + p;
+        }
+    }
+    // bits 8-9: element k = 4 tid + r; thread t then owns elements t + 256 j (j = 0..3)
+#pragma unroll
+    for (int r = 0; r < 4; r++) xs[4 * tid + r] = v[r];
+    __syncthreads();
+    float e[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) e[j] = xs[tid + 256 * j];
+    const float a2 = e[0] + e[1], b2 = e[0] - e[1], c2 = e[2] + e[3], d2 = e[2] - e[3];
+    e[0] = a2 + c2;
+    e[1] = b2 + d2;
+    e[2] = a2 - c2;
+    e[3] = b2 - d2;
+#pragma unroll
+    for (int j = 0; j < 4; j++) xs[tid + 256 * j] = e[j];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; r++) v[r] = xs[4 * tid + r] * 0.03125f;
+}
+
+__device__ inline float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// GDN output order: element i of the grouped head layout reads tiled position
+// h + 128 (k + 16 rr) for i = 128 t + h, t = 3 k + rr (shaders/ops.metal:47)
+__device__ inline int gdn_perm(int i) {
+    const int h = i & 127, t = i >> 7, rr = t % 3, k = t / 3;
+    return h + 128 * (k + 16 * rr);
+}
+
+// flags: 1 = add y, 2 = write xnew, 4 = write hout, 8 = hout fp16.
+// NB blocks per workgroup: NB = 1 -> grid (W/1024, M), every block's workgroup reads the
+// row for the sum of squares (few rows: more workgroups in flight); NB = W/1024 -> grid M,
+// one workgroup per row, the row read once and held in registers (many rows).
+template <int NB>
+__global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src, const float* __restrict__ src2,
+                                                   const float* __restrict__ gs, void* __restrict__ out, int out_dtype,
+                                                   int out_layout, float* __restrict__ xnew,
+                                                   const float* __restrict__ gamma, void* __restrict__ hout,
+                                                   int flags, int W, int mode) {
+    __shared__ float xs[1024];
+    __shared__ float part[4];
+    const int tid = threadIdx.x;
+    const int m = NB == 1 ? blockIdx.y : blockIdx.x, blk0 = NB == 1 ? blockIdx.x : 0;
+    const size_t ro = (size_t)m * W;
+    // v = x (+ y) of this thread's elements 1024 (blk0 + b) + 4 tid + r, b < NB
+    float s[NB][4];
+    if (mode == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int base = (blk0 + b) * 1024 + 4 * tid;
+            const float4 a = *(const float4*)(src + ro + base);
+            float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (flags & 1) c = *(const float4*)(src2 + ro + base);
+            s[b][0] = a.x + c.x;
+            s[b][1] = a.y + c.y;
+            s[b][2] = a.z + c.z;
+            s[b][3] = a.w + c.w;
+        }
+    }
+    float inv = 1.0f;
+    if (mode == 0) {
+        float ss = 0.0f;
+        if (NB == 1) {
+            for (int i = 4 * tid; i < W; i += 1024) {
+                const float4 a = *(const float4*)(src + ro + i);
+                float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (flags & 1) c = *(const float4*)(src2 + ro + i);
+                const float v0 = a.x + c.x, v1 = a.y + c.y, v2 = a.z + c.z, v3 = a.w + c.w;
+                ss += (v0 * v0 + v1 * v1) + (v2 * v2 + v3 * v3);
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; b++) ss += (s[b][0] * s[b][0] + s[b][1] * s[b][1]) + (s[b][2] * s[b][2] + s[b][3] * s[b][3]);
+        }
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) part[tid >> 6] = ss;
+        __syncthreads();
+        inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)W + kRmsEps);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int base = (blk0 + b) * 1024 + 4 * tid;
+        float v[4];
+        const float4 g = *(const float4*)(gs + base);
+        const float gv[4] = {g.x, g.y, g.z, g.w};
+        if (mode == 0) {
+            if (flags & 2) *(float4*)(xnew + ro + base) = make_float4(s[b][0], s[b][1], s[b][2], s[b][3]);
+            if (flags & 4) {
+                const float4 gm = *(const float4*)(gamma + base);
+                const float h[4] = {s[b][0] * inv * gm.x, s[b][1] * inv * gm.y, s[b][2] * inv * gm.z, s[b][3] * inv * gm.w};
+                if (flags & 8) {
+                    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                    *(h4*)((_Float16*)hout + ro + base) = h4{(_Float16)h[0], (_Float16)h[1], (_Float16)h[2], (_Float16)h[3]};
+                } else {
+                    *(float4*)((float*)hout + ro + base) = make_float4(h[0], h[1], h[2], h[3]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = s[b][r] * inv * gv[r];
+        } else if (mode == 1) {
+            const float4 a = *(const float4*)(src + ro + base);
+            const float4 c = *(const float4*)(src2 + ro + base);
+            const float av[4] = {a.x, a.y, a.z, a.w}, cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = silu(av[r]) * cv[r] * gv[r];
+        } else if (mode == 2) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = src[ro + gdn_perm(base + r)] * gv[r];
+        } else {
+            const float4 a = *(const float4*)(src + ro + base);
+            const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = av[r] * gv[r];
+        }
+        fwht1024(v, tid, xs);
+        if (out_dtype == 0) {
+            *(float4*)((float*)out + ro + base) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if (out_layout == 0) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            *(h4*)((_Float16*)out + ro + base) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+        } else {
+            _Float16* o = (_Float16*)out;        // [W][2]: token m at 2 i + m
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[2 * (base + r) + m] = (_Float16)v[r];
+        }
+        if (NB > 1) __syncthreads();             // xs is reused by the next block's transform
+    }
+}
+
+}  // namespace
+
+hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype,
+                            int out_layout, float* xnew, const float* gamma, void* hout, int flags, int W, int M,
+                            int mode, hipStream_t s) {
+    // whole rows per workgroup once there are enough rows to fill the CUs (hidden width 5120)
+    if (W == 5120 && M >= 64)
+        hipLaunchKernelGGL(k_norm_fwht<5>, dim3(M), dim3(256), 0, s, src, src2, gs, out, out_dtype, out_layout, xnew,
+                           gamma, hout, flags, W, mode);
+    else
+        hipLaunchKernelGGL(k_norm_fwht<1>, dim3(W / 1024, M), dim3(256), 0, s, src, src2, gs, out, out_dtype,
+                           out_layout, xnew, gamma, hout, flags, W, mode);
+    return hipGetLastError();
+}
+
+}  // namespace kata

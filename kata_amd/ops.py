@@ -125,6 +125,35 @@ def expand_i8(W: torch.Tensor, K: int, N: int):
 
 
 # ----------------------------------------------------------------------------- host packers
+# ----------------------------------------------------------------------------- matmul input transform
+def add_rms_fwht(x: torch.Tensor, gs: torch.Tensor, y: torch.Tensor | None = None, gamma: torch.Tensor | None = None,
+                 out_dtype=torch.float32, half2: bool = False, want_xnew: bool = False, hout_dtype=torch.float32):
+    """Residual add + RMSNorm + sign + 1024-block FWHT of fp32 rows x [M][W] (k_add_rms_fwht):
+    returns (out, xnew or None, hout or None)."""
+    _need_gpu(x, gs)
+    M, W = x.shape
+    out = (torch.empty((W, 2), dtype=torch.float16, device=x.device) if half2
+           else torch.empty((M, W), dtype=out_dtype, device=x.device))
+    xnew = torch.empty_like(x) if want_xnew else None
+    hout = torch.empty((M, W), dtype=hout_dtype, device=x.device) if gamma is not None else None
+    check(lib().kata_add_rms_fwht(_ptr(x), _ptr(y), _ptr(gs), _ptr(out), KATA_F16 if out.dtype == torch.float16 else KATA_F32,
+                                  KATA_X_HALF2 if half2 else KATA_X_ROWS, _ptr(xnew), _ptr(gamma), _ptr(hout),
+                                  KATA_F16 if hout_dtype == torch.float16 else KATA_F32, W, M, _stream(x)))
+    return out, xnew, hout
+
+
+def rms_fwht(src: torch.Tensor, gs: torch.Tensor, mode: int, src2: torch.Tensor | None = None,
+             out_dtype=torch.float32, half2: bool = False):
+    """The other input transforms (k_rms_fwht): mode 0 RMSNorm, 1 SwiGLU, 2 GDN head order, 3 plain."""
+    _need_gpu(src, gs)
+    M, W = src.shape
+    out = (torch.empty((W, 2), dtype=torch.float16, device=src.device) if half2
+           else torch.empty((M, W), dtype=out_dtype, device=src.device))
+    check(lib().kata_rms_fwht(_ptr(src), _ptr(src2), _ptr(gs), _ptr(out), KATA_F16 if out.dtype == torch.float16 else KATA_F32,
+                              KATA_X_HALF2 if half2 else KATA_X_ROWS, W, M, mode, _stream(src)))
+    return out
+
+
 def _np_ptr(a: np.ndarray):
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(ctypes.c_void_p)

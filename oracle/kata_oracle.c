@@ -359,6 +359,70 @@ void orc_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, f
     free(t8); free(sw);
 }
 
+/* ---------------------------------------------------------------- matmul input --------
+ * The input transform of a ternary matmul, in double (shaders/ops.metal:30-54,86-106;
+ * shaders/common.h:20-42; shaders/prefill.metal:59-97,266-285).  Per row m:
+ *   mode 0: v = src (+ src2 when add), inv = 1/sqrt(mean(v^2) + 1e-6), u = v*inv*gs,
+ *           hout = v*inv*gamma (gamma non-NULL)
+ *   mode 1: u = silu(src)*src2*gs;  mode 2: u[i] = src[gdn_perm(i)]*gs[i];  mode 3: u = src*gs
+ *   out[1024 b + j] = (1/32) sum_k (-1)^popcount(j & k) u[1024 b + k]
+ * The transform is the textbook recursive (Sylvester) Walsh-Hadamard butterfly in natural
+ * order.  Pinned: against scipy.linalg.hadamard(1024) products, involution (H/32)^2 = I,
+ * and closed forms of the norm and SwiGLU on special inputs.                              */
+static void orc_fwht_d(double* v, int n) {
+    for (int h = 1; h < n; h <<= 1)
+        for (int i = 0; i < n; i += 2 * h)
+            for (int j = i; j < i + h; j++) {
+                const double a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+}
+
+static int orc_gdn_perm(int i) {
+    const int h = i & 127, t = i >> 7, rr = t % 3, k = t / 3;
+    return h + 128 * (k + 16 * rr);
+}
+
+void orc_norm_fwht(const float* src, const float* src2, const float* gs, const float* gamma, double* out,
+                   double* hout, int W, int M, int mode, int add) {
+    double* u = (double*)malloc((size_t)W * sizeof(double));
+    for (int m = 0; m < M; m++) {
+        const float* s = src + (size_t)m * W;
+        const float* s2 = src2 ? src2 + (size_t)m * W : NULL;
+        double inv = 1.0;
+        if (mode == 0) {
+            double ss = 0.0;
+            for (int i = 0; i < W; i++) {
+                const double v = (double)s[i] + (add ? (double)s2[i] : 0.0);
+                ss += v * v;
+            }
+            inv = 1.0 / sqrt(ss / W + 1e-6);
+        }
+        for (int i = 0; i < W; i++) {
+            double v;
+            if (mode == 0) {
+                const double x = (double)s[i] + (add ? (double)s2[i] : 0.0);
+                if (gamma) hout[(size_t)m * W + i] = x * inv * gamma[i];
+                v = x * inv;
+            } else if (mode == 1) {
+                const double g = s[i];
+                v = g / (1.0 + exp(-g)) * s2[i];
+            } else if (mode == 2) {
+                v = s[orc_gdn_perm(i)];
+            } else {
+                v = s[i];
+            }
+            u[i] = v * gs[i];
+        }
+        for (int b = 0; b < W; b += 1024) {
+            orc_fwht_d(u + b, 1024);
+            for (int j = 0; j < 1024; j++) out[(size_t)m * W + b + j] = u[b + j] / 32.0;
+        }
+    }
+    free(u);
+}
+
 /* ---------------------------------------------------------------- CPU baseline --------
  * The reference has no CPU matmul; its host-side arithmetic for the path is the PTQ1_0
  * decoder (prism_ptq1_0_quant_dequant.c:54-84).  The baseline timed next to the GPU is

@@ -57,6 +57,7 @@ def lib():
             "orc_gemm_i8": (None, [P, P, i, P, P, P, i, i, i]),
             "orc_cpu_gemv_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
             "orc_cpu_gemm_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
+            "orc_norm_fwht": (None, [P, P, P, P, P, P, i, i, i, i]),
             "orc_omp_max_threads": (i, []),
         }
         for name, (res, args) in sig.items():
@@ -164,6 +165,20 @@ def gemm_i8(A8, SX, W, M, K, N, want_group_sums=False):
     GS = np.empty((M, N, K // GROUP), np.int32) if want_group_sums else None
     lib().orc_gemm_i8(_p(A8), _p(SX), ldS, _p(W), _p(C), _p(GS) if GS is not None else None, M, K, N)
     return (C, GS) if want_group_sums else C
+
+
+def norm_fwht(src, gs, mode, src2=None, gamma=None, add=False):
+    """Input transform (double): returns (out [M][W], hout or None)."""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    M, W = src.shape
+    gs = np.ascontiguousarray(gs, dtype=np.float32)
+    s2 = None if src2 is None else np.ascontiguousarray(src2, dtype=np.float32)
+    gm = None if gamma is None else np.ascontiguousarray(gamma, dtype=np.float32)
+    out = np.empty((M, W), np.float64)
+    hout = np.empty((M, W), np.float64) if gm is not None else None
+    lib().orc_norm_fwht(_p(src), None if s2 is None else _p(s2), _p(gs), None if gm is None else _p(gm), _p(out),
+                        None if hout is None else _p(hout), W, M, mode, 1 if add else 0)
+    return out, hout
 
 
 def cpu_gemm_f32(A, W, M, K, N, row0, nrows, nthreads):

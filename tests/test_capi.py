@@ -80,6 +80,15 @@ def test_other_entry_points_reject_bad_shapes():
     assert lib.kata_quant_rows_i8(FAKE, FAKE, FAKE, 4, 128, 2, None) == KATA_EINVAL            # ldS < M
     assert lib.kata_gemm_ptq1_i8(FAKE, FAKE, 4, FAKE, FAKE, 0, 4, 4, 128, 8, None) == KATA_EINVAL  # ldc < N
     assert lib.kata_gemv_ptq1(FAKE, ctypes.c_void_p(0x10008), 1, 0, FAKE, 128, 8, 1, None) == KATA_EINVAL  # x align
+    # matmul input transform: W % 1024, half2 only for fp16 with M == 2, mode 2 only at W = 6144,
+    # gamma and hout together
+    assert lib.kata_add_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, None, None, None, 0, 1000, 1, None) == KATA_EINVAL
+    assert lib.kata_add_rms_fwht(FAKE, None, FAKE, FAKE, 0, 1, None, None, None, 0, 1024, 2, None) == KATA_EINVAL
+    assert lib.kata_add_rms_fwht(FAKE, None, FAKE, FAKE, 1, 1, None, None, None, 0, 1024, 3, None) == KATA_EINVAL
+    assert lib.kata_add_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, None, FAKE, None, 0, 1024, 1, None) == KATA_EINVAL
+    assert lib.kata_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, 5120, 1, 2, None) == KATA_EINVAL
+    assert lib.kata_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, 5120, 1, 1, None) == KATA_EINVAL   # mode 1 needs src2
+    assert lib.kata_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, 5120, 1, 4, None) == KATA_EINVAL
     # the 27B shapes (K up to 17408) must fit for both T
     assert lib.kata_gemv_ptq1_max_k(1) >= 17408 and lib.kata_gemv_ptq1_max_k(2) >= 17408
     assert lib.kata_gemv_ptq1_max_k(1) % 128 == 0 and lib.kata_gemv_ptq1_max_k(2) % 128 == 0

@@ -216,3 +216,63 @@ def test_cpu_baseline_gemm_matches_oracle_gemm():
     C = orc.cpu_gemm_f32(A, W, M, K, N, 0, N, 2)
     R = orc.gemm_f16(A, W, M, K, N)
     assert np.abs(C - R).max() <= 1e-5 * np.abs(R).max()
+
+
+# ----------------------------------------------------------------------------- matmul input transform
+def test_norm_fwht_plain_matches_hadamard_matrix():
+    """Mode 3 (u = src * gs) against the Sylvester Hadamard matrix (scipy.linalg.hadamard,
+    natural order: H[j][k] = (-1)^popcount(j & k)) applied per 1024-block, / 32."""
+    from scipy.linalg import hadamard
+    H = hadamard(1024).astype(np.float64)
+    rng = np.random.default_rng(5)
+    src = rng.standard_normal((3, 2048)).astype(np.float32)
+    gs = rng.choice([-1.0, 1.0], size=2048).astype(np.float32)
+    out, _ = orc.norm_fwht(src, gs, 3)
+    u = src.astype(np.float64) * gs
+    ref = np.concatenate([u[:, :1024] @ H.T, u[:, 1024:] @ H.T], axis=1) / 32.0
+    assert np.abs(out - ref).max() < 1e-9 * np.abs(ref).max()
+
+
+def test_norm_fwht_involution_and_rms_closed_form():
+    """(H/32)^2 = I: transforming the transform with gs = 1 returns the input; mode 0 with a
+    constant row c gives inv = 1/sqrt(c^2 + 1e-6), so H of v*inv*gs is checked on a row whose
+    transform is known: a constant block maps to 32 * c * inv at j = 0 and 0 elsewhere."""
+    rng = np.random.default_rng(6)
+    src = rng.standard_normal((2, 1024)).astype(np.float32)
+    ones = np.ones(1024, np.float32)
+    once, _ = orc.norm_fwht(src, ones, 3)
+    twice, _ = orc.norm_fwht(once.astype(np.float32), ones, 3)
+    assert np.abs(twice - src).max() < 1e-5
+    c = 0.75
+    x = np.full((1, 1024), c, np.float32)
+    out, hout = orc.norm_fwht(x, ones, 0, gamma=np.full(1024, 2.0, np.float32))
+    inv = 1.0 / np.sqrt(c * c + 1e-6)
+    assert abs(out[0, 0] - 32.0 * c * inv) < 1e-9 and np.abs(out[0, 1:]).max() < 1e-12
+    assert np.allclose(hout, 2.0 * c * inv, rtol=1e-12)
+    # residual add: x + y with y = -x + c gives the same constant row
+    y = (c - src[:1]).astype(np.float32)
+    out2, _ = orc.norm_fwht(src[:1], ones, 0, src2=y, add=True)
+    assert abs(out2[0, 0] - 32.0 * c * inv) < 1e-5
+
+
+def test_norm_fwht_swiglu_and_gdn_order():
+    """Mode 1 is silu(a) * b (checked with H applied twice, back to the elementwise value);
+    mode 2 reads src[h + 128 (t/3 + 16 (t%3))] for i = 128 t + h, a permutation of 6144."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((1, 1024)).astype(np.float32)
+    b = rng.standard_normal((1, 1024)).astype(np.float32)
+    ones = np.ones(1024, np.float32)
+    out, _ = orc.norm_fwht(a, ones, 1, src2=b)
+    back, _ = orc.norm_fwht(out.astype(np.float32), ones, 3)
+    ref = a.astype(np.float64) / (1.0 + np.exp(-a.astype(np.float64))) * b
+    assert np.abs(back - ref).max() < 1e-5
+    i = np.arange(6144)
+    h, t = i & 127, i >> 7
+    perm = h + 128 * (t // 3 + 16 * (t % 3))
+    assert np.array_equal(np.sort(perm), i)
+    src = np.arange(6144, dtype=np.float32)[None, :]
+    ones6 = np.ones(6144, np.float32)
+    out, _ = orc.norm_fwht(src, ones6, 2)
+    back = np.concatenate([orc.norm_fwht(out[:, 1024 * k:1024 * (k + 1)].astype(np.float32), ones, 3)[0]
+                           for k in range(6)], axis=1)
+    assert np.abs(back[0] - perm).max() < 1e-3
