@@ -135,6 +135,31 @@ int kata_quantize_ptq1_0(const float* x, uint8_t* out, int64_t nrow, int64_t k);
  * raw bits) using the same byte encoding; used to build synthetic weights. */
 int kata_pack_ptq1_0(const int8_t* trits, const uint16_t* scales, uint8_t* out, int64_t nrow, int64_t k);
 
+/* ---------------------------------------------------------------- GGUF model file ----
+ * HOST: a GGUF v3 file memory-mapped read-only and indexed (src/gguf.cpp:41-71,
+ * src/gguf.h): tensor infos (name, ggml type — 143 PTQ1_0, 8 Q8_0, 0 F32 …, dims with
+ * dims[0] the row length, byte offset in the data region, byte size; 0 for a type not
+ * known here) and integer / string metadata.  kata_gguf_upload copies the whole data region
+ * to one device allocation: a matrix is then dev_base + offset, the weight base that
+ * kata_dispatch_create takes and the byte offsets its calls take (src/engine.cpp:27-37).
+ * NULL / negative returns set kata_last_error(). */
+typedef struct kata_gguf kata_gguf;
+kata_gguf* kata_gguf_open(const char* path);
+void kata_gguf_close(kata_gguf* g);
+int64_t kata_gguf_tensor_count(const kata_gguf* g);
+uint64_t kata_gguf_data_bytes(const kata_gguf* g);
+/* tensor i: any output pointer may be NULL; dims has room for 4 */
+int kata_gguf_tensor(const kata_gguf* g, int64_t i, const char** name, uint32_t* type, uint64_t* dims,
+                     uint64_t* offset, uint64_t* nbytes);
+int64_t kata_gguf_find(const kata_gguf* g, const char* name);          /* index, or KATA_EINVAL */
+int kata_gguf_get_int(const kata_gguf* g, const char* key, uint64_t* value);
+const char* kata_gguf_get_str(const kata_gguf* g, const char* key);   /* NULL if absent */
+/* synchronous device copy of the data region (a new hipMalloc); free with kata_gguf_free_device */
+int kata_gguf_upload(const kata_gguf* g, uint8_t** dev_base);
+/* the same copy into caller device memory of at least kata_gguf_data_bytes(g) bytes */
+int kata_gguf_upload_into(const kata_gguf* g, uint8_t* dev, uint64_t capacity);
+int kata_gguf_free_device(uint8_t* dev_base);
+
 /* ---------------------------------------------------------------- dispatcher ---------
  * An engine-side dispatcher that maps (byte offset into the weight file, K, N, matrix
  * name) to the kernels above, with the reference's per-matrix int8 selection.

@@ -47,6 +47,17 @@ SIGNATURES = {
     "kata_rms_fwht": (I, [P, P, P, P, I, I, I, I, I, P]),
     "kata_quantize_ptq1_0": (I, [P, P, I64, I64]),
     "kata_pack_ptq1_0": (I, [P, P, P, I64, I64]),
+    "kata_gguf_open": (P, [ctypes.c_char_p]),
+    "kata_gguf_close": (None, [P]),
+    "kata_gguf_tensor_count": (I64, [P]),
+    "kata_gguf_data_bytes": (U64, [P]),
+    "kata_gguf_tensor": (I, [P, I64, P, P, P, P, P]),
+    "kata_gguf_find": (I64, [P, ctypes.c_char_p]),
+    "kata_gguf_get_int": (I, [P, ctypes.c_char_p, P]),
+    "kata_gguf_get_str": (ctypes.c_char_p, [P, ctypes.c_char_p]),
+    "kata_gguf_upload": (I, [P, P]),
+    "kata_gguf_upload_into": (I, [P, P, U64]),
+    "kata_gguf_free_device": (I, [P]),
     "kata_dispatch_create": (P, [P]),
     "kata_dispatch_destroy": (None, [P]),
     "kata_dispatch_set_i8": (I, [P, ctypes.c_char_p]),

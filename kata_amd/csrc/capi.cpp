@@ -52,6 +52,10 @@ int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, con
 
 }  // namespace
 
+// for the other host sources of the library (gguf.cpp)
+int kata_internal_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
+
 extern "C" {
 
 const char* kata_last_error(void) { return g_err.c_str(); }
