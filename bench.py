@@ -414,6 +414,19 @@ def main():
         q8[name] = {"K": K, "N": N, "us": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
         del Wqs, Wq
 
+    # ---- lm_head (5120 -> 248320 PTQ1_0 GEMV, 278 MB) and the greedy argmax of its logits
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 700)
+    lm = [device_weights(torch, dev, 5120, 248320, gen) for _ in range(2)]   # 556 MB: past the MALL
+    lx = xs[next(g for _, K, _, g in SWEEP if K == 5120)]
+    ly = torch.empty((1, 248320), dtype=torch.float32, device=dev)
+    lidx = torch.empty(1, dtype=torch.int32, device=dev)
+    us_lm = time_reps(lambda r: ops.gemv_ptq1(lm[r % 2], lx, 5120, 248320, 1, out=ly), 40)
+    us_am = time_reps(lambda r: ops.argmax(ly, out=lidx), 40)
+    lm_head = {"K": 5120, "N": 248320, "gemv_us": round(us_lm, 2),
+               "GBps": round(lm[0].numel() / (us_lm * 1e-6) / 1e9, 1), "argmax_us": round(us_am, 2)}
+    del lm
+
     # ---- matmul input transform (residual add + RMSNorm + sign + FWHT), decode and prefill
     xform = {}
     for label, M in (("decode_m1", 1), ("prefill_m7300", 7300)):
@@ -489,6 +502,7 @@ def main():
         "q8_0_t1": q8,
         "prefill_gemm": gemm,
         "input_transform": xform,
+        "lm_head": lm_head,
         "config5": cfg5,
         "cpu_baseline": cpu,
     }

@@ -127,6 +127,13 @@ int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out
 int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype, int out_layout,
                   int W, int M, int mode, void* stream);
 
+/* Greedy argmax of n fp32 logits into *out (device int): an element counts only if strictly
+ * greater than the best so far (NaN and -inf never do), lowest index on ties, 0x7fffffff
+ * when none does.  x 16-byte aligned.  Deterministic; calls on one device must not overlap
+ * (module-scope partials).  Replaces k_argmax (shaders/ops.metal:66-78) after the lm_head
+ * GEMV (src/engine.cpp:191-192). */
+int kata_argmax(const float* x, int n, int* out, void* stream);
+
 /* ---------------------------------------------------------------- HOST packers -------
  * HOST: quantize_row_ptq1_0_ref over nrow rows of k floats (k % 128 == 0)
  * (docs/reference/prism_ptq1_0_quant_dequant.c:4-52, quantize_ptq1_0 :86-96). */

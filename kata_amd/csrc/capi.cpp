@@ -189,6 +189,14 @@ int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* ou
                         "rms_fwht");
 }
 
+// ------------------------------------------------------------------ argmax
+int kata_argmax(const float* x, int n, int* out, void* stream) {
+    if (!x || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (n <= 0) return fail(KATA_EINVAL, "n=%d must be positive", n);
+    if (!aligned(x, 16) || !aligned(out, 4)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
+    return check_launch(kata::launch_argmax(x, n, out, (hipStream_t)stream), "argmax");
+}
+
 // ------------------------------------------------------------------ host packers
 // Byte encoding of the quantiser (docs/reference/prism_ptq1_0_quant_dequant.c:20-46):
 // stages of 16 and 8 bytes carry 5 digits each (most significant first, element

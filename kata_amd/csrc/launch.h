@@ -35,4 +35,7 @@ hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs
                             int out_layout, float* xnew, const float* gamma, void* hout, int flags, int W, int M,
                             int mode, hipStream_t s);
 
+// ---- argmax of the logits (argmax.hip)
+hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s);
+
 }  // namespace kata

@@ -154,6 +154,14 @@ def rms_fwht(src: torch.Tensor, gs: torch.Tensor, mode: int, src2: torch.Tensor 
     return out
 
 
+def argmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy argmax of fp32 logits (k_argmax): a device int32 tensor of one element."""
+    _need_gpu(x)
+    o = out if out is not None else torch.empty(1, dtype=torch.int32, device=x.device)
+    check(lib().kata_argmax(_ptr(x), x.numel(), _ptr(o), _stream(x)))
+    return o
+
+
 def _np_ptr(a: np.ndarray):
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(ctypes.c_void_p)
