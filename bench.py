@@ -247,6 +247,7 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="replay each step's HIP graph instead of launching its GEMVs from Python")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer sweep and the M=7300 GEMMs")
+    ap.add_argument("--no-ffn", action="store_true", help="skip the FFN sublayer figures")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the pp512 prefill GEMMs (for counter runs), then exit")
     ap.add_argument("--step-only", action="store_true",
@@ -444,6 +445,51 @@ def main():
         nbytes = M * W * (4 + 4 + 4 + 2)              # x, y in; xnew fp32, out fp16 out
         xform[label] = {"M": M, "W": W, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
+    # ---- layer level: the FFN sublayer (27B shapes H=5120, F=17408) through the dispatcher,
+    # decode (4 launches) over 8 rotating weight sets (470 MB, past the MALL) and pp512 prefill
+    ffn = None
+    if not args.no_ffn:
+        from kata_amd.engine import Dispatch, ffn_prefill_work_bytes
+        H, F = 5120, 17408
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED + 800)
+        nset = 8
+        mats = []
+        for _ in range(nset):
+            mats += [device_weights(torch, dev, H, F, gen), device_weights(torch, dev, H, F, gen),
+                     device_weights(torch, dev, F, H, gen)]
+        wbuf = torch.cat([m.reshape(-1) for m in mats])
+        del mats
+        msz = [packed_bytes(H, F), packed_bytes(H, F), packed_bytes(F, H)]
+        set_b = sum(msz)
+        disp = Dispatch(wbuf)
+        offs = lambda r: (set_b * (r % nset), set_b * (r % nset) + msz[0], set_b * (r % nset) + msz[0] + msz[1])
+        fx = torch.randn(H, generator=gen, device=dev)
+        fy = torch.randn(H, generator=gen, device=dev)
+        fxn = torch.empty(H, device=dev)
+        gsi = torch.randn(H, generator=gen, device=dev).sign()
+        gsd = torch.randn(F, generator=gen, device=dev).sign()
+        fout = torch.empty(H, device=dev)
+        fwork = torch.empty(H + 3 * F, device=dev)
+        us_d = time_reps(lambda r: disp.ffn_decode(*offs(r), fx, fy, gsi, gsd, H, F, out=fout, xnew=fxn,
+                                                   work=fwork), 40)
+        ffn = {"H": H, "F": F, "decode_us": round(us_d, 2),
+               "decode_GBps": round(set_b / (us_d * 1e-6) / 1e9, 1)}
+        M = 512
+        px = torch.randn((M, H), generator=gen, device=dev)
+        py = torch.randn((M, H), generator=gen, device=dev)
+        pxn = torch.empty((M, H), device=dev)
+        pout = torch.empty((M, H), device=dev)
+        pwork = torch.empty(ffn_prefill_work_bytes(H, F, M), dtype=torch.uint8, device=dev)
+        for spec in ("none", "ffn"):
+            disp.set_i8(spec)
+            us_p = time_reps(lambda r: disp.ffn_prefill(*offs(r), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
+                                                        work=pwork), 10)
+            ffn[f"prefill_m512_i8_{spec}_us"] = round(us_p, 1)
+            ffn[f"prefill_m512_i8_{spec}_TFLOPS"] = round(2 * M * 3 * H * F / (us_p * 1e-6) / 1e12, 1)
+        disp.close()
+        del wbuf, disp
+
     # ---- pp512 prefill GEMM (config 4), fp16 exact path
     gemm = None if args.no_gemm else run_gemm(torch, ops, dev, stream, copies, ncopies)
 
@@ -503,6 +549,7 @@ def main():
         "prefill_gemm": gemm,
         "input_transform": xform,
         "lm_head": lm_head,
+        "ffn_sublayer": ffn,
         "config5": cfg5,
         "cpu_baseline": cpu,
     }

@@ -189,6 +189,21 @@ int kata_dispatch_prefill(kata_dispatch* d, uint64_t wOff, const uint16_t* A, fl
                           int K, int N, const char* name, int8_t* A8, float* SX, int ldS,
                           void* stream);
 
+/* Layer level: the FFN sublayer of Engine::step (src/engine.cpp:176-182) through the
+ * dispatcher's weights: h = H(rmsnorm(x + y) * gs_in) (x + y also to xnew when non-NULL; y
+ * may be NULL), g = W_gate h and u = W_up h in one launch, t = H(silu(g) * u * gs_down),
+ * out = W_down t.  x, y, xnew, out fp32 [H]; work H + 3F floats; H, F multiples of 1024. */
+int kata_dispatch_ffn_decode(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
+                             const float* y, float* xnew, const float* gs_in, const float* gs_down, float* work,
+                             float* out, int H, int F, void* stream);
+/* The same for M prefill rows (src/engine.cpp:247-300): fp16 rows into the GEMMs, each of
+ * gate / up / down on the fp16 exact or int8 path as kata_dispatch_set_i8 selected.  x, y,
+ * xnew, out fp32 [M][H]; work of kata_ffn_prefill_work_bytes(H, F, M) bytes, 16-byte aligned. */
+int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
+                              const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
+                              float* out, int H, int F, int M, void* stream);
+size_t kata_ffn_prefill_work_bytes(int H, int F, int M);
+
 #ifdef __cplusplus
 }
 #endif

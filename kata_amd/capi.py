@@ -66,6 +66,9 @@ SIGNATURES = {
     "kata_dispatch_i8_mask": (U32, [P]),
     "kata_dispatch_gemv": (I, [P, U64, P, P, I, I, P]),
     "kata_dispatch_prefill": (I, [P, U64, P, P, I, I, I, ctypes.c_char_p, P, P, I, P]),
+    "kata_dispatch_ffn_decode": (I, [P, U64, U64, U64, P, P, P, P, P, P, P, I, I, P]),
+    "kata_dispatch_ffn_prefill": (I, [P, U64, U64, U64, P, P, P, P, P, P, P, I, I, I, P]),
+    "kata_ffn_prefill_work_bytes": (SZ, [I, I, I]),
 }
 
 

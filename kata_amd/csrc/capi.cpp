@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <string>
 
 #include "../../include/kata_amd.h"
@@ -340,4 +341,57 @@ int kata_dispatch_prefill(kata_dispatch* d, uint64_t wOff, const uint16_t* A, fl
     return kata_gemm_ptq1_f16(A, K, W, C, KATA_F32, N, M, K, N, stream);
 }
 
+
+// ------------------------------------------------------------------ layer-level: the FFN sublayer
+// Engine::step's FFN (src/engine.cpp:176-182): h = H(rmsnorm(x + y) * gs_in) (the residual
+// x + y is kept in xnew), g = W_gate h, u = W_up h (one batched launch), t = H(silu(g) u *
+// gs_down), out = W_down t.  work: H + 3F floats.
+int kata_dispatch_ffn_decode(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
+                             const float* y, float* xnew, const float* gs_in, const float* gs_down, float* work,
+                             float* out, int H, int F, void* stream) {
+    if (!d || !x || !gs_in || !gs_down || !work || !out) return fail(KATA_EINVAL, "null argument");
+    if (H % 1024 != 0 || F % 1024 != 0 || H <= 0 || F <= 0) return fail(KATA_EINVAL, "H=%d F=%d must be multiples of 1024", H, F);
+    float* h = work;
+    float* g = work + H;
+    float* u = g + F;
+    float* t = u + F;
+    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_F32, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, 1, stream);
+    if (rc) return rc;
+    const uint8_t* Wg[2] = {d->wbase + offGate, d->wbase + offUp};
+    float* Yg[2] = {g, u};
+    const int Ng[2] = {F, F};
+    if ((rc = kata_gemv_ptq1_batch(2, Wg, Yg, Ng, h, KATA_F32, KATA_X_ROWS, H, 1, stream))) return rc;
+    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_F32, KATA_X_ROWS, F, 1, 1, stream))) return rc;
+    return kata_gemv_ptq1(d->wbase + offDown, t, KATA_F32, KATA_X_ROWS, out, F, H, 1, stream);
+}
+
+// The same sublayer for M prefill rows (src/engine.cpp:247-300): the GEMMs take fp16 rows,
+// gate / up / down each on the fp16 exact or the int8 path per the dispatcher's selection.
+// work: fp32 2 M F (g, u), then fp16 M H (h) and M F (t); with an int8 matrix also int8
+// M max(H, F) and fp32 (max(H, F) / 128) M (its quantised rows and scales).  out fp32 [M][H].
+int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
+                              const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
+                              float* out, int H, int F, int M, void* stream) {
+    if (!d || !x || !gs_in || !gs_down || !work || !out) return fail(KATA_EINVAL, "null argument");
+    if (H % 1024 != 0 || F % 1024 != 0 || H <= 0 || F <= 0 || M <= 0)
+        return fail(KATA_EINVAL, "H=%d F=%d must be multiples of 1024, M=%d positive", H, F, M);
+    float* g = (float*)work;
+    float* u = g + (size_t)M * F;
+    uint16_t* h = (uint16_t*)(u + (size_t)M * F);
+    uint16_t* t = h + (size_t)M * H;
+    const size_t kmax = (size_t)std::max(H, F);
+    int8_t* A8 = (int8_t*)(t + (size_t)M * F);
+    float* SX = (float*)(((uintptr_t)(A8 + (size_t)M * kmax) + 15) & ~(uintptr_t)15);
+    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_F16, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, M, stream);
+    if (rc) return rc;
+    if ((rc = kata_dispatch_prefill(d, offGate, h, g, M, H, F, "gate", A8, SX, M, stream))) return rc;
+    if ((rc = kata_dispatch_prefill(d, offUp, h, u, M, H, F, "up", A8, SX, M, stream))) return rc;
+    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_F16, KATA_X_ROWS, F, M, 1, stream))) return rc;
+    return kata_dispatch_prefill(d, offDown, t, out, M, F, H, "down", A8, SX, M, stream);
+}
+
+size_t kata_ffn_prefill_work_bytes(int H, int F, int M) {
+    const size_t kmax = (size_t)std::max(H, F);
+    return (size_t)M * F * 8 + (size_t)M * H * 2 + (size_t)M * F * 2 + (size_t)M * kmax + 16 + kmax / 128 * M * 4;
+}
 }  // extern "C"

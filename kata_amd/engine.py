@@ -62,3 +62,37 @@ class Dispatch:
         ldS = SX.shape[1] if SX is not None else M
         check(lib().kata_dispatch_prefill(self._h, wOff, _ptr(A), _ptr(C), M, K, N, name.encode(),
                                           _ptr(A8), _ptr(SX), ldS, _stream(self.wbuf)))
+
+    # ---- layer level: the FFN sublayer (src/engine.cpp:176-182 decode, :247-300 prefill)
+    def ffn_decode(self, offGate: int, offUp: int, offDown: int, x: torch.Tensor, y: torch.Tensor | None,
+                   gs_in: torch.Tensor, gs_down: torch.Tensor, H: int, F: int, out: torch.Tensor | None = None,
+                   xnew: torch.Tensor | None = None, work: torch.Tensor | None = None) -> torch.Tensor:
+        """out = W_down H(silu(W_gate h) * (W_up h) * gs_down), h = H(rmsnorm(x + y) * gs_in)."""
+        dev = x.device
+        if out is None:
+            out = torch.empty(H, dtype=torch.float32, device=dev)
+        if work is None:
+            work = torch.empty(H + 3 * F, dtype=torch.float32, device=dev)
+        check(lib().kata_dispatch_ffn_decode(self._h, offGate, offUp, offDown, _ptr(x), _ptr(y), _ptr(xnew),
+                                             _ptr(gs_in), _ptr(gs_down), _ptr(work), _ptr(out), H, F,
+                                             _stream(self.wbuf)))
+        return out
+
+    def ffn_prefill(self, offGate: int, offUp: int, offDown: int, x: torch.Tensor, y: torch.Tensor | None,
+                    gs_in: torch.Tensor, gs_down: torch.Tensor, H: int, F: int, out: torch.Tensor | None = None,
+                    xnew: torch.Tensor | None = None, work: torch.Tensor | None = None) -> torch.Tensor:
+        """The FFN sublayer over M = x.shape[0] rows; GEMMs on the paths set_i8 selected."""
+        M = x.shape[0]
+        dev = x.device
+        if out is None:
+            out = torch.empty((M, H), dtype=torch.float32, device=dev)
+        if work is None:
+            work = torch.empty(ffn_prefill_work_bytes(H, F, M), dtype=torch.uint8, device=dev)
+        check(lib().kata_dispatch_ffn_prefill(self._h, offGate, offUp, offDown, _ptr(x), _ptr(y), _ptr(xnew),
+                                              _ptr(gs_in), _ptr(gs_down), _ptr(work), _ptr(out), H, F, M,
+                                              _stream(self.wbuf)))
+        return out
+
+
+def ffn_prefill_work_bytes(H: int, F: int, M: int) -> int:
+    return int(lib().kata_ffn_prefill_work_bytes(H, F, M))

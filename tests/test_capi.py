@@ -140,3 +140,20 @@ def test_dispatch_i8_selection():
         assert not lib.kata_dispatch_i8(h, b"lm_head")
     finally:
         lib.kata_dispatch_destroy(h)
+
+
+def test_dispatch_ffn_rejects():
+    """The FFN sublayer entry points validate before any launch (no GPU needed)."""
+    lib = L.lib()
+    h = ctypes.c_void_p(lib.kata_dispatch_create(FAKE))
+    try:
+        p = FAKE
+        assert lib.kata_dispatch_ffn_decode(h, 0, 0, 0, p, None, None, p, p, p, p, 2048, 3000, None) == KATA_EINVAL
+        assert lib.kata_dispatch_ffn_decode(h, 0, 0, 0, None, None, None, p, p, p, p, 2048, 3072, None) == KATA_EINVAL
+        assert lib.kata_dispatch_ffn_decode(None, 0, 0, 0, p, None, None, p, p, p, p, 2048, 3072, None) == KATA_EINVAL
+        assert lib.kata_dispatch_ffn_prefill(h, 0, 0, 0, p, None, None, p, p, p, p, 2048, 3072, 0, None) == KATA_EINVAL
+        assert lib.kata_dispatch_ffn_prefill(h, 0, 0, 0, p, None, None, p, None, p, p, 2048, 3072, 4, None) == KATA_EINVAL
+    finally:
+        lib.kata_dispatch_destroy(h)
+    # g, u fp32 + h, t fp16 + int8 rows + 16 alignment + scales
+    assert lib.kata_ffn_prefill_work_bytes(1024, 2048, 8) == 8 * 2048 * 8 + 8 * 1024 * 2 + 8 * 2048 * 2 + 8 * 2048 + 16 + 16 * 8 * 4
