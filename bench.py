@@ -24,6 +24,7 @@ Also reported (same JSON line):
   per_matrix   GB/s of each matrix kind alone (200 repeats over rotating copies, replayed
                from one HIP graph so that the host's launch cost is not what is timed);
   verify_t2    config 3: the T=2 verify GEMV on the FFN and attention shapes;
+  verify_wide  the wide verification GEMV (T = 4, 8 token rows) on the same shapes;
   q8_0_t1      config 3: the Q8_0 MTP-head GEMV, 17408x5120 and 5120x17408;
   prefill_gemm pp512 exact fp16 GEMM TFLOPS (M=512, 5120->17408 and 17408->5120),
                vs 2.5 PFLOP/s dense fp16;
@@ -398,6 +399,20 @@ def main():
         us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], x2, K, N, 2, out=y2), args.reps)
         verify_t2[name] = {"K": K, "N": N, "us": round(us, 3),
                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
+    # wide verification GEMV (Engine::dWide): T = 4 and 8 token rows, one weight read
+    verify_wide = {}
+    for j, (name, K, N, grp) in enumerate(SWEEP):
+        if name not in ("gdn_qkv", "attn_q", "attn_o", "ffn_gate", "ffn_down"):
+            continue
+        ent = {"K": K, "N": N}
+        for T in (4, 8):
+            xw = torch.from_numpy(np.random.default_rng(SEED + 350 + j).standard_normal((T, K))
+                                  .astype(np.float16)).to(dev)
+            yw = torch.empty((T, N), dtype=torch.float32, device=dev)
+            us = time_reps(lambda r: ops.gemv_ptq1_wide(copies[r % ncopies][j], xw, K, N, out=yw), args.reps)
+            ent[f"t{T}_us"] = round(us, 3)
+            ent[f"t{T}_GBps"] = round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
+        verify_wide[name] = ent
     q8 = {}
     for name, K, N in (("gate", 5120, 17408), ("down", 17408, 5120)):
         nb = N * (K // 32) * 34
@@ -545,6 +560,7 @@ def main():
                                   "GBps": round(set_bytes * args.steps / (ms_single * 1e-3) / 1e9, 1)},
         "per_matrix": per_matrix,
         "verify_t2": verify_t2,
+        "verify_wide": verify_wide,
         "q8_0_t1": q8,
         "prefill_gemm": gemm,
         "input_transform": xform,

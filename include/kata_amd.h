@@ -64,6 +64,17 @@ int kata_gemv_ptq1_max_k(int T);
 int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, const int* N,
                          const void* x, int x_dtype, int x_layout, int K, int T, void* stream);
 
+/* Wide verification GEMV: the same y[t][n] for T in 1..8 token rows, x [T][K] fp16 or fp32
+ * (16-byte aligned), y [T][N] fp32, any K % 128 == 0 (the activation is quantised per K
+ * chunk in-kernel, same 16-bit block fixed point as above).  Every weight byte is read
+ * once for all T rows.  When K is split over workgroups the partial sums use the per-device
+ * workspace of kata_gemm_ptq1_f16 (same rules: calls on one device must not overlap, the
+ * first such call must not be captured).
+ * Replaces Engine::dWide / xWideGemv (src/engine.cpp:542-556, src/engine.h:109,140; kernel
+ * k_wide_m16_n16_k128_g4, shaders/wide.metal:41-99, whose x is fp16 rows padded to 16). */
+int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                        void* stream);
+
 /* Q8_0 GEMV for the MTP head: y[t][n] = sum_b d[n,b] * sum_i q[n,b,i] * x[t][32b+i].
  * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16 (16-byte aligned), y [T][N] fp32.
  * W is 2-byte aligned (the block layout's granularity).

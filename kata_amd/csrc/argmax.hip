@@ -4,10 +4,11 @@
 //
 // Design: a grid of up to 256 workgroups, each reducing a contiguous range (16-byte loads,
 // a fixed-order reduction across lanes and waves) to one (value, index) pair in a
-// module-scope device array; the workgroup that takes the last ticket of a module-scope
-// counter reduces those pairs in workgroup order, writes the index and resets the counter,
-// so the result is deterministic and no memory has to be cleared between calls (the
-// counter starts at zero when the library loads).  Calls on one device must not overlap.
+// module-scope device array, then a one-workgroup launch reduces those pairs in workgroup
+// order and writes the index: deterministic, and nothing has to be cleared between calls.
+// (A last-arriving-workgroup reduction in one launch needs a device-scope release per
+// workgroup, an L2 write-back on this chip, which costs more than the second launch.)
+// Calls on one device must not overlap (the pairs are module-scope).
 #include "launch.h"
 
 #include <math.h>
@@ -21,7 +22,6 @@ namespace {
 constexpr int kMaxGroups = 256;
 __device__ float g_part_v[kMaxGroups];
 __device__ int g_part_i[kMaxGroups];
-__device__ unsigned int g_ticket;
 
 // element b at index ib after the current best a (indices increasing): strictly greater
 __device__ inline void take(float& a, int& ia, float b, int ib) {
@@ -51,10 +51,9 @@ __device__ inline void block_best(float& v, int& i, float* sv, int* si) {
         for (int w = 1; w < (int)blockDim.x / 64; w++) better(v, i, sv[w], si[w]);
 }
 
-__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int n, int* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int n) {
     __shared__ float sv[4];
     __shared__ int si[4];
-    __shared__ bool last;
     const int tid = threadIdx.x, G = gridDim.x;
     const int lo = (int)(((long)blockIdx.x * n) / G), hi = (int)(((long)(blockIdx.x + 1) * n) / G);
     float v = -INFINITY;
@@ -74,31 +73,28 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int
     if (tid == 0) {
         g_part_v[blockIdx.x] = v;
         g_part_i[blockIdx.x] = idx;
-        __threadfence();
-        last = atomicAdd(&g_ticket, 1u) == (unsigned)G - 1;
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+}
+
+__global__ __launch_bounds__(256) void k_argmax_final(int G, int* __restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int g = tid; g < G; g += 256) {
-        const float pv = __builtin_nontemporal_load(&g_part_v[g]);
-        const int pi = __builtin_nontemporal_load(&g_part_i[g]);
-        better(bv, bi, pv, pi);
-    }
+    for (int g = tid; g < G; g += 256) better(bv, bi, g_part_v[g], g_part_i[g]);
     block_best(bv, bi, sv, si);
-    if (tid == 0) {
-        *out = bi;
-        g_ticket = 0;
-    }
+    if (tid == 0) *out = bi;
 }
 
 }  // namespace
 
 hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s) {
     const int G = std::max(1, std::min(kMaxGroups, n / 1024));
-    hipLaunchKernelGGL(k_argmax, dim3(G), dim3(256), 0, s, x, n, out);
+    hipLaunchKernelGGL(k_argmax, dim3(G), dim3(256), 0, s, x, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, G, out);
     return hipGetLastError();
 }
 

@@ -85,6 +85,17 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
                         "gemv ptq1 batch");
 }
 
+int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, void* stream) {
+    if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
+    if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
+    if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
+    return check_launch(kata::launch_gemv_wide(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv ptq1 wide");
+}
+
 // ------------------------------------------------------------------ Q8_0 GEMV
 int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, void* stream) {
     if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");

@@ -543,6 +543,232 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     }
 }
 
+
+// ---------------------------------------------------------------------------------------
+// Wide verification GEMV: T <= 8 token rows against one read of the weights
+// (shaders/wide.metal:41-99, dispatched by Engine::dWide, src/engine.cpp:542-556).
+//
+// The same integer decode and 16-bit two-limb activation as k_gemv_ptq1, with the MFMA
+// operands laid out for many tokens instead of many blocks: B column x = weight row x of a
+// 16-row tile (lane group g decodes segment g of that row's block, no rotation), A row
+// i = (token i >> 1, limb i & 1) of the same block, so every product of the 16 x 16 result
+// is used: lane x + 16 g ends with the int32 sums of tokens 2g, 2g+1 for row x.
+//
+// Job = (row group of 128 rows, chunk of up to KC blocks): 4 waves, 2 tiles each.  A
+// workgroup issues all its weight loads first (KC x 2 x 8 bytes per lane), builds the
+// 16-replica trit table, quantises the chunk's activation into the LDS image
+// [block][mfma 3][g 4][A row 16][16 B] (padded) with per (block, token) scales, then runs the tiles.
+// With several K chunks each writes fp32 partial sums [chunk][t][n] to a workspace and a
+// second launch adds them in chunk order: deterministic.  (A last-arriver reduction inside
+// the kernel needs a device-scope release per workgroup, an L2 write-back on this chip,
+// which costs far more than the extra launch.)
+constexpr int kWideRows = 128;              // rows per job: 4 waves x 2 tiles x 16
+// A image strides: per lane group 256 B of rows + 16 B, per MFMA 4 groups, per block 3
+// MFMAs.  The pads spread the quantiser's byte stores over the LDS banks (a store
+// instruction of the unpadded layout needs ~15 passes, this one ~1.25); the A reads stay
+// 256 contiguous bytes per 16 lanes.
+constexpr int kWideG = 272, kWideM = 4 * kWideG;
+constexpr int kWideBlkBytes = 3 * kWideM;
+constexpr int kWideLR = 4;                  // 16 trit-table replicas (16 KB)
+
+struct alignas(16) WideOffTable {
+    uint16_t v[128];
+};
+constexpr WideOffTable make_wide_off_table() {
+    WideOffTable t{};
+    for (int e = 0; e < 128; e++) {
+        const int o = gemv_elem_img_off(e, 0, 8);   // [mfma][g][row 16][16 B], unpadded
+        t.v[e] = (uint16_t)((o >> 10) * kWideM + ((o >> 8) & 3) * kWideG + (o & 15));
+    }
+    return t;
+}
+__constant__ WideOffTable kWideOff = make_wide_off_table();
+
+template <int KC, bool XF16>
+__global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W, const void* __restrict__ x,
+                                                   float* __restrict__ y, float* __restrict__ ws,
+                                                   int K, int N, int ldy, int T, int kcb, int nsplit) {
+    constexpr int REPS = 1 << kWideLR;
+    __shared__ uint4 lut[lut_bytes(kWideLR) / 16];
+    __shared__ __align__(16) uint8_t img[KC * kWideBlkBytes];
+    __shared__ float2 scl[KC][4];             // [block][token pair]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int xn = lane & 15, g = lane >> 4;
+    const int nb = K >> 7;
+    const int rg = (int)blockIdx.x / nsplit, kc = (int)blockIdx.x - rg * nsplit;
+    const int b0 = kc * kcb, nblk = min(kcb, nb - b0);
+
+    // (1) the activation chunks this thread quantises (task j = tid + 256 i = (token, block,
+    // 8-element chunk)), then all weight loads of the job, so both are in flight together
+    constexpr int QI = (8 * KC * 16 + 255) / 256;
+    constexpr int XW = XF16 ? 1 : 2;
+    const int ntask = T * nblk * 16;
+    uint4 xr[QI][XW];
+#pragma unroll
+    for (int i = 0; i < QI; i++) {
+        const int j = tid + 256 * i;
+        if (j < ntask) {
+            const int ch = j & 15, bt = j >> 4;
+            const int t = bt / nblk, b = bt - t * nblk;
+            const size_t k0 = (size_t)t * K + (b0 + b) * 128 + ch * 8;
+            if constexpr (XF16) {
+                xr[i][0] = *(const uint4*)((const _Float16*)x + k0);
+            } else {
+                xr[i][0] = *(const uint4*)((const float*)x + k0);
+                xr[i][XW - 1] = *(const uint4*)((const float*)x + k0 + 4);
+            }
+        }
+    }
+
+    // all weight loads of the job: row (rg, wave, tile, xn), block b0 + b, segment g
+    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
+    const int row0 = rg * kWideRows + wave * 32 + xn;
+    const uint32_t voff = (uint32_t)row0 * row_bytes + (uint32_t)b0 * kBlockBytes + (uint32_t)gemv_seg_byte0(g);
+    uint32_t wl[KC][2], wh[KC][2];
+#pragma unroll
+    for (int b = 0; b < KC; b++)
+#pragma unroll
+        for (int tl = 0; tl < 2; tl++) {
+            const uint32_t so = b < nblk ? (uint32_t)b * kBlockBytes + (uint32_t)tl * 16 * row_bytes : 0x80000000u;
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, (int)voff, (int)so, 0));
+            wl[b][tl] = w.x;
+            wh[b][tl] = w.y;
+        }
+
+    // (2) trit table, cleared image and scales
+#pragma unroll
+    for (int i = 0; i < lut_bytes(kWideLR) / 16 / 256; i++) {
+        const int o = tid + i * 256;
+        const uint32_t bv = (uint32_t)o / (REPS / 4);
+        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
+                       m4 = (m3 * 3u) & 0xffu;
+        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
+                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
+        lut[o] = make_uint4(e, e, e, e);
+    }
+    for (int o = tid; o < KC * kWideBlkBytes / 16; o += 256) ((uint4*)img)[o] = make_uint4(0, 0, 0, 0);
+    if (tid < KC * 4) (&scl[0][0])[tid] = make_float2(0.0f, 0.0f);
+    // LDS-only barrier: the weight loads stay in flight (a fence would wait for them)
+    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+
+    // (3) quantise: task j = (token, block, 8-element chunk), 16 consecutive lanes per
+    // (token, block) for the amax; s = amax / 32639, q = rint(x * 32639 / amax), limbs
+    // hi = (q + 128) >> 8 at A row 2t and lo = q - 256 hi at row 2t + 1
+#pragma unroll
+    for (int i = 0; i < QI; i++) {
+        const int j = tid + 256 * i;
+        if (j >= ntask) break;                    // whole 16-lane rows drop out together
+        const int ch = j & 15, bt = j >> 4;
+        const int t = bt / nblk, b = bt - t * nblk;
+        float v[8];
+        if constexpr (XF16) {
+            const uint32_t w4[4] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const v2h h = __builtin_bit_cast(v2h, w4[q]);
+                v[2 * q] = (float)h[0];
+                v[2 * q + 1] = (float)h[1];
+            }
+        } else {
+            const uint4 a = xr[i][0], c = xr[i][XW - 1];
+            v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
+            v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
+            v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
+        }
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(v[e]));
+        a = row16_max(a);
+        const float inv = a > 0.0f ? kQMax / a : 0.0f;
+        if (ch == 0) {
+            float* sp = &scl[b][t >> 1].x;
+            sp[t & 1] = a * (1.0f / kQMax);
+        }
+        const uint4 ow4 = *(const uint4*)&kWideOff.v[8 * ch];
+        const uint32_t ow[4] = {ow4.x, ow4.y, ow4.z, ow4.w};
+        uint8_t* ib = img + b * kWideBlkBytes + 32 * t;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int off = (int)((ow[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+            const int q = (int)rintf(v[e] * inv);
+            ib[off] = (uint8_t)((q + 128) >> 8);
+            ib[off + 16] = (uint8_t)q;
+        }
+    }
+    // LDS-only barrier: the weight loads stay in flight (a fence would wait for them)
+    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+
+    // (4) tiles: per block the A operand once, then the wave's two tiles
+    const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
+    lds_u8* lb = (lds_u8*)lut;
+    const uint8_t* xa = img + g * kWideG + xn * 16;
+    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+#pragma unroll
+    for (int b = 0; b < KC; b++) {
+        if (b >= nblk) break;
+        v4i A[kMfmaPerBlock];
+#pragma unroll
+        for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(xa + b * kWideBlkBytes + m * kWideM);
+        const float2 s = scl[b][g];
+#pragma unroll
+        for (int tl = 0; tl < 2; tl++) {
+            const uint32_t w0 = wl[b][tl], w1 = wh[b][tl];
+            v4i B[kMfmaPerBlock];
+            B[0] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 1, laneoff)),
+                       (int)lds_u32(lb, lut_addr<kWideLR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 3, laneoff))};
+            B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 0, laneoff)),
+                       (int)lds_u32(lb, lut_addr<kWideLR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 2, laneoff))};
+            B[2] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
+            v4i D = {0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], D, 0, 0, 0);
+            // the row's scale sits in bytes 26..27, read by lane group 0
+            const uint32_t dbits = (uint32_t)__builtin_amdgcn_ds_bpermute(xn * 4, (int)w1) >> 16;
+            const float d = half_bits_to_float(dbits);
+            acc[tl][0] += (float)(D[0] * 256 + D[1]) * (d * s.x);
+            acc[tl][1] += (float)(D[2] * 256 + D[3]) * (d * s.y);
+        }
+    }
+
+    // (5) results: tokens 2g, 2g + 1 of rows row0 and row0 + 16
+    const int t0 = 2 * g;
+    if (nsplit == 1) {
+#pragma unroll
+        for (int tl = 0; tl < 2; tl++) {
+            const int row = row0 + 16 * tl;
+            if (row < N) {
+                if (t0 < T) y[(size_t)t0 * ldy + row] = acc[tl][0];
+                if (t0 + 1 < T) y[(size_t)(t0 + 1) * ldy + row] = acc[tl][1];
+            }
+        }
+        return;
+    }
+    float* wp = ws + (size_t)kc * T * N;
+#pragma unroll
+    for (int tl = 0; tl < 2; tl++) {
+        const int row = row0 + 16 * tl;
+        if (row < N) {
+            if (t0 < T) wp[(size_t)t0 * N + row] = acc[tl][0];
+            if (t0 + 1 < T) wp[(size_t)(t0 + 1) * N + row] = acc[tl][1];
+        }
+    }
+}
+
+// y[t][row] = sum of the K chunks' partial sums in chunk order (deterministic)
+__global__ __launch_bounds__(256) void k_gemv_wide_sum(const float* __restrict__ ws, float* __restrict__ y, int N,
+                                                       int ldy, int T, int nsplit) {
+    const int o = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (o >= T * N) return;
+    const int t = o / N, row = o - t * N;
+    float sum = 0.0f;
+    for (int c = 0; c < nsplit; c++) sum += ws[(size_t)c * T * N + o];
+    y[(size_t)t * ldy + row] = sum;
+}
+
 }  // namespace
 
 // steps (of 4 blocks) per tile; blocks past K are zero padding
@@ -680,6 +906,58 @@ hipError_t launch_gemv_ptq1_multi(int count, const uint8_t* const* W, float* con
 hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                             hipStream_t s) {
     return launch_gemv_ptq1_multi(1, &W, &y, &N, x, x_dtype, x_layout, K, T, s);
+}
+
+hipError_t gemm_device(bool need_ws, int* n_cu, float** ws);
+
+// Wide GEMV launch: row groups of 128 rows x K chunks of at most kWideKC blocks; more
+// chunks than needed until there are about two jobs per CU.  With several chunks the
+// partial sums use the GEMM's per-device workspace (n_cu x 128 KB); rows beyond what it
+// holds go to further launches.
+constexpr int kWideKC = 11;   // 3 workgroups per CU: LDS 16 KB table + 11 x 3 KB image
+hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                            hipStream_t s) {
+    int n_cu = 0;
+    float* ws = nullptr;
+    hipError_t e = gemm_device(false, &n_cu, &ws);
+    if (e != hipSuccess) return e;
+    const int nb = K / kGroup;
+    const size_t row_bytes = (size_t)nb * kBlockBytes;
+    const size_t ws_floats = (size_t)n_cu * 256 * 128;
+    // rows per launch: 32-bit buffer offsets
+    const int max_rows = (int)((((size_t)1 << 31) / row_bytes) / kWideRows * kWideRows);
+    for (int n0 = 0; n0 < N;) {
+        int rows = std::min(N - n0, max_rows);
+        const int groups_all = (rows + kWideRows - 1) / kWideRows;
+        // one round of jobs on 3 workgroups per CU when the rows allow it, else the fewest
+        // K chunks (several rounds)
+        const int slots = 3 * n_cu;
+        int nsplit = (nb + kWideKC - 1) / kWideKC;
+        if ((long long)groups_all * nsplit < slots) nsplit = std::max(nsplit, std::min(nb, slots / groups_all));
+        const int kcb = (nb + nsplit - 1) / nsplit;
+        nsplit = (nb + kcb - 1) / kcb;
+        if (nsplit > 1) {
+            if ((e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
+            const size_t fit = ws_floats / ((size_t)nsplit * T) / kWideRows * kWideRows;
+            if (fit == 0) return hipErrorInvalidValue;
+            rows = (int)std::min<size_t>((size_t)rows, fit);
+        }
+        const int groups = (rows + kWideRows - 1) / kWideRows;
+        if (x_dtype == 1)
+            hipLaunchKernelGGL((k_gemv_wide<kWideKC, true>), dim3(groups * nsplit), dim3(256), 0, s,
+                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit);
+        else
+            hipLaunchKernelGGL((k_gemv_wide<kWideKC, false>), dim3(groups * nsplit), dim3(256), 0, s,
+                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (nsplit > 1) {
+            hipLaunchKernelGGL(k_gemv_wide_sum, dim3((T * rows + 255) / 256), dim3(256), 0, s, ws, y + n0, rows, N, T,
+                               nsplit);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        n0 += rows;
+    }
+    return hipSuccess;
 }
 
 int gemv_max_mats() { return kMaxMats; }

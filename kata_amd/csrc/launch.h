@@ -14,6 +14,9 @@ hipError_t launch_gemv_ptq1_multi(int count, const uint8_t* const* W, float* con
                                   int x_dtype, int x_layout, int K, int T, hipStream_t s);
 int gemv_max_k(int T);   // largest K the PTQ1_0 GEMV accepts (its activation image lives in LDS)
 int gemv_max_mats();     // most matrices one launch takes
+// wide verification GEMV, T in 1..8 token rows x [T][K] (fp16 or fp32), y [T][N]
+hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                            hipStream_t s);
 
 // ---- Q8_0 GEMV (gemv_q8.hip)
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,

@@ -63,6 +63,15 @@ def gemv_ptq1_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, half2: bool = F
     return ys
 
 
+def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Wide verification GEMV: y[T][N] fp32 for x [T][K] (fp16 or fp32), T = x.shape[0] in 1..8."""
+    _need_gpu(W, x)
+    T = x.shape[0]
+    y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
+    check(lib().kata_gemv_ptq1_wide(_ptr(W), _ptr(x), _xdtype(x), _ptr(y), K, N, T, _stream(W)))
+    return y
+
+
 def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
             out: torch.Tensor | None = None) -> torch.Tensor:
     _need_gpu(W, x)

@@ -157,3 +157,15 @@ def test_dispatch_ffn_rejects():
         lib.kata_dispatch_destroy(h)
     # g, u fp32 + h, t fp16 + int8 rows + 16 alignment + scales
     assert lib.kata_ffn_prefill_work_bytes(1024, 2048, 8) == 8 * 2048 * 8 + 8 * 1024 * 2 + 8 * 2048 * 2 + 8 * 2048 + 16 + 16 * 8 * 4
+
+
+def test_gemv_wide_rejects():
+    lib = L.lib()
+    p = FAKE
+    assert lib.kata_gemv_ptq1_wide(p, p, 1, p, 1024, 16, 0, None) == KATA_EINVAL
+    assert lib.kata_gemv_ptq1_wide(p, p, 1, p, 1024, 16, 9, None) == KATA_EINVAL
+    assert lib.kata_gemv_ptq1_wide(p, p, 1, p, 1000, 16, 4, None) == KATA_EINVAL
+    assert lib.kata_gemv_ptq1_wide(p, p, 1, p, 1024, 0, 4, None) == KATA_EINVAL
+    assert lib.kata_gemv_ptq1_wide(p, p, 7, p, 1024, 16, 4, None) == KATA_EINVAL
+    assert lib.kata_gemv_ptq1_wide(p, ctypes.c_void_p(0x10008), 1, p, 1024, 16, 4, None) == KATA_EINVAL
+    assert lib.kata_gemv_ptq1_wide(None, p, 1, p, 1024, 16, 4, None) == KATA_EINVAL
