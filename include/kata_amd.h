@@ -214,6 +214,14 @@ int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp
                               const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
                               float* out, int H, int F, int M, void* stream);
 size_t kata_ffn_prefill_work_bytes(int H, int F, int M);
+/* The same for T in 1..8 verification tokens (Engine::verifyWide's FFN block,
+ * src/engine.cpp:627-629): fp16 token rows through kata_gemv_ptq1_wide (its workspace
+ * rules apply).  x, y, xnew, out fp32 [T][H]; work of kata_ffn_verify_work_bytes(H, F, T)
+ * bytes, 16-byte aligned. */
+int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
+                             const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
+                             float* out, int H, int F, int T, void* stream);
+size_t kata_ffn_verify_work_bytes(int H, int F, int T);
 
 #ifdef __cplusplus
 }

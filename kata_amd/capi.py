@@ -70,6 +70,8 @@ SIGNATURES = {
     "kata_dispatch_ffn_decode": (I, [P, U64, U64, U64, P, P, P, P, P, P, P, I, I, P]),
     "kata_dispatch_ffn_prefill": (I, [P, U64, U64, U64, P, P, P, P, P, P, P, I, I, I, P]),
     "kata_ffn_prefill_work_bytes": (SZ, [I, I, I]),
+    "kata_dispatch_ffn_verify": (I, [P, U64, U64, U64, P, P, P, P, P, P, P, I, I, I, P]),
+    "kata_ffn_verify_work_bytes": (SZ, [I, I, I]),
 }
 
 

@@ -401,6 +401,29 @@ int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp
     return kata_dispatch_prefill(d, offDown, t, out, M, F, H, "down", A8, SX, M, stream);
 }
 
+// The sublayer for T <= 8 verification tokens (Engine::verifyWide's FFN, src/engine.cpp:
+// 627-629): fp16 token rows through the wide GEMV.  work: fp16 h [T][H], fp32 g, u [T][F],
+// fp16 t [T][F].
+int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
+                             const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
+                             float* out, int H, int F, int T, void* stream) {
+    if (!d || !x || !gs_in || !gs_down || !work || !out) return fail(KATA_EINVAL, "null argument");
+    if (H % 1024 != 0 || F % 1024 != 0 || H <= 0 || F <= 0 || T < 1 || T > 8)
+        return fail(KATA_EINVAL, "H=%d F=%d must be multiples of 1024, T=%d in 1..8", H, F, T);
+    uint16_t* h = (uint16_t*)work;
+    float* g = (float*)(h + (size_t)T * H);
+    float* u = g + (size_t)T * F;
+    uint16_t* t = (uint16_t*)(u + (size_t)T * F);
+    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_F16, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, T, stream);
+    if (rc) return rc;
+    if ((rc = kata_gemv_ptq1_wide(d->wbase + offGate, h, KATA_F16, g, H, F, T, stream))) return rc;
+    if ((rc = kata_gemv_ptq1_wide(d->wbase + offUp, h, KATA_F16, u, H, F, T, stream))) return rc;
+    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_F16, KATA_X_ROWS, F, T, 1, stream))) return rc;
+    return kata_gemv_ptq1_wide(d->wbase + offDown, t, KATA_F16, out, F, H, T, stream);
+}
+
+size_t kata_ffn_verify_work_bytes(int H, int F, int T) { return (size_t)T * H * 2 + (size_t)T * F * 10; }
+
 size_t kata_ffn_prefill_work_bytes(int H, int F, int M) {
     const size_t kmax = (size_t)std::max(H, F);
     return (size_t)M * F * 8 + (size_t)M * H * 2 + (size_t)M * F * 2 + (size_t)M * kmax + 16 + kmax / 128 * M * 4;

@@ -6,6 +6,8 @@ src/engine.cpp:27) and maps (byte offset, K, N, matrix name) to the kernels:
   prefill(wOff, A, C, K, N, name)   <- Engine::dExpandGemm (src/engine.cpp:208-219)
   set_i8(spec) / i8(name)           <- Engine::setI8 / i8 (src/engine.cpp:529-537,
                                        src/engine.h:89-95)
+  ffn_decode / ffn_prefill / ffn_verify  <- the FFN block of Engine::step, prefill and
+                                       verifyWide (src/engine.cpp:176-182, 247-300, 627-629)
 Errors raise KataError instead of the reference's exit(1).
 """
 from __future__ import annotations
@@ -91,6 +93,21 @@ class Dispatch:
         check(lib().kata_dispatch_ffn_prefill(self._h, offGate, offUp, offDown, _ptr(x), _ptr(y), _ptr(xnew),
                                               _ptr(gs_in), _ptr(gs_down), _ptr(work), _ptr(out), H, F, M,
                                               _stream(self.wbuf)))
+        return out
+
+    def ffn_verify(self, offGate: int, offUp: int, offDown: int, x: torch.Tensor, y: torch.Tensor | None,
+                   gs_in: torch.Tensor, gs_down: torch.Tensor, H: int, F: int, out: torch.Tensor | None = None,
+                   xnew: torch.Tensor | None = None, work: torch.Tensor | None = None) -> torch.Tensor:
+        """The FFN sublayer for T = x.shape[0] <= 8 verification tokens (wide GEMVs)."""
+        T = x.shape[0]
+        dev = x.device
+        if out is None:
+            out = torch.empty((T, H), dtype=torch.float32, device=dev)
+        if work is None:
+            work = torch.empty(int(lib().kata_ffn_verify_work_bytes(H, F, T)), dtype=torch.uint8, device=dev)
+        check(lib().kata_dispatch_ffn_verify(self._h, offGate, offUp, offDown, _ptr(x), _ptr(y), _ptr(xnew),
+                                             _ptr(gs_in), _ptr(gs_down), _ptr(work), _ptr(out), H, F, T,
+                                             _stream(self.wbuf)))
         return out
 
 

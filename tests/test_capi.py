@@ -153,8 +153,11 @@ def test_dispatch_ffn_rejects():
         assert lib.kata_dispatch_ffn_decode(None, 0, 0, 0, p, None, None, p, p, p, p, 2048, 3072, None) == KATA_EINVAL
         assert lib.kata_dispatch_ffn_prefill(h, 0, 0, 0, p, None, None, p, p, p, p, 2048, 3072, 0, None) == KATA_EINVAL
         assert lib.kata_dispatch_ffn_prefill(h, 0, 0, 0, p, None, None, p, None, p, p, 2048, 3072, 4, None) == KATA_EINVAL
+        assert lib.kata_dispatch_ffn_verify(h, 0, 0, 0, p, None, None, p, p, p, p, 2048, 3072, 9, None) == KATA_EINVAL
+        assert lib.kata_dispatch_ffn_verify(h, 0, 0, 0, p, None, None, p, p, p, p, 2000, 3072, 2, None) == KATA_EINVAL
     finally:
         lib.kata_dispatch_destroy(h)
+    assert lib.kata_ffn_verify_work_bytes(1024, 2048, 3) == 3 * 1024 * 2 + 3 * 2048 * 10
     # g, u fp32 + h, t fp16 + int8 rows + 16 alignment + scales
     assert lib.kata_ffn_prefill_work_bytes(1024, 2048, 8) == 8 * 2048 * 8 + 8 * 1024 * 2 + 8 * 2048 * 2 + 8 * 2048 + 16 + 16 * 8 * 4
 

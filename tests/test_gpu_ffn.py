@@ -142,3 +142,37 @@ def test_ffn_prefill_decode_agree(dev):
     a = d.ffn_decode(og, ou, od, T(x[0]), T(y[0]), T(gs_in), T(gs_down), H, F).cpu().numpy()
     b = d.ffn_prefill(og, ou, od, T(x), T(y), T(gs_in), T(gs_down), H, F).cpu().numpy()
     assert rel_l2(b, a[None]).max() < 1e-2
+
+
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_ffn_verify(dev, T):
+    """T verification tokens through the wide GEMV: each step against the oracle fed with
+    the GPU's previous step (work buffer: h fp16 [T][H], g, u fp32 [T][F], t fp16 [T][F]),
+    then end to end against the composition from x (fp16 rounding of h and t may differ by
+    one ulp from the double-precision composition)."""
+    from kata_amd.capi import lib
+    H, F = 2048, 3072
+    buf, (og, ou, od), W = _weights(H, F, 42 + T)
+    Wg, Wu, Wd = W
+    d = Dispatch(torch.from_numpy(buf).to(dev))
+    x, y, gs_in, gs_down = _inputs(T, H, F, 17 + T)
+    Tt = lambda a: torch.from_numpy(a).to(dev)
+    xnew = torch.empty((T, H), dtype=torch.float32, device=dev)
+    work = torch.full((int(lib().kata_ffn_verify_work_bytes(H, F, T)),), 0x7f, dtype=torch.uint8, device=dev)
+    out = d.ffn_verify(og, ou, od, Tt(x), Tt(y), Tt(gs_in), Tt(gs_down), H, F, xnew=xnew, work=work).cpu().numpy()
+    assert np.array_equal(xnew.cpu().numpy(), x + y)
+    wk = work.cpu().numpy()
+    o = 0
+    h = wk[o:o + 2 * T * H].view(np.float16).reshape(T, H); o += 2 * T * H
+    g = wk[o:o + 4 * T * F].view(np.float32).reshape(T, F); o += 4 * T * F
+    u = wk[o:o + 4 * T * F].view(np.float32).reshape(T, F); o += 4 * T * F
+    t = wk[o:o + 2 * T * F].view(np.float16).reshape(T, F)
+    h_ref, _ = orc.norm_fwht(x, gs_in, 0, src2=y, add=True)
+    assert np.abs(h.astype(np.float64) - h_ref).max() <= np.abs(h_ref).max() * 2.0 ** -11
+    assert rel_l2(g, orc.gemv_ptq1(Wg, h.astype(np.float32), H, F, T)).max() < 2e-4
+    assert rel_l2(u, orc.gemv_ptq1(Wu, h.astype(np.float32), H, F, T)).max() < 2e-4
+    t_ref, _ = orc.norm_fwht(g, gs_down, 1, src2=u)
+    assert np.abs(t.astype(np.float64) - t_ref).max() <= np.abs(t_ref).max() * 2.0 ** -11
+    assert rel_l2(out, orc.gemv_ptq1(Wd, t.astype(np.float32), F, H, T)).max() < 2e-4
+    ref = _ref_decode(W, x[:1], y[:1], gs_in, gs_down, H, F)
+    assert rel_l2(out[:1], ref).max() < 2e-3
