@@ -257,10 +257,14 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
 
 // Work split ("activation-stationary").  One 1024-thread workgroup (16 waves) per CU owns
 // the contiguous tile range [wt0, wt0 + Tt) (4 rows per tile) of one matrix.  Its work
-// items (c, tile) — 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered
-// c-major, s = c * Tt + tile, and cut into 16 equal contiguous runs, one per wave, so a wave
-// keeps the A operand of one block step c in registers across many tiles and reloads it
-// from LDS only when c changes.  Lane x + 16*g: B column x = (row r = x & 3, block 4c + kq
+// items (c, tile) — 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered by
+// pairs of block steps, s = (c / 2) * 2 Tt + 2 tile + c % 2 (nq rounded up to even), and cut
+// into 16 contiguous runs of even length, one per wave, so a wave keeps the A operands of
+// one pair (c, c + 1) in registers across many tiles and reloads them from LDS only when the
+// pair changes.  Consecutive items of a wave read the two halves of 224 contiguous bytes of
+// each row, so a 128-byte line shared by block steps c and c + 1 is read twice in a row;
+// with the steps a whole pass over the tiles apart, a launch whose weights exceed an XCD's
+// L2 fetched such lines twice from memory.  Lane x + 16*g: B column x = (row r = x & 3, block 4c + kq
 // with kq = x >> 2), A row x = (block 4c + (x >> 2), token (x >> 1) & 1, limb x & 1);
 // result rows 4g..4g+3 belong to block 4c + g, so lane 20*q + r holds row r's sum over
 // block 4c + q.  Those 16 lanes store their scaled sums to the item's LDS slot (the other
@@ -330,9 +334,9 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const int tiles = (N + 3) >> 2;
     const int wt0 = ((int)blockIdx.x - wg0) * tpw;
     const int Tt = min(tiles, wt0 + tpw) - wt0;
-    const int S = nq * Tt;
-    const int s0 = (wave * S) / kWaves, s1 = ((wave + 1) * S) / kWaves;
-    const int n = s1 - s0;                       // this wave's run length (wave-uniform)
+    const int S = nq * Tt;                       // nq is even: whole pairs of block steps
+    const int s0 = ((wave * S) / kWaves) & ~1, s1 = wave == kWaves - 1 ? S : (((wave + 1) * S) / kWaves) & ~1;
+    const int n = s1 - s0;                       // this wave's run length (even, wave-uniform)
     const int qbytes = nq * BLK;                 // A image bytes per quarter
     uint8_t* As = smem;
     uint8_t* Ss = smem + gemv_a_lds_bytes(qbytes);            // (scale, 0) pairs [vb][t]
@@ -389,19 +393,27 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
     const uint32_t voff = (uint32_t)r * row_bytes + (uint32_t)kq * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
-    int lt = s0 % Tt;                            // load cursor: tile, item offset, items left
-    uint32_t lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(s0 / Tt) * 4 * kBlockBytes;
+    // item s = (c/2, tile, c%2): pair index s / (2 Tt), tile (s % (2 Tt)) / 2, block step
+    // parity s % 2; runs start at even s, so the ring slot's parity is the item's
+    int lt = (s0 % (2 * Tt)) >> 1;               // load cursor: tile, item offset, items left
+    uint32_t lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(2 * (s0 / (2 * Tt))) * 4 * kBlockBytes;
     int lrem = n;
-    const uint32_t cwrap = 4 * kBlockBytes - (uint32_t)(Tt - 1) * tstep;   // last tile -> next c
+    const uint32_t cstep = 4 * kBlockBytes;      // even c -> c + 1, same tile
+    const uint32_t tnext = tstep - cstep;        // odd c -> c - 1, next tile
+    const uint32_t cwrap = cstep - (uint32_t)(Tt - 1) * tstep;   // odd c, last tile -> next pair
     uint32_t wl[D], wh[D];
     auto load_next = [&](int slot) {
         const uint32_t so = lrem > 0 ? lso : 0x80000000u;
         const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, (int)voff, (int)so, 0));
         wl[slot] = w.x;
         wh[slot] = w.y;
-        const bool wrap = ++lt == Tt;
-        lt = wrap ? 0 : lt;
-        lso += wrap ? cwrap : tstep;
+        if (slot & 1) {
+            const bool wrap = ++lt == Tt;
+            lt = wrap ? 0 : lt;
+            lso += wrap ? cwrap : tnext;
+        } else {
+            lso += cstep;
+        }
         --lrem;
     };
 #pragma unroll
@@ -470,13 +482,17 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // their scratch word: address = base + diag * item offset
     const uint32_t diag = g == kq ? 1u : 0u;
     uint8_t* pbase = diag ? (uint8_t*)part + (g * 4 + r) * 4 : Js + lane * 4;
-    v4i A[kMfmaPerBlock];
-    float sc[T];
-    auto load_a = [&](int c) {
+    v4i A[2][kMfmaPerBlock];                     // block steps 2 cp and 2 cp + 1
+    float sc[2][T];
+    auto load_a = [&](int cp) {
 #pragma unroll
-        for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(xa + c * BLK + m * ASTRIDE);
+        for (int h = 0; h < 2; h++) {
+            const int c = 2 * cp + h;
 #pragma unroll
-        for (int t = 0; t < T; t++) sc[t] = xs[c * 8 * T + 2 * t];
+            for (int m = 0; m < kMfmaPerBlock; m++) A[h][m] = *(const v4i*)(xa + c * BLK + m * ASTRIDE);
+#pragma unroll
+            for (int t = 0; t < T; t++) sc[h][t] = xs[c * 8 * T + 2 * t];
+        }
     };
     auto decode = [&](uint32_t w0, uint32_t w1, v4i* B) {
         B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 1, laneoff)),
@@ -485,7 +501,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
                    (int)lds_u32(lb, lut_addr<LR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w1, 2, laneoff))};
         B[2] = v4i{(int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
     };
-    int ct = s0 % Tt, cv = s0 / Tt;              // compute cursor: tile, block step
+    int ct = (s0 % (2 * Tt)) >> 1, cp = s0 / (2 * Tt);   // compute cursor: tile, pair
     uint32_t pofs = (uint32_t)s0 * T * 64;        // item slot offset (bytes)
     v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
     // item in ring slot u; `next`: item + 1 is in the run (its operands are read here)
@@ -495,21 +511,21 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         const v4i* B = (u & 1) ? B1 : B0;
         v4i Dm = {0, 0, 0, 0};
 #pragma unroll
-        for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], Dm, 0, 0, 0);
+        for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
         float d = half_bits_to_float(wh[u] >> 16);
-        if (PAD && 4 * cv + kq >= nb) d = 0.0f;
+        if (PAD && 4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
         float* dst = (float*)(pbase + diag * pofs);
 #pragma unroll
-        for (int t = 0; t < T; t++) dst[16 * t] = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[t]);
+        for (int t = 0; t < T; t++) dst[16 * t] = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[u & 1][t]);
         pofs += T * 64;
-        if (++ct == Tt) {
+        if ((u & 1) && ++ct == Tt) {
             ct = 0;
-            ++cv;
-            if (next) load_a(cv);
+            ++cp;
+            if (next) load_a(cp);
         }
     };
     if (n > 0) {
-        load_a(cv);
+        load_a(cp);
         decode(wl[0], wh[0], B0);
     }
     int j = 0;
@@ -533,7 +549,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         const int tl = o / (4 * T), rr = (o / T) & 3, t = o % T;
         float sum = 0.0f;
         for (int c = sub; c < nq; c += 16) {
-            const float* p = part + ((c * Tt + tl) * T + t) * 16 + rr;
+            const float* p = part + ((((c >> 1) * Tt + tl) * 2 + (c & 1)) * T + t) * 16 + rr;
 #pragma unroll
             for (int q = 0; q < 4; q++) sum += p[4 * q];
         }
@@ -771,8 +787,8 @@ __global__ __launch_bounds__(256) void k_gemv_wide_sum(const float* __restrict__
 
 }  // namespace
 
-// steps (of 4 blocks) per tile; blocks past K are zero padding
-static int gemv_nq(int K) { return (K / kGroup + 3) / 4; }
+// steps (of 4 blocks) per tile, rounded up to whole pairs; blocks past K are zero padding
+static int gemv_nq(int K) { return ((K / kGroup + 3) / 4 + 1) & ~1; }
 
 constexpr int kLdsMax = 160 * 1024;
 
@@ -820,9 +836,9 @@ template <int T, int LR, bool XS>
 static hipError_t launch_gemv_pad(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
                                   hipStream_t s) {
     if (P.count > 1)
-        return (K / kGroup) % 4 ? launch_gemv_cfg<T, LR, true, XS, true>(P, x, x_dtype, x_layout, K, lds, s)
+        return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XS, true>(P, x, x_dtype, x_layout, K, lds, s)
                                 : launch_gemv_cfg<T, LR, false, XS, true>(P, x, x_dtype, x_layout, K, lds, s);
-    return (K / kGroup) % 4 ? launch_gemv_cfg<T, LR, true, XS, false>(P, x, x_dtype, x_layout, K, lds, s)
+    return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XS, false>(P, x, x_dtype, x_layout, K, lds, s)
                             : launch_gemv_cfg<T, LR, false, XS, false>(P, x, x_dtype, x_layout, K, lds, s);
 }
 
