@@ -333,21 +333,31 @@ def main():
         else:
             runners[fname] = fn
 
-    def timed(fname, n_steps):
+    batch_ms = []
+
+    def timed(fname, n_steps, nbatch=1):
+        """ms of n_steps steps; with nbatch > 1 also events between nbatch equal batches of
+        them (batch_ms), for the best / median batch figures."""
         run = runners[fname]
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(nbatch + 1)]
+        cuts = [(b * n_steps) // nbatch for b in range(nbatch + 1)]
         torch.cuda.synchronize()
-        e0.record(stream)
+        ev[0].record(stream)
+        b = 1
         for i in range(n_steps):
             run(i)
-        e1.record(stream)
+            while b <= nbatch and cuts[b] == i + 1:
+                ev[b].record(stream)
+                b += 1
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1)
+        if nbatch > 1:
+            batch_ms[:] = [ev[j].elapsed_time(ev[j + 1]) / max(1, cuts[j + 1] - cuts[j]) for j in range(nbatch)]
+        return ev[0].elapsed_time(ev[nbatch])
 
     for i in range(args.warmup):
         runners["step"](i)
     torch.cuda.synchronize()
-    ms_total = timed("step", args.steps)
+    ms_total = timed("step", args.steps, nbatch=8 if args.steps >= 8 else 1)
     ms_step = ms_total / args.steps
     value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
     if args.step_only:
@@ -556,6 +566,9 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_ptq1<1>", "avg_launch_us": round(gemv_launch_us, 3),
                      "bytes_per_launch": bytes_per_launch},
+        "step_batches": ({"n": len(batch_ms), "best_GBps": round(set_bytes / (min(batch_ms) * 1e-3) / 1e9, 1),
+                          "median_GBps": round(set_bytes / (float(np.median(batch_ms)) * 1e-3) / 1e9, 1)}
+                         if batch_ms else None),
         "one_launch_per_matrix": {"ms_per_step": round(ms_single / args.steps, 5),
                                   "GBps": round(set_bytes * args.steps / (ms_single * 1e-3) / 1e9, 1)},
         "per_matrix": per_matrix,

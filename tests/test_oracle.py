@@ -276,3 +276,20 @@ def test_norm_fwht_swiglu_and_gdn_order():
     back = np.concatenate([orc.norm_fwht(out[:, 1024 * k:1024 * (k + 1)].astype(np.float32), ones, 3)[0]
                            for k in range(6)], axis=1)
     assert np.abs(back[0] - perm).max() < 1e-3
+
+
+def test_float_pipe_identity_exhaustive(golden):
+    """The reference's float-pipe decode (shaders/gemv_fast.metal:2-3): with u = b / 256 and
+    g_k = floor(3^k u), digit n = g_{n+1} - 3 g_n, evaluated in fp32 (exact: 3^5 * 255 =
+    61965 < 2^24), equals the integer digit for all 256 bytes x 5 digits; and its
+    coefficient form sum_n t_n y_n = sum_{k=1..4} g_k (y_{k-1} - 3 y_k) + g_5 y_4 holds."""
+    b = np.arange(256, dtype=np.float32)
+    u = b / np.float32(256.0)
+    g = [np.floor(np.float32(3.0 ** k) * u) for k in range(6)]
+    digits = np.stack([g[n + 1] - 3 * g[n] for n in range(5)], axis=1).astype(np.int64)
+    assert np.array_equal(digits, golden["digit_table"].astype(np.int64))
+    assert np.array_equal(digits, np.array([[orc.digit(int(v), n) for n in range(5)] for v in range(256)]))
+    y = np.random.default_rng(0).standard_normal((256, 5))
+    lhs = (digits * y).sum(axis=1)
+    rhs = sum(g[k].astype(np.float64) * (y[:, k - 1] - 3 * y[:, k]) for k in range(1, 5)) + g[5] * y[:, 4]
+    assert np.allclose(lhs, rhs, rtol=0, atol=1e-12)
