@@ -341,8 +341,8 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     uint8_t* As = smem;
     uint8_t* Ss = smem + gemv_a_lds_bytes(qbytes);            // (scale, 0) pairs [vb][t]
     uint8_t* Os = Ss + gemv_s_lds_bytes(nbv, T);               // scatter offsets [64][8] u16
-    uint8_t* Js = Os + 1024;                                   // scratch slot [T][64] floats
-    float* part = (float*)(Js + 512);                          // [S][T][16]
+    uint8_t* Js = Os + 1024;                                   // scratch slots (1 KB)
+    float* part = (float*)(Js + 1024);                         // [S][T][16]
     uint8_t* Xs = (uint8_t*)part;                // XS: raw activation, until the main loop
 
     // (1a) wave 0: DMA of the scatter offsets and (XS) the raw activation; without XS every
@@ -479,9 +479,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const uint8_t* xa = As + kq * (qbytes + QPAD) + g * (2 * T * 16) + (x_ & (2 * T - 1)) * 16;
     const float* xs = (const float*)Ss + kq * (2 * T);
     // item sums: the diagonal lanes 20*q + r store to slot 4q + r of the item, the others to
-    // their scratch word: address = base + diag * item offset
+    // a scratch word.  Item u of a ring pass stores at pcur + 64 T u (an immediate offset);
+    // after a pass pcur advances by 64 T D on the diagonal lanes and stays on the others,
+    // whose scratch words Js + 4 lane + 64 T u (u < D) stay inside the 1 KB scratch area.
     const uint32_t diag = g == kq ? 1u : 0u;
-    uint8_t* pbase = diag ? (uint8_t*)part + (g * 4 + r) * 4 : Js + lane * 4;
+    uint8_t* pcur = diag ? (uint8_t*)part + (g * 4 + r) * 4 + (uint32_t)s0 * T * 64 : Js + lane * 4;
+    const uint32_t pinc = diag * (uint32_t)(D * T * 64);
     v4i A[2][kMfmaPerBlock];                     // block steps 2 cp and 2 cp + 1
     float sc[2][T];
     auto load_a = [&](int cp) {
@@ -502,7 +505,6 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         B[2] = v4i{(int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
     };
     int ct = (s0 % (2 * Tt)) >> 1, cp = s0 / (2 * Tt);   // compute cursor: tile, pair
-    uint32_t pofs = (uint32_t)s0 * T * 64;        // item slot offset (bytes)
     v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
     // item in ring slot u; `next`: item + 1 is in the run (its operands are read here)
     auto body = [&](auto uc, bool next) {
@@ -514,10 +516,9 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
         float d = half_bits_to_float(wh[u] >> 16);
         if (PAD && 4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
-        float* dst = (float*)(pbase + diag * pofs);
+        float* dst = (float*)(pcur + u * T * 64);
 #pragma unroll
         for (int t = 0; t < T; t++) dst[16 * t] = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[u & 1][t]);
-        pofs += T * 64;
         if ((u & 1) && ++ct == Tt) {
             ct = 0;
             ++cp;
@@ -534,6 +535,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
             body(uc, true);
             load_next(decltype(uc)::value);
         });
+        pcur += pinc;
     }
     static_for<D>([&](auto uc) {                 // the last 1..D items
         constexpr int u = decltype(uc)::value;
@@ -801,7 +803,7 @@ constexpr int kRing = 4;
 // tpw tiles and (xbytes > 0) the staged raw activation, whole 1 KB DMA chunks
 static int gemv_lds_bytes(int K, int T, int LR, int tpw, int xbytes) {
     const int nq = gemv_nq(K);
-    return gemv_static_lds_bytes(LR) + gemv_a_lds_bytes(nq * kAImageBytes * 2 * T) + gemv_s_lds_bytes(4 * nq, T) + 1536 +
+    return gemv_static_lds_bytes(LR) + gemv_a_lds_bytes(nq * kAImageBytes * 2 * T) + gemv_s_lds_bytes(4 * nq, T) + 2048 +
            std::max(nq * tpw * T * 16 * 4, (xbytes + 1023) & ~1023);
 }
 
