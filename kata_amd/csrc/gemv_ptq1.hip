@@ -502,10 +502,13 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
                    (int)lds_u32(lb, lut_addr<LR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 3, laneoff))};
         B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<LR>(w1, 0, laneoff)),
                    (int)lds_u32(lb, lut_addr<LR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w1, 2, laneoff))};
-        B[2] = v4i{(int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
+        B[2][0] = (int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff));   // B[2][2..3] stay zero
+        B[2][1] = (int)trit0_word(w1);
     };
     int ct = (s0 % (2 * Tt)) >> 1, cp = s0 / (2 * Tt);   // compute cursor: tile, pair
     v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
+    B0[2] = v4i{0, 0, 0, 0};
+    B1[2] = v4i{0, 0, 0, 0};
     // item in ring slot u; `next`: item + 1 is in the run (its operands are read here)
     auto body = [&](auto uc, bool next) {
         constexpr int u = decltype(uc)::value;
