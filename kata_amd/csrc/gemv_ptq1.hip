@@ -268,8 +268,9 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
 // with kq = x >> 2), A row x = (block 4c + (x >> 2), token (x >> 1) & 1, limb x & 1);
 // result rows 4g..4g+3 belong to block 4c + g, so lane 20*q + r holds row r's sum over
 // block 4c + q.  Those 16 lanes store their scaled sums to the item's LDS slot (the other
-// lanes store to a scratch slot: no exec-mask changes in the loop); at the end each
-// output row adds its nq * 4 slots in a fixed order (deterministic, no atomics).
+// lanes store to a scratch slot: no exec-mask changes in the loop; the two items of a step
+// pair add in registers first, halving the slots); at the end each output row adds its
+// nq * 2 slots in a fixed order (deterministic, no atomics).
 //
 // Timeline.  (1) Wave 0 (the first wave of the workgroup to launch) copies the scatter
 // offsets and (XS) the raw activation into LDS by DMA before any weight load is queued on
@@ -342,7 +343,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     uint8_t* Ss = smem + gemv_a_lds_bytes(qbytes);            // (scale, 0) pairs [vb][t]
     uint8_t* Os = Ss + gemv_s_lds_bytes(nbv, T);               // scatter offsets [64][8] u16
     uint8_t* Js = Os + 1024;                                   // scratch slots (1 KB)
-    float* part = (float*)(Js + 1024);                         // [S][T][16]
+    float* part = (float*)(Js + 1024);                         // [S / 2][T][16]
     uint8_t* Xs = (uint8_t*)part;                // XS: raw activation, until the main loop
 
     // (1a) wave 0: DMA of the scatter offsets and (XS) the raw activation; without XS every
@@ -478,13 +479,15 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // A rows with token >= T only feed result rows that are never stored
     const uint8_t* xa = As + kq * (qbytes + QPAD) + g * (2 * T * 16) + (x_ & (2 * T - 1)) * 16;
     const float* xs = (const float*)Ss + kq * (2 * T);
-    // item sums: the diagonal lanes 20*q + r store to slot 4q + r of the item, the others to
-    // a scratch word.  Item u of a ring pass stores at pcur + 64 T u (an immediate offset);
-    // after a pass pcur advances by 64 T D on the diagonal lanes and stays on the others,
-    // whose scratch words Js + 4 lane + 64 T u (u < D) stay inside the 1 KB scratch area.
+    // item sums: the two items of a block-step pair (consecutive, same tile) are added in
+    // registers; the diagonal lanes 20*q + r store the pair's sum to slot 4q + r of the
+    // pair's LDS slot, the others to a scratch word.  Pair u/2 of a ring pass stores at
+    // pcur + 64 T (u/2) (an immediate offset); after a pass pcur advances by 64 T D/2 on the
+    // diagonal lanes and stays on the others, whose scratch words stay inside the 1 KB area.
     const uint32_t diag = g == kq ? 1u : 0u;
-    uint8_t* pcur = diag ? (uint8_t*)part + (g * 4 + r) * 4 + (uint32_t)s0 * T * 64 : Js + lane * 4;
-    const uint32_t pinc = diag * (uint32_t)(D * T * 64);
+    uint8_t* pcur = diag ? (uint8_t*)part + (g * 4 + r) * 4 + (uint32_t)(s0 >> 1) * T * 64 : Js + lane * 4;
+    const uint32_t pinc = diag * (uint32_t)(D / 2 * T * 64);
+    float vprev[T];
     v4i A[2][kMfmaPerBlock];                     // block steps 2 cp and 2 cp + 1
     float sc[2][T];
     auto load_a = [&](int cp) {
@@ -519,9 +522,15 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
         float d = half_bits_to_float(wh[u] >> 16);
         if (PAD && 4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
-        float* dst = (float*)(pcur + u * T * 64);
+        float* dst = (float*)(pcur + (u >> 1) * T * 64);
 #pragma unroll
-        for (int t = 0; t < T; t++) dst[16 * t] = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[u & 1][t]);
+        for (int t = 0; t < T; t++) {
+            const float val = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[u & 1][t]);
+            if (u & 1)
+                dst[16 * t] = vprev[t] + val;
+            else
+                vprev[t] = val;
+        }
         if ((u & 1) && ++ct == Tt) {
             ct = 0;
             ++cp;
@@ -546,15 +555,15 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     });
     __syncthreads();
 
-    // row sums: output (tile tl, row rr, token t) adds its item slots over c ascending and
-    // quarters ascending, 16 lanes per output (lane sub takes c = sub, sub + 16, ...), then
-    // a fixed-order DPP reduction over the 16 lanes
+    // row sums: output (tile tl, row rr, token t) adds its pair slots over step pairs
+    // ascending and quarters ascending, 16 lanes per output (lane sub takes pairs sub,
+    // sub + 16, ...), then a fixed-order DPP reduction over the 16 lanes
     for (int o16 = tid; o16 < Tt * 4 * T * 16; o16 += 1024) {
         const int o = o16 >> 4, sub = o16 & 15;
         const int tl = o / (4 * T), rr = (o / T) & 3, t = o % T;
         float sum = 0.0f;
-        for (int c = sub; c < nq; c += 16) {
-            const float* p = part + ((((c >> 1) * Tt + tl) * 2 + (c & 1)) * T + t) * 16 + rr;
+        for (int cp2 = sub; cp2 < nq / 2; cp2 += 16) {
+            const float* p = part + ((cp2 * Tt + tl) * T + t) * 16 + rr;
 #pragma unroll
             for (int q = 0; q < 4; q++) sum += p[4 * q];
         }
@@ -807,7 +816,7 @@ constexpr int kRing = 4;
 static int gemv_lds_bytes(int K, int T, int LR, int tpw, int xbytes) {
     const int nq = gemv_nq(K);
     return gemv_static_lds_bytes(LR) + gemv_a_lds_bytes(nq * kAImageBytes * 2 * T) + gemv_s_lds_bytes(4 * nq, T) + 2048 +
-           std::max(nq * tpw * T * 16 * 4, (xbytes + 1023) & ~1023);
+           std::max(nq / 2 * tpw * T * 16 * 4, (xbytes + 1023) & ~1023);
 }
 
 static int device_cus() {
