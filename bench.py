@@ -438,6 +438,12 @@ def main():
         yq = torch.empty((1, N), dtype=torch.float32, device=dev)
         us = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq, K, N, 1, out=yq), max(20, args.reps // 4))
         q8[name] = {"K": K, "N": N, "us": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
+        # the MTP head's two-row form (mtpRows, R = 2): both rows per weight read
+        xq2 = torch.from_numpy(np.random.default_rng(SEED + 600 + K).standard_normal((2, K))
+                               .astype(np.float16)).to(dev)
+        yq2 = torch.empty((2, N), dtype=torch.float32, device=dev)
+        us2 = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq2, K, N, 2, out=yq2), max(20, args.reps // 4))
+        q8[name].update({"t2_us": round(us2, 3), "t2_GBps": round(nb / (us2 * 1e-6) / 1e9, 1)})
         del Wqs, Wq
 
     # ---- lm_head (5120 -> 248320 PTQ1_0 GEMV, 278 MB) and the greedy argmax of its logits
