@@ -69,7 +69,8 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
  * chunk in-kernel, same 16-bit block fixed point as above).  Every weight byte is read
  * once for all T rows.  When K is split over workgroups the partial sums use the per-device
  * workspace of kata_gemm_ptq1_f16 (same rules: calls on one device must not overlap, the
- * first such call must not be captured).
+ * first such call must not be captured).  T <= 2 runs the decode GEMV above (same result
+ * as kata_gemv_ptq1 with these rows, no workspace).
  * Replaces Engine::dWide / xWideGemv (src/engine.cpp:542-556, src/engine.h:109,140; kernel
  * k_wide_m16_n16_k128_g4, shaders/wide.metal:41-99, whose x is fp16 rows padded to 16). */
 int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,

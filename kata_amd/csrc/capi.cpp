@@ -93,6 +93,10 @@ int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, 
     if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
     if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
     if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
+    // one or two tokens: the decode GEMV reads the weights once for both as well, faster
+    if (T <= 2 && K <= kata::gemv_max_k(T))
+        return check_launch(kata::launch_gemv_ptq1(W, x, x_dtype, KATA_X_ROWS, y, K, N, T, (hipStream_t)stream),
+                            "gemv ptq1 wide (T <= 2)");
     return check_launch(kata::launch_gemv_wide(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv ptq1 wide");
 }
 
