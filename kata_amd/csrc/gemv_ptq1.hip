@@ -584,10 +584,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 // i = (token i >> 1, limb i & 1) of the same block, so every product of the 16 x 16 result
 // is used: lane x + 16 g ends with the int32 sums of tokens 2g, 2g+1 for row x.
 //
-// Job = (row group of 128 rows, chunk of up to KC blocks): 4 waves, 2 tiles each.  A
-// workgroup issues all its weight loads first (KC x 2 x 8 bytes per lane), builds the
-// 16-replica trit table, quantises the chunk's activation into the LDS image
-// [block][mfma 3][g 4][A row 16][16 B] (padded) with per (block, token) scales, then runs the tiles.
+// Job = (row group of 128 rows, chunk of up to KC blocks): 4 waves, 2 tiles each.  At most
+// 3 workgroups per CU, each on a contiguous range of the chunk-major job list: it builds
+// the 16-replica trit table once, and per job issues all its weight loads (KC x 2 x 8 bytes
+// per lane), quantises the chunk's activation into the LDS image [block][mfma 3][g 4]
+// [A row 16][16 B] (padded) with per (block, token) scales only when the chunk changes,
+// then runs the tiles.
 // With several K chunks each writes fp32 partial sums [chunk][t][n] to a workspace and a
 // second launch adds them in chunk order: deterministic.  (A last-arriver reduction inside
 // the kernel needs a device-scope release per workgroup, an L2 write-back on this chip,
@@ -617,7 +619,7 @@ __constant__ WideOffTable kWideOff = make_wide_off_table();
 template <int KC, bool XF16>
 __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W, const void* __restrict__ x,
                                                    float* __restrict__ y, float* __restrict__ ws,
-                                                   int K, int N, int ldy, int T, int kcb, int nsplit) {
+                                                   int K, int N, int ldy, int T, int kcb, int nsplit, int groups) {
     constexpr int REPS = 1 << kWideLR;
     __shared__ uint4 lut[lut_bytes(kWideLR) / 16];
     __shared__ __align__(16) uint8_t img[KC * kWideBlkBytes];
@@ -625,17 +627,42 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int xn = lane & 15, g = lane >> 4;
     const int nb = K >> 7;
-    const int rg = (int)blockIdx.x / nsplit, kc = (int)blockIdx.x - rg * nsplit;
-    const int b0 = kc * kcb, nblk = min(kcb, nb - b0);
-
-    // (1) the activation chunks this thread quantises (task j = tid + 256 i = (token, block,
-    // 8-element chunk)), then all weight loads of the job, so both are in flight together
     constexpr int QI = (8 * KC * 16 + 255) / 256;
     constexpr int XW = XF16 ? 1 : 2;
+    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
+    // this workgroup's jobs: a contiguous range of the chunk-major job list (job =
+    // kc * groups + rg), so consecutive jobs mostly share the K chunk and its quantised image
+    const int njobs = groups * nsplit;
+    const int j0 = (int)(((long long)blockIdx.x * njobs) / gridDim.x);
+    const int j1 = (int)(((long long)(blockIdx.x + 1) * njobs) / gridDim.x);
+
+    // trit table, once per workgroup (visible after the first job's barriers)
+#pragma unroll
+    for (int i = 0; i < lut_bytes(kWideLR) / 16 / 256; i++) {
+        const int o = tid + i * 256;
+        const uint32_t bv = (uint32_t)o / (REPS / 4);
+        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
+                       m4 = (m3 * 3u) & 0xffu;
+        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
+                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
+        lut[o] = make_uint4(e, e, e, e);
+    }
+    int kc_cur = -1;
+    for (int job = j0; job < j1; job++) {
+    const int kc = job / groups, rg = job - kc * groups;
+    const int b0 = kc * kcb, nblk = min(kcb, nb - b0);
+    const bool newk = kc != kc_cur;
+
+    // (1) for a new K chunk the activation chunks this thread quantises (task j = tid + 256 i
+    // = (token, block, 8-element chunk)), then all weight loads of the job, so both are in
+    // flight together
     const int ntask = T * nblk * 16;
     uint4 xr[QI][XW];
 #pragma unroll
     for (int i = 0; i < QI; i++) {
+        if (!newk) break;
         const int j = tid + 256 * i;
         if (j < ntask) {
             const int ch = j & 15, bt = j >> 4;
@@ -651,9 +678,6 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
     }
 
     // all weight loads of the job: row (rg, wave, tile, xn), block b0 + b, segment g
-    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
-    const __amdgpu_buffer_rsrc_t wrsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
     const int row0 = rg * kWideRows + wave * 32 + xn;
     const uint32_t voff = (uint32_t)row0 * row_bytes + (uint32_t)b0 * kBlockBytes + (uint32_t)gemv_seg_byte0(g);
     uint32_t wl[KC][2], wh[KC][2];
@@ -667,17 +691,12 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
             wh[b][tl] = w.y;
         }
 
-    // (2) trit table, cleared image and scales
-#pragma unroll
-    for (int i = 0; i < lut_bytes(kWideLR) / 16 / 256; i++) {
-        const int o = tid + i * 256;
-        const uint32_t bv = (uint32_t)o / (REPS / 4);
-        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
-                       m4 = (m3 * 3u) & 0xffu;
-        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
-                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
-        lut[o] = make_uint4(e, e, e, e);
-    }
+    if (newk) {
+    // (2) a new chunk: after every wave is done with the previous image, clear it and the
+    // scales, then (3) quantise into it.  LDS-only barriers: the weight loads stay in flight
+    // (a fence would wait for them)
+    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
     for (int o = tid; o < KC * kWideBlkBytes / 16; o += 256) ((uint4*)img)[o] = make_uint4(0, 0, 0, 0);
     if (tid < KC * 4) (&scl[0][0])[tid] = make_float2(0.0f, 0.0f);
     // LDS-only barrier: the weight loads stay in flight (a fence would wait for them)
@@ -728,9 +747,10 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
             ib[off + 16] = (uint8_t)q;
         }
     }
-    // LDS-only barrier: the weight loads stay in flight (a fence would wait for them)
     __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
+    kc_cur = kc;
+    }
 
     // (4) tiles: per block the A operand once, then the wave's two tiles
     const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
@@ -775,17 +795,18 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
                 if (t0 + 1 < T) y[(size_t)(t0 + 1) * ldy + row] = acc[tl][1];
             }
         }
-        return;
-    }
-    float* wp = ws + (size_t)kc * T * N;
+    } else {
+        float* wp = ws + (size_t)kc * T * N;
 #pragma unroll
-    for (int tl = 0; tl < 2; tl++) {
-        const int row = row0 + 16 * tl;
-        if (row < N) {
-            if (t0 < T) wp[(size_t)t0 * N + row] = acc[tl][0];
-            if (t0 + 1 < T) wp[(size_t)(t0 + 1) * N + row] = acc[tl][1];
+        for (int tl = 0; tl < 2; tl++) {
+            const int row = row0 + 16 * tl;
+            if (row < N) {
+                if (t0 < T) wp[(size_t)t0 * N + row] = acc[tl][0];
+                if (t0 + 1 < T) wp[(size_t)(t0 + 1) * N + row] = acc[tl][1];
+            }
         }
     }
+    }   // job loop
 }
 
 // y[t][row] = sum of the K chunks' partial sums in chunk order (deterministic)
@@ -973,12 +994,14 @@ hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float*
             rows = (int)std::min<size_t>((size_t)rows, fit);
         }
         const int groups = (rows + kWideRows - 1) / kWideRows;
+        // persistent workgroups, at most 3 per CU, each on a contiguous range of the jobs
+        const int grid = std::min(groups * nsplit, 3 * n_cu);
         if (x_dtype == 1)
-            hipLaunchKernelGGL((k_gemv_wide<kWideKC, true>), dim3(groups * nsplit), dim3(256), 0, s,
-                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit);
+            hipLaunchKernelGGL((k_gemv_wide<kWideKC, true>), dim3(grid), dim3(256), 0, s,
+                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit, groups);
         else
-            hipLaunchKernelGGL((k_gemv_wide<kWideKC, false>), dim3(groups * nsplit), dim3(256), 0, s,
-                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit);
+            hipLaunchKernelGGL((k_gemv_wide<kWideKC, false>), dim3(grid), dim3(256), 0, s,
+                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit, groups);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (nsplit > 1) {
             hipLaunchKernelGGL(k_gemv_wide_sum, dim3((T * rows + 255) / 256), dim3(256), 0, s, ws, y + n0, rows, N, T,
