@@ -980,11 +980,12 @@ hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float*
     for (int n0 = 0; n0 < N;) {
         int rows = std::min(N - n0, max_rows);
         const int groups_all = (rows + kWideRows - 1) / kWideRows;
-        // one round of jobs on 3 workgroups per CU when the rows allow it, else the fewest
-        // K chunks (several rounds)
+        // up to one job per workgroup slot (3 per CU) when the rows allow it, chunks of at
+        // least 6 blocks (smaller jobs cost more in per-job setup than they gain in spread),
+        // else the fewest K chunks
         const int slots = 3 * n_cu;
         int nsplit = (nb + kWideKC - 1) / kWideKC;
-        if ((long long)groups_all * nsplit < slots) nsplit = std::max(nsplit, std::min(nb, slots / groups_all));
+        if ((long long)groups_all * nsplit < slots) nsplit = std::max(nsplit, std::min(std::max(1, nb / 6), slots / groups_all));
         const int kcb = (nb + nsplit - 1) / nsplit;
         nsplit = (nb + kcb - 1) / kcb;
         if (nsplit > 1) {
