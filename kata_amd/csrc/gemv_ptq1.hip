@@ -662,9 +662,8 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
     uint4 xr[QI][XW];
 #pragma unroll
     for (int i = 0; i < QI; i++) {
-        if (!newk) break;
         const int j = tid + 256 * i;
-        if (j < ntask) {
+        if (newk && j < ntask) {
             const int ch = j & 15, bt = j >> 4;
             const int t = bt / nblk, b = bt - t * nblk;
             const size_t k0 = (size_t)t * K + (b0 + b) * 128 + ch * 8;
@@ -709,42 +708,43 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
 #pragma unroll
     for (int i = 0; i < QI; i++) {
         const int j = tid + 256 * i;
-        if (j >= ntask) break;                    // whole 16-lane rows drop out together
-        const int ch = j & 15, bt = j >> 4;
-        const int t = bt / nblk, b = bt - t * nblk;
-        float v[8];
-        if constexpr (XF16) {
-            const uint32_t w4[4] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w};
+        if (j < ntask) {                          // whole 16-lane rows drop out together
+            const int ch = j & 15, bt = j >> 4;
+            const int t = bt / nblk, b = bt - t * nblk;
+            float v[8];
+            if constexpr (XF16) {
+                const uint32_t w4[4] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w};
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const v2h h = __builtin_bit_cast(v2h, w4[q]);
-                v[2 * q] = (float)h[0];
-                v[2 * q + 1] = (float)h[1];
+                for (int q = 0; q < 4; q++) {
+                    const v2h h = __builtin_bit_cast(v2h, w4[q]);
+                    v[2 * q] = (float)h[0];
+                    v[2 * q + 1] = (float)h[1];
+                }
+            } else {
+                const uint4 a = xr[i][0], c = xr[i][XW - 1];
+                v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
+                v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
+                v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
             }
-        } else {
-            const uint4 a = xr[i][0], c = xr[i][XW - 1];
-            v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
-            v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
-            v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
-        }
-        float a = 0.0f;
+            float a = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(v[e]));
-        a = row16_max(a);
-        const float inv = a > 0.0f ? kQMax / a : 0.0f;
-        if (ch == 0) {
-            float* sp = &scl[b][t >> 1].x;
-            sp[t & 1] = a * (1.0f / kQMax);
-        }
-        const uint4 ow4 = *(const uint4*)&kWideOff.v[8 * ch];
-        const uint32_t ow[4] = {ow4.x, ow4.y, ow4.z, ow4.w};
-        uint8_t* ib = img + b * kWideBlkBytes + 32 * t;
+            for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(v[e]));
+            a = row16_max(a);
+            const float inv = a > 0.0f ? kQMax / a : 0.0f;
+            if (ch == 0) {
+                float* sp = &scl[b][t >> 1].x;
+                sp[t & 1] = a * (1.0f / kQMax);
+            }
+            const uint4 ow4 = *(const uint4*)&kWideOff.v[8 * ch];
+            const uint32_t ow[4] = {ow4.x, ow4.y, ow4.z, ow4.w};
+            uint8_t* ib = img + b * kWideBlkBytes + 32 * t;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int off = (int)((ow[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-            const int q = (int)rintf(v[e] * inv);
-            ib[off] = (uint8_t)((q + 128) >> 8);
-            ib[off + 16] = (uint8_t)q;
+            for (int e = 0; e < 8; e++) {
+                const int off = (int)((ow[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+                const int q = (int)rintf(v[e] * inv);
+                ib[off] = (uint8_t)((q + 128) >> 8);
+                ib[off + 16] = (uint8_t)q;
+            }
         }
     }
     __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
@@ -759,28 +759,29 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
     float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
 #pragma unroll
     for (int b = 0; b < KC; b++) {
-        if (b >= nblk) break;
-        v4i A[kMfmaPerBlock];
+        if (b < nblk) {
+            v4i A[kMfmaPerBlock];
 #pragma unroll
-        for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(xa + b * kWideBlkBytes + m * kWideM);
-        const float2 s = scl[b][g];
+            for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(xa + b * kWideBlkBytes + m * kWideM);
+            const float2 s = scl[b][g];
 #pragma unroll
-        for (int tl = 0; tl < 2; tl++) {
-            const uint32_t w0 = wl[b][tl], w1 = wh[b][tl];
-            v4i B[kMfmaPerBlock];
-            B[0] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 1, laneoff)),
-                       (int)lds_u32(lb, lut_addr<kWideLR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 3, laneoff))};
-            B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 0, laneoff)),
-                       (int)lds_u32(lb, lut_addr<kWideLR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 2, laneoff))};
-            B[2] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
-            v4i D = {0, 0, 0, 0};
+            for (int tl = 0; tl < 2; tl++) {
+                const uint32_t w0 = wl[b][tl], w1 = wh[b][tl];
+                v4i B[kMfmaPerBlock];
+                B[0] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 1, laneoff)),
+                           (int)lds_u32(lb, lut_addr<kWideLR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 3, laneoff))};
+                B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 0, laneoff)),
+                           (int)lds_u32(lb, lut_addr<kWideLR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 2, laneoff))};
+                B[2] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
+                v4i D = {0, 0, 0, 0};
 #pragma unroll
-            for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], D, 0, 0, 0);
-            // the row's scale sits in bytes 26..27, read by lane group 0
-            const uint32_t dbits = (uint32_t)__builtin_amdgcn_ds_bpermute(xn * 4, (int)w1) >> 16;
-            const float d = half_bits_to_float(dbits);
-            acc[tl][0] += (float)(D[0] * 256 + D[1]) * (d * s.x);
-            acc[tl][1] += (float)(D[2] * 256 + D[3]) * (d * s.y);
+                for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], D, 0, 0, 0);
+                // the row's scale sits in bytes 26..27, read by lane group 0
+                const uint32_t dbits = (uint32_t)__builtin_amdgcn_ds_bpermute(xn * 4, (int)w1) >> 16;
+                const float d = half_bits_to_float(dbits);
+                acc[tl][0] += (float)(D[0] * 256 + D[1]) * (d * s.x);
+                acc[tl][1] += (float)(D[2] * 256 + D[3]) * (d * s.y);
+            }
         }
     }
 
