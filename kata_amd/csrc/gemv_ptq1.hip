@@ -914,7 +914,8 @@ static int gemv_split(GemvMats& P, int wgs) {
 
 // Configuration choice, first that fits 160 KB of LDS: about one workgroup per CU, else
 // smaller tile ranges (more workgroups); the staged activation (XS) before per-thread
-// loads; a 64-replica trit table (one v_perm per lookup) before a 16-replica one.
+// loads, except for K > 8192 (measured: 0.7 us faster at K = 17408, slower at 5120); a
+// 64-replica trit table (one v_perm per lookup) before a 16-replica one.
 template <int T>
 static hipError_t launch_gemv_t(GemvMats& P, const void* x, int x_dtype, int x_layout, int K, hipStream_t s) {
     const int cus = device_cus();
@@ -923,6 +924,9 @@ static hipError_t launch_gemv_t(GemvMats& P, const void* x, int x_dtype, int x_l
     for (int wgs = cus;; wgs *= 2) {
         const int tpw = gemv_split(P, wgs);
         int lds;
+        // long activations (K > 8192): per-thread loads start sooner than one wave's copy
+        if (K > 8192 && regs_ok && (lds = gemv_lds_bytes(K, T, 6, tpw, 0)) <= kLdsMax)
+            return launch_gemv_pad<T, 6, false>(P, x, x_dtype, x_layout, K, lds, s);
         if ((lds = gemv_lds_bytes(K, T, 6, tpw, xbytes)) <= kLdsMax)
             return launch_gemv_pad<T, 6, true>(P, x, x_dtype, x_layout, K, lds, s);
         if ((lds = gemv_lds_bytes(K, T, 4, tpw, xbytes)) <= kLdsMax)
