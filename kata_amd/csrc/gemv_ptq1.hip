@@ -17,7 +17,9 @@
 //    core sums trit*limb exactly in int32, so sum(trit*q) = 256*D_hi + D_lo per block and
 //    token, and y += d * s * that in fp32.  The only approximation is the 16-bit
 //    block-fixed-point activation (|x - s*q| <= amax/65278), far inside the 1e-3
-//    relative-L2 contract.
+//    relative-L2 contract.  A block holding a NaN or an infinity gets s = NaN, so every
+//    output row is NaN, as the reference's coefficient-form sum gives (its block `sumy` is
+//    then non-finite, shaders/gemv_fast.metal:21-45).
 //  * Work item = 4 consecutive blocks of a 4-row tile.  The 16 B columns of the MFMA are
 //    (row r, block 4c + kq) and the 16 A rows are (block 4c + kq, token, limb), so one item
 //    decodes four 112-byte runs of the matrix and the products of mismatched blocks are
@@ -291,6 +293,7 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
 template <int T, int LR, int D, bool PAD, bool XS, bool MULTI>
 __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __restrict__ x, int x_dtype, int x_layout,
                                                     int K, int nq) {
+#pragma clang fp contract(off)
     static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by item parity");
     constexpr int ASTRIDE = 4 * 2 * T * 16;      // A image bytes per (virtual block, MFMA)
     constexpr int BLK = kMfmaPerBlock * ASTRIDE;  // A image bytes per virtual block
@@ -446,11 +449,19 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 float a = 0.0f;
+                bool bad = false;
 #pragma unroll
-                for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(vv[t][e]));
-                a = row16_max(a);
-                const float inv = a > 0.0f ? kQMax / a : 0.0f;
-                if ((j & 15) == 0) ((int2*)Ss)[b * T + t] = make_int2(__builtin_bit_cast(int, a * (1.0f / kQMax)), 0);
+                for (int e = 0; e < 8; e++) {
+                    const float av = fabsf(vv[t][e]);
+                    bad |= !(av <= 3.402823466e38f);   // NaN or infinity
+                    a = fmaxf(a, av);
+                }
+                a = row16_max(bad ? __builtin_inff() : a);
+                // a block holding a non-finite value gets scale NaN: every output row is NaN
+                const bool blk_bad = !(a <= 3.402823466e38f);
+                const float inv = (a > 0.0f && !blk_bad) ? kQMax / a : 0.0f;
+                const float sc = blk_bad ? __builtin_nanf("") : a * (1.0f / kQMax);
+                if ((j & 15) == 0) ((int2*)Ss)[b * T + t] = make_int2(__builtin_bit_cast(int, sc), 0);
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int q = (int)rintf(vv[t][e] * inv);
@@ -529,11 +540,13 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         float* dst = (float*)(pcur + (u >> 1) * T * 64);
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const float val = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]) * (d * sc[u & 1][t]);
+            // explicit fma, contraction off (below): every instantiation (one matrix or a
+            // batch) rounds alike, so a batched launch equals the per-matrix launches bit for bit
+            const float fi = (float)(Dm[2 * t] * 256 + Dm[2 * t + 1]), fs = d * sc[u & 1][t];
             if (u & 1)
-                dst[16 * t] = vprev[t] + val;
+                dst[16 * t] = __builtin_fmaf(fi, fs, vprev[t]);
             else
-                vprev[t] = val;
+                vprev[t] = fi * fs;
         }
         if ((u & 1) && ++ct == Tt) {
             ct = 0;
@@ -731,13 +744,19 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
                 v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
             }
             float a = 0.0f;
+            bool bad = false;
 #pragma unroll
-            for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(v[e]));
-            a = row16_max(a);
-            const float inv = a > 0.0f ? kQMax / a : 0.0f;
+            for (int e = 0; e < 8; e++) {
+                const float av = fabsf(v[e]);
+                bad |= !(av <= 3.402823466e38f);   // NaN or infinity
+                a = fmaxf(a, av);
+            }
+            a = row16_max(bad ? __builtin_inff() : a);
+            const bool blk_bad = !(a <= 3.402823466e38f);
+            const float inv = (a > 0.0f && !blk_bad) ? kQMax / a : 0.0f;
             if (ch == 0) {
                 float* sp = &scl[b][t >> 1].x;
-                sp[t & 1] = a * (1.0f / kQMax);
+                sp[t & 1] = blk_bad ? __builtin_nanf("") : a * (1.0f / kQMax);
             }
             const uint4 ow4 = *(const uint4*)&kWideOff.v[8 * ch];
             const uint32_t ow[4] = {ow4.x, ow4.y, ow4.z, ow4.w};
