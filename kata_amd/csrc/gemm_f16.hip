@@ -30,6 +30,8 @@
 //    row tiles, and with them the A rows in that XCD's L2.
 #include "common.h"
 #include "launch.h"
+
+#include <mutex>
 #include "gemm_sched.h"
 
 #include <algorithm>
@@ -317,10 +319,13 @@ hipError_t gemm_device(bool need_ws, int* n_cu, float** ws) {
         float* ws = nullptr;
     };
     static Dev tab[64];
+    static std::mutex mu;            // first-time set-up from several host threads
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    Dev& D = tab[dev & 63];
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    Dev& D = tab[dev];
     if (!D.n_cu) {
         int n = 0;
         e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
