@@ -76,6 +76,18 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
 int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                         void* stream);
 
+/* The same wide verification GEMV, allocating nothing: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as kata_gemv_ptq1_wide (bit
+ * for bit); the K-chunk partial sums go to a fixed per-device array of
+ * kata_gemv_ptq1_wide_noalloc_scratch_bytes() bytes (4 MiB) held by each device the library
+ * runs on until the process ends, instead of the workspace.  Rejects (KATA_EINVAL) a K and T
+ * whose partial sums for one 128-row group would not fit it (K beyond ~786000 at T = 8).
+ * Calls that overlap in time on one device share the array and race. */
+int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                                void* stream);
+size_t kata_gemv_ptq1_wide_noalloc_scratch_bytes(void);
+
 /* Q8_0 GEMV for the MTP head: y[t][n] = sum_b d[n,b] * sum_i q[n,b,i] * x[t][32b+i].
  * K % 32 == 0, T in {1,2}, x [T][K] fp32 or fp16 (16-byte aligned), y [T][N] fp32.
  * W is 2-byte aligned (the block layout's granularity).

@@ -60,6 +60,8 @@ SIGNATURES = {
     "kata_gguf_upload_into": (I, [P, P, U64]),
     "kata_gguf_free_device": (I, [P]),
     "kata_gemv_ptq1_wide": (I, [P, P, I, P, I, I, I, P]),
+    "kata_gemv_ptq1_wide_noalloc": (I, [P, P, I, P, I, I, I, P]),
+    "kata_gemv_ptq1_wide_noalloc_scratch_bytes": (SZ, []),
     "kata_dispatch_create": (P, [P]),
     "kata_dispatch_destroy": (None, [P]),
     "kata_dispatch_set_i8": (I, [P, ctypes.c_char_p]),

@@ -100,6 +100,28 @@ int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, 
     return check_launch(kata::launch_gemv_wide(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv ptq1 wide");
 }
 
+int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                                void* stream) {
+    if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
+    if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
+    if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
+    // T <= 2: the decode GEMV, which uses no scratch at all
+    if (T <= 2 && K <= kata::gemv_max_k(T))
+        return check_launch(kata::launch_gemv_ptq1(W, x, x_dtype, KATA_X_ROWS, y, K, N, T, (hipStream_t)stream),
+                            "gemv ptq1 wide no-alloc (T <= 2)");
+    if (!kata::gemv_wide_noalloc_fits(K, T))
+        return fail(KATA_EINVAL, "K=%d, T=%d needs more than the %zu-byte no-allocation scratch", K, T,
+                    kata::gemv_wide_noalloc_scratch_bytes());
+    return check_launch(kata::launch_gemv_wide_noalloc(W, x, x_dtype, y, K, N, T, (hipStream_t)stream),
+                        "gemv ptq1 wide no-alloc");
+}
+
+size_t kata_gemv_ptq1_wide_noalloc_scratch_bytes(void) { return kata::gemv_wide_noalloc_scratch_bytes(); }
+
 // ------------------------------------------------------------------ Q8_0 GEMV
 int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, void* stream) {
     if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");

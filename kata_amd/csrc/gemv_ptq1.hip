@@ -30,6 +30,7 @@
 #include "launch.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace kata {
@@ -989,35 +990,42 @@ hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_
 
 hipError_t gemm_device(bool need_ws, int* n_cu, float** ws);
 
-// Wide GEMV launch: row groups of 128 rows x K chunks of at most kWideKC blocks; more
+// Wide GEMV launches: row groups of 128 rows x K chunks of at most kWideKC blocks; more
 // chunks than needed until there are about two jobs per CU.  With several chunks the
-// partial sums use the GEMM's per-device workspace (n_cu x 128 KB); rows beyond what it
-// holds go to further launches.
+// partial sums go to the workspace `ws` (ws_floats floats; get_ws() supplies it the first
+// time it is needed); rows beyond what it holds go to further launches.
 constexpr int kWideKC = 11;   // 3 workgroups per CU: LDS 16 KB table + 11 x 3 KB image
-hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
-                            hipStream_t s) {
-    int n_cu = 0;
-    float* ws = nullptr;
-    hipError_t e = gemm_device(false, &n_cu, &ws);
-    if (e != hipSuccess) return e;
+
+// K chunks of a launch over `rows` rows
+static int wide_nsplit(int nb, int rows, int n_cu) {
+    const int groups_all = (rows + kWideRows - 1) / kWideRows;
+    // up to one job per workgroup slot (3 per CU) when the rows allow it, chunks of at least
+    // 6 blocks (smaller jobs cost more in per-job setup than they gain in spread), else the
+    // fewest K chunks
+    const int slots = 3 * n_cu;
+    int nsplit = (nb + kWideKC - 1) / kWideKC;
+    if ((long long)groups_all * nsplit < slots) nsplit = std::max(nsplit, std::min(std::max(1, nb / 6), slots / groups_all));
+    const int kcb = (nb + nsplit - 1) / nsplit;
+    return (nb + kcb - 1) / kcb;
+}
+
+template <typename GetWs>
+static hipError_t wide_launches(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, int n_cu,
+                                GetWs get_ws, size_t ws_floats, hipStream_t s) {
     const int nb = K / kGroup;
     const size_t row_bytes = (size_t)nb * kBlockBytes;
-    const size_t ws_floats = (size_t)n_cu * 256 * 128;
     // rows per launch: 32-bit buffer offsets
     const int max_rows = (int)((((size_t)1 << 31) / row_bytes) / kWideRows * kWideRows);
+    hipError_t e;
+    // one K chunking for the whole call: the result does not depend on how many launches
+    // the workspace size cuts the rows into
+    const int nsplit = wide_nsplit(nb, std::min(N, max_rows), n_cu);
+    const int kcb = (nb + nsplit - 1) / nsplit;
     for (int n0 = 0; n0 < N;) {
         int rows = std::min(N - n0, max_rows);
-        const int groups_all = (rows + kWideRows - 1) / kWideRows;
-        // up to one job per workgroup slot (3 per CU) when the rows allow it, chunks of at
-        // least 6 blocks (smaller jobs cost more in per-job setup than they gain in spread),
-        // else the fewest K chunks
-        const int slots = 3 * n_cu;
-        int nsplit = (nb + kWideKC - 1) / kWideKC;
-        if ((long long)groups_all * nsplit < slots) nsplit = std::max(nsplit, std::min(std::max(1, nb / 6), slots / groups_all));
-        const int kcb = (nb + nsplit - 1) / nsplit;
-        nsplit = (nb + kcb - 1) / kcb;
+        float* ws = nullptr;
         if (nsplit > 1) {
-            if ((e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
+            if ((e = get_ws(&ws)) != hipSuccess) return e;
             const size_t fit = ws_floats / ((size_t)nsplit * T) / kWideRows * kWideRows;
             if (fit == 0) return hipErrorInvalidValue;
             rows = (int)std::min<size_t>((size_t)rows, fit);
@@ -1040,6 +1048,65 @@ hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float*
         n0 += rows;
     }
     return hipSuccess;
+}
+
+// The library-owned per-device workspace of the prefill GEMM (allocated on first use).
+hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                            hipStream_t s) {
+    int n_cu = 0;
+    float* ws = nullptr;
+    hipError_t e = gemm_device(false, &n_cu, &ws);
+    if (e != hipSuccess) return e;
+    auto get_ws = [&](float** p) {
+        int n = 0;
+        return gemm_device(true, &n, p);
+    };
+    return wide_launches(W, x, x_dtype, y, K, N, T, n_cu, get_ws, (size_t)n_cu * 256 * 128, s);
+}
+
+// ---- the no-allocation form: partial sums in a fixed device array.  `scratch` is a
+// host-side stand-in for the array, never a device address: the address each device holds
+// its copy at comes from hipGetSymbolAddress once per device (with that device current) and
+// only that address is handed to kernels.  Calls that overlap on one device share the array
+// and race; nothing needs clearing (every partial sum is written before it is read).
+constexpr size_t kNoAllocFloats = (size_t)1 << 20;   // 4 MiB per device
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+static hipError_t noalloc_scratch(float** p) {
+    static std::mutex mu;
+    static float* addr[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* a = nullptr;
+        if ((e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        addr[dev] = (float*)a;
+    }
+    *p = addr[dev];
+    return hipSuccess;
+}
+
+size_t gemv_wide_noalloc_scratch_bytes() { return kNoAllocFloats * sizeof(float); }
+
+// true if one row group of a K x (any N) problem with T tokens fits the scratch
+bool gemv_wide_noalloc_fits(int K, int T) {
+    const int nsplit = wide_nsplit(K / kGroup, kWideRows, device_cus());
+    return nsplit == 1 || (size_t)nsplit * T * kWideRows <= kNoAllocFloats;
+}
+
+hipError_t launch_gemv_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                                    hipStream_t s) {
+    float* ws = nullptr;
+    hipError_t e = noalloc_scratch(&ws);
+    if (e != hipSuccess) return e;
+    auto get_ws = [&](float** p) {
+        *p = ws;
+        return hipSuccess;
+    };
+    return wide_launches(W, x, x_dtype, y, K, N, T, device_cus(), get_ws, kNoAllocFloats, s);
 }
 
 int gemv_max_mats() { return kMaxMats; }

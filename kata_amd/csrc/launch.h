@@ -17,6 +17,11 @@ int gemv_max_mats();     // most matrices one launch takes
 // wide verification GEMV, T in 1..8 token rows x [T][K] (fp16 or fp32), y [T][N]
 hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                             hipStream_t s);
+// the same with its partial sums in a fixed per-device device array (no allocation)
+hipError_t launch_gemv_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
+                                    hipStream_t s);
+bool gemv_wide_noalloc_fits(int K, int T);
+size_t gemv_wide_noalloc_scratch_bytes();
 
 // ---- Q8_0 GEMV (gemv_q8.hip)
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
