@@ -103,7 +103,10 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
  * K % 128 == 0; any M >= 1, N >= 1.
  * The K-pieces of the last round of tiles use a per-device workspace (at most one fp32
  * 256x128 tile per CU), allocated on the device's first call that needs it and kept: calls
- * on one device must not overlap in time, and that first call must not be captured.
+ * on one device must not overlap in time, and that first call must not be captured.  The
+ * one workspace is shared by every entry point that uses it: kata_gemm_ptq1_f16,
+ * kata_gemm_ptq1_i8, kata_gemv_ptq1_wide and the dispatcher's prefill and verification
+ * calls (kata_dispatch_prefill, kata_dispatch_ffn_prefill, kata_dispatch_ffn_verify). 
  * Replaces Engine::dExpandGemm's fp16 path (src/engine.cpp:208-219: k_expand_ptq1_v2 into
  * a 178 MB stage, then Engine::dGemm / k_gemm_f16, shaders/prefill.metal:31-41). */
 int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
@@ -144,7 +147,11 @@ int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, v
  * k_add_rms_fwht_t (shaders/prefill.metal:59-78,266-285). */
 int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out, int out_dtype, int out_layout,
                       float* xnew, const float* gamma, void* hout, int hout_dtype, int W, int M, void* stream);
-/* The other input transforms, same out formats: mode 0 RMSNorm of src (as above, no
+/* Outputs (out, xnew, hout) must not overlap each other or any input (x, y, gs, gamma):
+ * KATA_EINVAL otherwise; an in-place residual update needs a second buffer, as the
+ * reference alternates two (src/engine.cpp:136-146). */
+
+/* The other input transforms, same out formats (out must not overlap src, src2 or gs): mode 0 RMSNorm of src (as above, no
  * residual), 1 SwiGLU v = silu(src) * src2, 2 src in the grouped GDN head order
  * (v[128 t + h] = src[h + 128 (t/3 + 16 (t%3))], W == 6144), 3 v = src; out = H(v * gs).
  * Replaces k_rms_fwht (shaders/ops.metal:30-54) and k_rms_fwht_b (shaders/prefill.metal:81-97). */
@@ -169,8 +176,10 @@ int kata_pack_ptq1_0(const int8_t* trits, const uint16_t* scales, uint8_t* out, 
 /* ---------------------------------------------------------------- GGUF model file ----
  * HOST: a GGUF v3 file memory-mapped read-only and indexed (src/gguf.cpp:41-71,
  * src/gguf.h): tensor infos (name, ggml type — 143 PTQ1_0, 8 Q8_0, 0 F32 …, dims with
- * dims[0] the row length, byte offset in the data region, byte size; 0 for a type not
- * known here) and integer / string metadata.  kata_gguf_upload copies the whole data region
+ * dims[0] the row length, byte offset in the data region, byte size) and integer / string
+ * metadata.  A file with a tensor of a ggml type not supported here (the reference exits on
+ * one, src/gguf.cpp:25-37), an element count that is not whole blocks or overflows, or any
+ * tensor outside the data region is rejected (NULL).  kata_gguf_upload copies the whole data region
  * to one device allocation: a matrix is then dev_base + offset, the weight base that
  * kata_dispatch_create takes and the byte offsets its calls take (src/engine.cpp:27-37).
  * NULL / negative returns set kata_last_error(). */

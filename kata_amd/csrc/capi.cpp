@@ -27,6 +27,17 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+// a byte range [p, p + n); null pointers overlap nothing
+struct Span {
+    const void* p;
+    size_t n;
+};
+bool overlap(const Span& a, const Span& b) {
+    if (!a.p || !b.p || !a.n || !b.n) return false;
+    const uintptr_t a0 = (uintptr_t)a.p, b0 = (uintptr_t)b.p;
+    return a0 < b0 + b.n && b0 < a0 + a.n;
+}
+
 int check_launch(hipError_t e, const char* what) {
     if (e != hipSuccess) return fail(KATA_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
     g_err.clear();
@@ -202,6 +213,20 @@ int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out
                       float* xnew, const float* gamma, void* hout, int hout_dtype, int W, int M, void* stream) {
     if (!x || !gs || !out) return fail(KATA_EINVAL, "null pointer argument");
     if (int rc = check_fwht_out(out, out_dtype, out_layout, W, M)) return rc;
+    // no output may overlap an input: a workgroup re-reads its whole row while others write
+    // theirs (the reference alternates two residual buffers, src/engine.cpp:136-146)
+    {
+        const size_t rows = (size_t)W * M * sizeof(float);
+        const size_t ob = (size_t)W * M * (out_dtype == KATA_F16 ? 2 : 4);
+        const size_t hb = (size_t)W * M * (hout_dtype == KATA_F16 ? 2 : 4);
+        const Span ins[] = {{x, rows}, {y, rows}, {gs, (size_t)W * 4}, {gamma, (size_t)W * 4}};
+        const Span outs[] = {{out, ob}, {xnew, rows}, {hout, hb}};
+        for (const Span& o : outs)
+            for (const Span& i : ins)
+                if (overlap(o, i)) return fail(KATA_EINVAL, "an output (out, xnew or hout) overlaps an input (x, y, gs or gamma)");
+        if (overlap(outs[0], outs[1]) || overlap(outs[0], outs[2]) || overlap(outs[1], outs[2]))
+            return fail(KATA_EINVAL, "the outputs out, xnew and hout overlap");
+    }
     if ((gamma == nullptr) != (hout == nullptr)) return fail(KATA_EINVAL, "gamma and hout go together");
     if (hout && hout_dtype != KATA_F32 && hout_dtype != KATA_F16) return fail(KATA_EINVAL, "hout_dtype=%d", hout_dtype);
     if (!aligned(x, 16) || (y && !aligned(y, 16)) || !aligned(gs, 16) || (xnew && !aligned(xnew, 16)) ||
@@ -220,6 +245,12 @@ int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* ou
     if (mode == 1 && !src2) return fail(KATA_EINVAL, "mode 1 needs src2");
     if (mode == 2 && W != 6144) return fail(KATA_EINVAL, "mode 2 (GDN head order) needs W == 6144");
     if (int rc = check_fwht_out(out, out_dtype, out_layout, W, M)) return rc;
+    {
+        const size_t rows = (size_t)W * M * sizeof(float);
+        const Span o{out, (size_t)W * M * (out_dtype == KATA_F16 ? 2 : 4)};
+        if (overlap(o, {src, rows}) || overlap(o, {mode == 1 ? src2 : nullptr, rows}) || overlap(o, {gs, (size_t)W * 4}))
+            return fail(KATA_EINVAL, "out overlaps an input (src, src2 or gs)");
+    }
     if (!aligned(src, 16) || (src2 && !aligned(src2, 16)) || !aligned(gs, 16))
         return fail(KATA_EINVAL, "vectors must be 16-byte aligned");
     return check_launch(kata::launch_norm_fwht(src, mode == 1 ? src2 : nullptr, gs, out, out_dtype, out_layout, nullptr,

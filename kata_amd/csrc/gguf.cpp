@@ -16,6 +16,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cstdint>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -42,20 +43,21 @@ struct kata_gguf {
 
 namespace {
 
-// bytes of n elements of a ggml type, 0 when the type is not known here
-uint64_t tensor_bytes(uint32_t type, uint64_t n) {
+// Block geometry of a ggml type: elements and bytes per block; false for a type not known
+// here (the reference exits on one, src/gguf.cpp:25-37).
+bool type_block(uint32_t type, uint64_t& elems, uint64_t& bytes) {
     switch (type) {
-        case 0: return n * 4;                    // F32
-        case 1: return n * 2;                    // F16
-        case 30: return n * 2;                   // BF16
-        case 8: return n / 32 * 34;              // Q8_0
-        case 143: return n / 128 * 28;           // PTQ1_0
-        case 142: return n / 128 * 34;           // PQ2_0
-        case 10: return n / 256 * 84;            // Q2_K
-        case 11: return n / 256 * 110;           // Q3_K
-        case 12: return n / 256 * 144;           // Q4_K
-        case 14: return n / 256 * 210;           // Q6_K
-        default: return 0;
+        case 0: elems = 1; bytes = 4; return true;        // F32
+        case 1: elems = 1; bytes = 2; return true;        // F16
+        case 30: elems = 1; bytes = 2; return true;       // BF16
+        case 8: elems = 32; bytes = 34; return true;      // Q8_0
+        case 143: elems = 128; bytes = 28; return true;   // PTQ1_0
+        case 142: elems = 128; bytes = 34; return true;   // PQ2_0
+        case 10: elems = 256; bytes = 84; return true;    // Q2_K
+        case 11: elems = 256; bytes = 110; return true;   // Q3_K
+        case 12: elems = 256; bytes = 144; return true;   // Q4_K
+        case 14: elems = 256; bytes = 210; return true;   // Q6_K
+        default: return false;
     }
 }
 
@@ -160,29 +162,44 @@ kata_gguf* kata_gguf_open(const char* path) {
             r.ok = false;
         }
     }
-    for (uint64_t i = 0; i < nt && r.ok; i++) {
+    const char* why = nullptr;
+    for (uint64_t i = 0; i < nt && r.ok && !why; i++) {
         kata_gguf::Tensor t;
         t.name = r.str();
         t.ndims = r.rd<uint32_t>();
         if (t.ndims > 4) r.ok = false;
         uint64_t ne = 1;
-        for (uint32_t d = 0; d < t.ndims && r.ok; d++) ne *= (t.dims[d] = r.rd<uint64_t>());
+        for (uint32_t d = 0; d < t.ndims && r.ok; d++) {
+            t.dims[d] = r.rd<uint64_t>();
+            if (t.dims[d] != 0 && ne > UINT64_MAX / t.dims[d]) why = "a tensor's element count overflows";
+            else ne *= t.dims[d];
+        }
         t.type = r.rd<uint32_t>();
         t.offset = r.rd<uint64_t>();
-        t.nbytes = tensor_bytes(t.type, ne);
+        uint64_t be = 0, bb = 0;
+        if (!r.ok || why) break;
+        if (!type_block(t.type, be, bb)) why = "a tensor has a ggml type not supported here";
+        else if (ne % be != 0) why = "a tensor's element count is not a whole number of blocks";
+        else if (ne / be > UINT64_MAX / bb) why = "a tensor's byte size overflows";
+        else t.nbytes = ne / be * bb;
         g->by_name[t.name] = g->tensors.size();
         g->tensors.push_back(t);
     }
-    if (!r.ok || alignment == 0 || (alignment & (alignment - 1))) {
-        kata_gguf_close(g);
-        return kata_internal_fail(KATA_EINVAL, "truncated or malformed GGUF header"), nullptr;
+    if (!why && (!r.ok || alignment == 0 || (alignment & (alignment - 1)) || alignment > ((uint64_t)1 << 30)))
+        why = "truncated or malformed GGUF header";
+    if (!why) {
+        g->data_start = (r.p + alignment - 1) / alignment * alignment;
+        if (g->data_start > g->size) why = "the data region starts past the end of the file";
     }
-    g->data_start = (r.p + alignment - 1) / alignment * alignment;
-    for (const auto& t : g->tensors)
-        if (g->data_start + t.offset + t.nbytes > g->size) {
-            kata_gguf_close(g);
-            return kata_internal_fail(KATA_EINVAL, "a tensor lies past the end of the file"), nullptr;
-        }
+    for (size_t i = 0; i < g->tensors.size() && !why; i++) {
+        const auto& t = g->tensors[i];
+        const uint64_t room = g->size - g->data_start;   // no wrap-around: each term checked alone
+        if (t.offset > room || t.nbytes > room - t.offset) why = "a tensor lies past the end of the file";
+    }
+    if (why) {
+        kata_gguf_close(g);
+        return kata_internal_fail(KATA_EINVAL, why), nullptr;
+    }
     return g;
 }
 

@@ -31,6 +31,23 @@ def _need_gpu(*ts: torch.Tensor):
             raise ValueError("kata_amd ops take contiguous tensors")
 
 
+def _bytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+def _need_bytes(name: str, t: torch.Tensor | None, nbytes: int):
+    """The kernels read or write nbytes of t from its start: a shorter tensor would be an
+    out-of-bounds device access, so it is a ValueError here."""
+    if t is not None and _bytes(t) < nbytes:
+        raise ValueError(f"{name} holds {_bytes(t)} bytes, the call needs {nbytes}")
+
+
+def _ptq1_bytes(K: int, N: int) -> int:
+    if K <= 0 or K % GROUP or N <= 0:
+        raise ValueError(f"K={K} must be a positive multiple of {GROUP}, N={N} positive")
+    return N * (K // GROUP) * BLOCK_BYTES
+
+
 def _xdtype(x: torch.Tensor) -> int:
     if x.dtype == torch.float16:
         return KATA_F16
@@ -43,6 +60,9 @@ def _xdtype(x: torch.Tensor) -> int:
 def gemv_ptq1(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1, half2: bool = False,
               out: torch.Tensor | None = None) -> torch.Tensor:
     """y[T][N] fp32 = PTQ1_0 W (N x K) times x ([T][K], or [K][2] fp16 when half2)."""
+    _need_bytes("W", W, _ptq1_bytes(K, N))
+    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("out", out, T * N * 4)
     _need_gpu(W, x)
     y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
     check(lib().kata_gemv_ptq1(_ptr(W), _ptr(x), _xdtype(x), KATA_X_HALF2 if half2 else KATA_X_ROWS,
@@ -52,6 +72,12 @@ def gemv_ptq1(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1, half
 
 def gemv_ptq1_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, half2: bool = False, outs=None):
     """PTQ1_0 GEMVs of up to 4 matrices sharing the activation x, one launch: returns [y_i]."""
+    if len(Ws) != len(Ns) or (outs is not None and len(outs) != len(Ns)):
+        raise ValueError("Ws, Ns (and outs) must have the same length")
+    for i, (W, N) in enumerate(zip(Ws, Ns)):
+        _need_bytes(f"Ws[{i}]", W, _ptq1_bytes(K, N))
+        _need_bytes(f"outs[{i}]", outs[i] if outs is not None else None, T * N * 4)
+    _need_bytes("x", x, T * K * x.element_size())
     _need_gpu(x, *Ws)
     n = len(Ws)
     ys = outs if outs is not None else [torch.empty((T, N), dtype=torch.float32, device=x.device) for N in Ns]
@@ -65,8 +91,11 @@ def gemv_ptq1_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, half2: bool = F
 
 def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """Wide verification GEMV: y[T][N] fp32 for x [T][K] (fp16 or fp32), T = x.shape[0] in 1..8."""
-    _need_gpu(W, x)
     T = x.shape[0]
+    _need_bytes("W", W, _ptq1_bytes(K, N))
+    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("out", out, T * N * 4)
+    _need_gpu(W, x)
     y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
     check(lib().kata_gemv_ptq1_wide(_ptr(W), _ptr(x), _xdtype(x), _ptr(y), K, N, T, _stream(W)))
     return y
@@ -74,6 +103,11 @@ def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.
 
 def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
             out: torch.Tensor | None = None) -> torch.Tensor:
+    if K <= 0 or K % Q8_GROUP or N <= 0:
+        raise ValueError(f"K={K} must be a positive multiple of {Q8_GROUP}, N={N} positive")
+    _need_bytes("W", W, N * (K // Q8_GROUP) * Q8_BLOCK_BYTES)
+    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("out", out, T * N * 4)
     _need_gpu(W, x)
     y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
     check(lib().kata_gemv_q8_0(_ptr(W), _ptr(x), _xdtype(x), _ptr(y), K, N, T, _stream(W)))
@@ -83,10 +117,15 @@ def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
 # ----------------------------------------------------------------------------- prefill
 def gemm_ptq1_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=torch.float32,
                   out: torch.Tensor | None = None) -> torch.Tensor:
-    _need_gpu(A, W)
     if A.dtype != torch.float16:
         raise ValueError("A must be fp16")
+    if A.dim() != 2 or A.shape[1] < K:
+        raise ValueError(f"A must be [M][lda] with lda >= K={K}")
     M = A.shape[0]
+    _need_bytes("W", W, _ptq1_bytes(K, N))
+    if out is not None and (out.dim() != 2 or out.shape[0] < M or out.shape[1] < N):
+        raise ValueError(f"out must be [>= {M}][>= {N}]")
+    _need_gpu(A, W)
     C = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=A.device)
     cdt = KATA_F16 if C.dtype == torch.float16 else KATA_F32
     check(lib().kata_gemm_ptq1_f16(_ptr(A), A.shape[1], _ptr(W), _ptr(C), cdt, C.shape[1], M, K, N, _stream(A)))
@@ -95,9 +134,14 @@ def gemm_ptq1_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=to
 
 def quant_rows(X: torch.Tensor, ldS: int | None = None, out=None):
     """int8 rows and group scales of X; `out` = (Q, SX) to write into existing tensors."""
-    _need_gpu(X)
     M, K = X.shape
     ldS = M if ldS is None else ldS
+    if K % GROUP or ldS < M:
+        raise ValueError(f"K={K} must be a multiple of {GROUP} and ldS={ldS} >= M={M}")
+    if out is not None:
+        _need_bytes("Q", out[0], M * K)
+        _need_bytes("SX", out[1], (K // GROUP) * ldS * 4)
+    _need_gpu(X)
     if out is not None:
         Q, SX = out
     else:
@@ -109,8 +153,15 @@ def quant_rows(X: torch.Tensor, ldS: int | None = None, out=None):
 
 def gemm_ptq1_i8(A8: torch.Tensor, SX: torch.Tensor, W: torch.Tensor, K: int, N: int,
                  out_dtype=torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
-    _need_gpu(A8, SX, W)
     M = A8.shape[0]
+    if A8.dim() != 2 or A8.shape[1] != K:
+        raise ValueError(f"A8 must be [M][K={K}]")
+    if SX.dim() != 2 or SX.shape[0] < K // GROUP or SX.shape[1] < M:
+        raise ValueError(f"SX must be [>= {K // GROUP}][ldS >= {M}]")
+    _need_bytes("W", W, _ptq1_bytes(K, N))
+    if out is not None and (out.dim() != 2 or out.shape[0] < M or out.shape[1] < N):
+        raise ValueError(f"out must be [>= {M}][>= {N}]")
+    _need_gpu(A8, SX, W)
     C = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=A8.device)
     cdt = KATA_F16 if C.dtype == torch.float16 else KATA_F32
     check(lib().kata_gemm_ptq1_i8(_ptr(A8), _ptr(SX), SX.shape[1], _ptr(W), _ptr(C), cdt, C.shape[1],
@@ -119,6 +170,7 @@ def gemm_ptq1_i8(A8: torch.Tensor, SX: torch.Tensor, W: torch.Tensor, K: int, N:
 
 
 def expand_f16(W: torch.Tensor, K: int, N: int) -> torch.Tensor:
+    _need_bytes("W", W, _ptq1_bytes(K, N))
     _need_gpu(W)
     out = torch.empty((N, K), dtype=torch.float16, device=W.device)
     check(lib().kata_expand_ptq1_f16(_ptr(W), _ptr(out), K, N, _stream(W)))
@@ -126,6 +178,7 @@ def expand_f16(W: torch.Tensor, K: int, N: int) -> torch.Tensor:
 
 
 def expand_i8(W: torch.Tensor, K: int, N: int):
+    _need_bytes("W", W, _ptq1_bytes(K, N))
     _need_gpu(W)
     T8 = torch.empty((N, K), dtype=torch.int8, device=W.device)
     SW = torch.empty((N, K // GROUP), dtype=torch.float32, device=W.device)

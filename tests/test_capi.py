@@ -172,3 +172,49 @@ def test_gemv_wide_rejects():
     assert lib.kata_gemv_ptq1_wide(p, p, 7, p, 1024, 16, 4, None) == KATA_EINVAL
     assert lib.kata_gemv_ptq1_wide(p, ctypes.c_void_p(0x10008), 1, p, 1024, 16, 4, None) == KATA_EINVAL
     assert lib.kata_gemv_ptq1_wide(None, p, 1, p, 1024, 16, 4, None) == KATA_EINVAL
+
+
+def test_fwht_rejects_aliasing():
+    """An output overlapping an input is rejected before any launch (workgroups re-read their
+    row while others write theirs); no GPU is needed for the argument checks."""
+    import ctypes
+    from kata_amd.capi import lib, KATA_EINVAL
+    L = lib()
+    buf = (ctypes.c_float * (4 * 1024 * 4 + 64))()
+    base = (ctypes.addressof(buf) + 15) & ~15
+    x, y, gs, out = base, base + 4096 * 4, base + 2 * 4096 * 4, base + 3 * 4096 * 4
+    W, M = 1024, 4
+    # xnew == x (in-place residual), xnew == y, out over x, out over gs
+    for args in ((x, y, gs, out, x), (x, y, gs, out, y), (x, y, gs, x + 64, None), (x, y, gs, gs, None)):
+        xx, yy, gg, oo, xn = args
+        rc = L.kata_add_rms_fwht(xx, yy, gg, oo, 0, 0, xn, None, None, 0, W, M, None)
+        assert rc == KATA_EINVAL and b"overlap" in L.kata_last_error(), args
+    rc = L.kata_rms_fwht(x, y, gs, y, 0, 0, W, M, 1, None)       # out over src2 (SwiGLU)
+    assert rc == KATA_EINVAL and b"overlap" in L.kata_last_error()
+
+
+def test_torch_front_end_checks_sizes():
+    """Shape arguments that do not match the tensors raise ValueError before anything
+    reaches the device (CPU tensors: the size checks come first)."""
+    import torch
+    from kata_amd import ops
+    W = torch.zeros(2 * 40 * 28, dtype=torch.uint8)            # 2 rows of K = 5120
+    x = torch.zeros((1, 5120), dtype=torch.float16)
+    with pytest.raises(ValueError, match="W holds"):
+        ops.gemv_ptq1(W, x, 5120, 3)                            # N too large for W
+    with pytest.raises(ValueError, match="x holds"):
+        ops.gemv_ptq1(W, x, 5120, 2, T=2)                       # x has one token
+    with pytest.raises(ValueError, match="out holds"):
+        ops.gemv_ptq1(W, x, 5120, 2, out=torch.zeros(1))
+    with pytest.raises(ValueError, match="multiple"):
+        ops.gemv_ptq1(W, x, 5000, 2)
+    with pytest.raises(ValueError, match=r"Ws\[1\] holds"):
+        ops.gemv_ptq1_batch([W, W[:100]], x, 5120, [2, 2])
+    with pytest.raises(ValueError, match="W holds"):
+        ops.gemv_q8(torch.zeros(10, dtype=torch.uint8), x, 5120, 1)
+    with pytest.raises(ValueError, match="lda"):
+        ops.gemm_ptq1_f16(torch.zeros((4, 1024), dtype=torch.float16), W, 5120, 2)
+    with pytest.raises(ValueError, match="SX"):
+        ops.gemm_ptq1_i8(torch.zeros((4, 5120), dtype=torch.int8), torch.zeros((40, 2)), W, 5120, 2)
+    with pytest.raises(ValueError, match="W holds"):
+        ops.expand_f16(W, 5120, 3)

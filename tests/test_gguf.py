@@ -88,3 +88,46 @@ def test_gguf_upload_feeds_gemv_by_offset(tmp_path):
     xq = torch.from_numpy(orc.synth_x(1, 64, 3)).to(dev)
     yq = ops.gemv_q8(buf[o:o + q8.nbytes], xq, 64, 16, 1).cpu().numpy()
     assert rel_l2(yq, orc.gemv_q8(q8.reshape(16, -1), xq.cpu().numpy(), 64, 16, 1)).max() < 1e-5
+
+
+def _raw(infos, data_len, alignment=32, pad_data=True):
+    """A GGUF file with hand-written tensor infos [(name, dims, type, offset)] and data_len
+    zero bytes of data (pad_data=False: the file ends right after the header, unpadded)."""
+    import struct
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(infos), 1) + s("general.alignment") + struct.pack("<II", 4, alignment)
+    for name, dims, typ, off in infos:
+        head += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", typ, off)
+    if pad_data:
+        head += b"\0" * ((-len(head)) % alignment)
+    return head + b"\0" * data_len
+
+
+def test_gguf_rejects_out_of_range_and_unknown(tmp_path):
+    """Tensor ranges checked term by term (no uint64 wrap-around), unknown ggml types and
+    element counts that overflow or are not whole blocks rejected, a header that runs past
+    the end of the file rejected."""
+    ok = _raw([("w", [256, 2], GGML_PTQ1_0, 0)], 112)
+    p = tmp_path / "ok.gguf"
+    p.write_bytes(ok)
+    h = L.lib().kata_gguf_open(str(p).encode())
+    assert h
+    L.lib().kata_gguf_close(h)
+    cases = {
+        "wrapped_offset": _raw([("w", [256, 2], GGML_PTQ1_0, (1 << 64) - 64)], 112),
+        "offset_past_end": _raw([("w", [256, 2], GGML_PTQ1_0, 64)], 112),
+        "bytes_past_end": _raw([("w", [256, 2], GGML_PTQ1_0, 0)], 100),
+        "unknown_type": _raw([("w", [256, 2], 99, 0)], 112),
+        "dims_overflow": _raw([("w", [1 << 40, 1 << 40], GGML_F32, 0)], 64),
+        "bytes_overflow": _raw([("w", [1 << 62, 1], GGML_F32, 0)], 64),
+        "not_whole_blocks": _raw([("w", [100, 2], GGML_PTQ1_0, 0)], 112),
+        "header_past_end": _raw([], 0, alignment=1 << 20, pad_data=False),
+    }
+    for name, data in cases.items():
+        q = tmp_path / f"{name}.gguf"
+        q.write_bytes(data)
+        assert not L.lib().kata_gguf_open(str(q).encode()), name
+        assert L.lib().kata_last_error(), name
