@@ -245,6 +245,33 @@ int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp,
                              float* out, int H, int F, int T, void* stream);
 size_t kata_ffn_verify_work_bytes(int H, int F, int T);
 
+/* Any sublayer's matmul halves through the dispatcher's weights, in the three forms of the
+ * engine: KATA_FORM_DECODE (M == 1: Engine::step, src/engine.cpp:150-182), KATA_FORM_PREFILL
+ * (M rows, GEMMs on the fp16 exact or int8 path as kata_dispatch_set_i8 selected, h quantised
+ * once for its int8 matrices: Engine::prefill, src/engine.cpp:247-300) and KATA_FORM_VERIFY
+ * (M <= 8 tokens through the wide GEMV: Engine::verify2 / verifyWide, src/engine.cpp:454-491,
+ * 627-629).
+ * Input half: h = H(rmsnorm(x + y) * gs) (x + y also to xnew; gamma/hout as in
+ * kata_add_rms_fwht: the plain normalised rows the GDN alpha/beta projections read), then
+ * outs[i] = W_i h (fp32 [M][N[i]]) for the 1..4 matrices that read h, at byte offsets offs[i],
+ * named as in kata_dispatch_set_i8 (GDN: "qkv", "z"; GQA: "wq", "wk", "wv"; FFN: "gate",
+ * "up").  offs, N, names, outs are HOST arrays; x, y, xnew fp32 [M][H].
+ * Output half: t = H(v * gs), v per mode of kata_rms_fwht (1 SwiGLU of src, src2 before
+ * "down"; 2 GDN head order of src, W == 6144, before "ssmout"; 3 src before "wo"), then
+ * out = W t (fp32 [M][H]).  src, src2 fp32 [M][W].
+ * H, W multiples of 1024; work of kata_dispatch_work_bytes(form, H or W, M) bytes, 16-byte
+ * aligned; the prefill and verify forms use the workspace of kata_gemm_ptq1_f16. */
+#define KATA_FORM_DECODE 0
+#define KATA_FORM_PREFILL 1
+#define KATA_FORM_VERIFY 2
+int kata_dispatch_in(kata_dispatch* d, int form, int count, const uint64_t* offs, const int* N,
+                     const char* const* names, float* const* outs, const float* x, const float* y, float* xnew,
+                     const float* gs, const float* gamma, void* hout, int hout_dtype, void* work, int H, int M,
+                     void* stream);
+int kata_dispatch_out(kata_dispatch* d, int form, uint64_t off, const char* name, const float* src, const float* src2,
+                      int mode, const float* gs, void* work, float* out, int W, int H, int M, void* stream);
+size_t kata_dispatch_work_bytes(int form, int K, int M);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ _lib = None
 KATA_F32, KATA_F16 = 0, 1
 KATA_X_ROWS, KATA_X_HALF2 = 0, 1
 KATA_EINVAL, KATA_ELAUNCH = -1, -2
+KATA_FORM_DECODE, KATA_FORM_PREFILL, KATA_FORM_VERIFY = 0, 1, 2
 
 
 class KataError(RuntimeError):
@@ -74,6 +75,9 @@ SIGNATURES = {
     "kata_ffn_prefill_work_bytes": (SZ, [I, I, I]),
     "kata_dispatch_ffn_verify": (I, [P, U64, U64, U64, P, P, P, P, P, P, P, I, I, I, P]),
     "kata_ffn_verify_work_bytes": (SZ, [I, I, I]),
+    "kata_dispatch_in": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, I, P, I, I, P]),
+    "kata_dispatch_out": (I, [P, I, U64, ctypes.c_char_p, P, P, I, P, P, P, I, I, I, P]),
+    "kata_dispatch_work_bytes": (SZ, [I, I, I]),
 }
 
 

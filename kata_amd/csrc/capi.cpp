@@ -479,6 +479,108 @@ int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp,
     return kata_gemv_ptq1_wide(d->wbase + offDown, t, KATA_F16, out, F, H, T, stream);
 }
 
+// ------------------------------------------------------------------ sublayer halves
+// Work layout of kata_dispatch_in / _out for a transform width K and M rows: decode fp32
+// [K]; verify fp16 [M][K]; prefill fp16 [M][K], then int8 [M][K] and fp32 [K/128][M] for the
+// int8 path's quantised rows and scales (16-byte aligned parts).
+static size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
+
+size_t kata_dispatch_work_bytes(int form, int K, int M) {
+    if (K <= 0 || M <= 0) return 0;
+    const size_t k = (size_t)K, m = (size_t)M;
+    switch (form) {
+        case KATA_FORM_DECODE: return align16(4 * k);
+        case KATA_FORM_VERIFY: return align16(2 * m * k);
+        case KATA_FORM_PREFILL: return align16(2 * m * k) + align16(m * k) + align16(4 * (k / 128) * m);
+        default: return 0;
+    }
+}
+
+namespace {
+struct HalfWork {
+    void* act;      // the transformed activation: fp32 (decode) or fp16 rows
+    int8_t* A8;     // prefill: quantised rows
+    float* SX;      // prefill: their group scales [K/128][M]
+};
+HalfWork half_work(void* work, int K, int M) {
+    uint8_t* b = (uint8_t*)work;
+    const size_t k = (size_t)K, m = (size_t)M;
+    HalfWork w{b, (int8_t*)(b + align16(2 * m * k)), nullptr};
+    w.SX = (float*)((uint8_t*)w.A8 + align16(m * k));
+    return w;
+}
+int check_form(int form, int M, int K) {
+    if (form != KATA_FORM_DECODE && form != KATA_FORM_PREFILL && form != KATA_FORM_VERIFY)
+        return fail(KATA_EINVAL, "form=%d", form);
+    if (form == KATA_FORM_DECODE && M != 1) return fail(KATA_EINVAL, "the decode form takes M == 1 (M=%d)", M);
+    if (form == KATA_FORM_VERIFY && (M < 1 || M > 8)) return fail(KATA_EINVAL, "the verify form takes 1..8 tokens (M=%d)", M);
+    if (M < 1) return fail(KATA_EINVAL, "M=%d must be positive", M);
+    if (K <= 0 || K % 1024 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 1024", K);
+    return KATA_OK;
+}
+// one matmul of the transformed activation (K wide, M rows) with the named matrix
+int half_matmul(kata_dispatch* d, int form, uint64_t off, const char* name, const HalfWork& w, float* out, int K,
+                int N, int M, bool quantised, hipStream_t st) {
+    const uint8_t* Wm = d->wbase + off;
+    switch (form) {
+        case KATA_FORM_DECODE:
+            return kata_gemv_ptq1(Wm, w.act, KATA_F32, KATA_X_ROWS, out, K, N, 1, st);
+        case KATA_FORM_VERIFY:
+            return kata_gemv_ptq1_wide(Wm, w.act, KATA_F16, out, K, N, M, st);
+        default:
+            if (kata_dispatch_i8(d, name)) {
+                int rc = quantised ? KATA_OK : kata_quant_rows_i8((const uint16_t*)w.act, w.A8, w.SX, M, K, M, st);
+                return rc ? rc : kata_gemm_ptq1_i8(w.A8, w.SX, M, Wm, out, KATA_F32, N, M, K, N, st);
+            }
+            return kata_gemm_ptq1_f16((const uint16_t*)w.act, K, Wm, out, KATA_F32, N, M, K, N, st);
+    }
+}
+}  // namespace
+
+int kata_dispatch_in(kata_dispatch* d, int form, int count, const uint64_t* offs, const int* N,
+                     const char* const* names, float* const* outs, const float* x, const float* y, float* xnew,
+                     const float* gs, const float* gamma, void* hout, int hout_dtype, void* work, int H, int M,
+                     void* stream) {
+    if (!d || !offs || !N || !names || !outs || !x || !gs || !work) return fail(KATA_EINVAL, "null argument");
+    if (count < 1 || count > 4) return fail(KATA_EINVAL, "count=%d must be 1..4", count);
+    if (int rc = check_form(form, M, H)) return rc;
+    for (int i = 0; i < count; i++) {
+        if (!outs[i] || N[i] <= 0) return fail(KATA_EINVAL, "matrix %d: null output or N=%d", i, N[i]);
+        if (!names[i] || !i8_bit(names[i], strlen(names[i])))
+            return fail(KATA_EINVAL, "matrix %d: unknown name '%s'", i, names[i] ? names[i] : "(null)");
+    }
+    const hipStream_t st = (hipStream_t)stream;
+    const HalfWork w = half_work(work, H, M);
+    const int act_dt = form == KATA_FORM_DECODE ? KATA_F32 : KATA_F16;
+    int rc = kata_add_rms_fwht(x, y, gs, w.act, act_dt, KATA_X_ROWS, xnew, gamma, hout, hout_dtype, H, M, stream);
+    if (rc) return rc;
+    if (form == KATA_FORM_DECODE) {                  // one launch for all matrices that read h
+        const uint8_t* Wm[4];
+        for (int i = 0; i < count; i++) Wm[i] = d->wbase + offs[i];
+        return kata_gemv_ptq1_batch(count, Wm, outs, N, w.act, KATA_F32, KATA_X_ROWS, H, 1, stream);
+    }
+    bool quantised = false;                          // prefill: quantise h once for its int8 matrices
+    for (int i = 0; i < count; i++) {
+        if ((rc = half_matmul(d, form, offs[i], names[i], w, outs[i], H, N[i], M, quantised, st))) return rc;
+        quantised = quantised || (form == KATA_FORM_PREFILL && kata_dispatch_i8(d, names[i]));
+    }
+    return KATA_OK;
+}
+
+int kata_dispatch_out(kata_dispatch* d, int form, uint64_t off, const char* name, const float* src, const float* src2,
+                      int mode, const float* gs, void* work, float* out, int W, int H, int M, void* stream) {
+    if (!d || !name || !src || !gs || !work || !out) return fail(KATA_EINVAL, "null argument");
+    if (!i8_bit(name, strlen(name))) return fail(KATA_EINVAL, "unknown matrix name '%s'", name);
+    if (mode < 1 || mode > 3) return fail(KATA_EINVAL, "mode=%d must be 1 (SwiGLU), 2 (GDN order) or 3 (plain)", mode);
+    if (int rc = check_form(form, M, W)) return rc;
+    if (H <= 0) return fail(KATA_EINVAL, "H=%d must be positive", H);
+    const HalfWork w = half_work(work, W, M);
+    int rc = kata_rms_fwht(src, src2, gs, w.act, form == KATA_FORM_DECODE ? KATA_F32 : KATA_F16, KATA_X_ROWS, W, M, mode,
+                           stream);
+    if (rc) return rc;
+    return half_matmul(d, form, off, name, w, out, W, H, M, false, (hipStream_t)stream);
+}
+
 size_t kata_ffn_verify_work_bytes(int H, int F, int T) { return (size_t)T * H * 2 + (size_t)T * F * 10; }
 
 size_t kata_ffn_prefill_work_bytes(int H, int F, int M) {

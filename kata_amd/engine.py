@@ -8,6 +8,10 @@ src/engine.cpp:27) and maps (byte offset, K, N, matrix name) to the kernels:
                                        src/engine.h:89-95)
   ffn_decode / ffn_prefill / ffn_verify  <- the FFN block of Engine::step, prefill and
                                        verifyWide (src/engine.cpp:176-182, 247-300, 627-629)
+  sub_in / sub_out                  <- the matmul halves of any sublayer (GDN: qkv + z and
+                                       ssm_out; GQA: q + k + v and o; FFN: gate + up and
+                                       down) in the decode, prefill and verify forms
+                                       (src/engine.cpp:150-182, 247-300, 454-491)
 Errors raise KataError instead of the reference's exit(1).
 """
 from __future__ import annotations
@@ -16,7 +20,7 @@ import ctypes
 
 import torch
 
-from .capi import KataError, check, lib
+from .capi import KATA_FORM_DECODE, KATA_FORM_PREFILL, KATA_FORM_VERIFY, KataError, check, lib
 from .ops import _ptr, _stream
 
 I8_NAMES = ("qkv", "z", "ssmout", "wq", "wk", "wv", "wo", "gate", "up", "down")
@@ -109,6 +113,46 @@ class Dispatch:
                                              _ptr(gs_in), _ptr(gs_down), _ptr(work), _ptr(out), H, F, T,
                                              _stream(self.wbuf)))
         return out
+
+
+    # ---- layer level: any sublayer's matmul halves
+    _FORMS = {"decode": KATA_FORM_DECODE, "prefill": KATA_FORM_PREFILL, "verify": KATA_FORM_VERIFY}
+
+    def sub_in(self, form: str, mats, x: torch.Tensor, y: torch.Tensor | None, gs: torch.Tensor,
+               xnew: torch.Tensor | None = None, gamma: torch.Tensor | None = None,
+               hout: torch.Tensor | None = None, work: torch.Tensor | None = None):
+        """h = H(rmsnorm(x + y) * gs) over M = x.shape[0] rows (decode: M == 1), then W_i h for
+        mats = [(offset, N, name)]: returns the fp32 outputs [M][N_i]."""
+        M, H = x.shape
+        dev = x.device
+        n = len(mats)
+        outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for _, N, _ in mats]
+        if work is None:
+            work = torch.empty(dispatch_work_bytes(form, H, M), dtype=torch.uint8, device=dev)
+        offs = (ctypes.c_uint64 * n)(*[o for o, _, _ in mats])
+        Ns = (ctypes.c_int * n)(*[N for _, N, _ in mats])
+        names = (ctypes.c_char_p * n)(*[nm.encode() for _, _, nm in mats])
+        optr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        hdt = 1 if hout is not None and hout.dtype == torch.float16 else 0
+        check(lib().kata_dispatch_in(self._h, self._FORMS[form], n, offs, Ns, names, optr, _ptr(x), _ptr(y), _ptr(xnew),
+                                     _ptr(gs), _ptr(gamma), _ptr(hout), hdt, _ptr(work), H, M, _stream(self.wbuf)))
+        return outs
+
+    def sub_out(self, form: str, off: int, name: str, src: torch.Tensor, src2: torch.Tensor | None, mode: int,
+                gs: torch.Tensor, H: int, work: torch.Tensor | None = None) -> torch.Tensor:
+        """t = H(transform_mode(src, src2) * gs), then W t: fp32 [M][H]."""
+        M, W = src.shape
+        dev = src.device
+        out = torch.empty((M, H), dtype=torch.float32, device=dev)
+        if work is None:
+            work = torch.empty(dispatch_work_bytes(form, W, M), dtype=torch.uint8, device=dev)
+        check(lib().kata_dispatch_out(self._h, self._FORMS[form], off, name.encode(), _ptr(src), _ptr(src2), mode,
+                                      _ptr(gs), _ptr(work), _ptr(out), W, H, M, _stream(self.wbuf)))
+        return out
+
+
+def dispatch_work_bytes(form: str, K: int, M: int) -> int:
+    return int(lib().kata_dispatch_work_bytes(Dispatch._FORMS[form], K, M))
 
 
 def ffn_prefill_work_bytes(H: int, F: int, M: int) -> int:

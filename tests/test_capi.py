@@ -162,6 +162,41 @@ def test_dispatch_ffn_rejects():
     assert lib.kata_ffn_prefill_work_bytes(1024, 2048, 8) == 8 * 2048 * 8 + 8 * 1024 * 2 + 8 * 2048 * 2 + 8 * 2048 + 16 + 16 * 8 * 4
 
 
+def test_dispatch_sub_rejects():
+    """The sublayer halves validate form, row count, widths and names before any launch."""
+    lib = L.lib()
+    h = ctypes.c_void_p(lib.kata_dispatch_create(FAKE))
+    p = FAKE
+    offs = (ctypes.c_uint64 * 2)(0, 100)
+    Ns = (ctypes.c_int * 2)(1024, 1024)
+    outs = (ctypes.c_void_p * 2)(0x10000, 0x20000)
+
+    def sub_in(form, names, H=2048, M=1, count=2):
+        nm = (ctypes.c_char_p * 2)(*[n.encode() for n in names])
+        return lib.kata_dispatch_in(h, form, count, offs, Ns, nm, outs, p, None, None, p, None, None, 0, p, H, M, None)
+    try:
+        assert sub_in(3, ["wq", "wk"]) == KATA_EINVAL                  # unknown form
+        assert sub_in(0, ["wq", "wk"], M=2) == KATA_EINVAL             # decode is one row
+        assert sub_in(2, ["wq", "wk"], M=9) == KATA_EINVAL             # verify holds <= 8 tokens
+        assert sub_in(1, ["wq", "wk"], M=0) == KATA_EINVAL
+        assert sub_in(1, ["wq", "wk"], H=2000, M=4) == KATA_EINVAL     # H a multiple of 1024
+        assert sub_in(1, ["wq", "lm_head"], M=4) == KATA_EINVAL        # names from the i8 set
+        assert sub_in(1, ["wq", "wk"], M=4, count=5) == KATA_EINVAL
+        out = lib.kata_dispatch_out
+        assert out(h, 0, 0, b"wo", p, None, 4, p, p, p, 6144, 5120, 1, None) == KATA_EINVAL     # mode 1..3
+        assert out(h, 0, 0, b"bogus", p, None, 3, p, p, p, 6144, 5120, 1, None) == KATA_EINVAL
+        assert out(h, 2, 0, b"wo", p, None, 3, p, p, p, 6144, 5120, 9, None) == KATA_EINVAL
+        assert out(h, 1, 0, b"wo", p, None, 3, p, p, p, 6000, 5120, 4, None) == KATA_EINVAL
+        assert out(h, 1, 0, b"wo", p, None, 3, p, p, p, 6144, 0, 4, None) == KATA_EINVAL
+        assert out(h, 1, 0, b"wo", None, None, 3, p, p, p, 6144, 5120, 4, None) == KATA_EINVAL
+    finally:
+        lib.kata_dispatch_destroy(h)
+    assert lib.kata_dispatch_work_bytes(0, 5120, 1) == 4 * 5120
+    assert lib.kata_dispatch_work_bytes(2, 5120, 3) == 2 * 3 * 5120
+    assert lib.kata_dispatch_work_bytes(1, 5120, 5) == 2 * 5 * 5120 + 5 * 5120 + 4 * 40 * 5
+    assert lib.kata_dispatch_work_bytes(3, 5120, 5) == 0
+
+
 def test_gemv_wide_rejects():
     lib = L.lib()
     p = FAKE
