@@ -28,9 +28,10 @@ Also reported (same JSON line):
   q8_0_t1      config 3: the Q8_0 MTP-head GEMV, 17408x5120 and 5120x17408;
   prefill_gemm pp512 exact fp16 GEMM TFLOPS (M=512, 5120->17408 and 17408->5120),
                vs 2.5 PFLOP/s dense fp16;
-  cpu_baseline the reference's host arithmetic for the path (PTQ1_0 decode + fp32 dot,
-               oracle/kata_oracle.c:orc_cpu_gemv_ptq1_f32) on a bounded row sample of the
-               same sweep, on this machine's host cores.
+  cpu_baseline the reference's host path for BASELINE config 1 (the full 17408x5120 matrix:
+               stage-loop dequantize_row_ptq1_0 + fp32 dot,
+               oracle/kata_oracle.c:orc_cpu_gemv_ptq1_stage) on all host cores this process
+               may use (nproc and the thread count stated), and on one thread.
 """
 from __future__ import annotations
 
@@ -159,20 +160,20 @@ def run_config5(torch, ops, dev, stream):
     return out
 
 
-def cpu_baseline(sample_rows: int, threads: int):
-    """Times the reference's host decode + fp32 dot on `sample_rows` rows of every sweep
-    matrix (same shapes and distributions), returns GB/s of packed bytes."""
+def cpu_baseline(threads: int, reps: int = 3):
+    """BASELINE config 1 on the host: the full 17408x5120 gate matrix, each row expanded by the
+    reference's stage-loop dequantize_row_ptq1_0 then fp32 dots (orc_cpu_gemv_ptq1_stage),
+    OpenMP over rows; best of `reps` runs, GB/s of packed bytes."""
     from oracle import oracle as orc
-    total_bytes, total_t = 0, 0.0
-    for i, (name, K, N, _) in enumerate(SWEEP):
-        rows = min(sample_rows, N)
-        W, _, _ = orc.synth_ptq1(rows, K, SEED + 1000 + i)
-        x = orc.synth_x(1, K, SEED + 2000 + i).astype(np.float32)
+    K, N = 5120, 17408
+    W, _, _ = orc.synth_ptq1(N, K, SEED + 1000)
+    x = orc.synth_x(1, K, SEED + 2000).astype(np.float32)
+    best = float("inf")
+    for _ in range(reps):
         t0 = time.perf_counter()
-        orc.cpu_gemv_f32(W, x, K, rows, 1, 0, rows, threads)
-        total_t += time.perf_counter() - t0
-        total_bytes += packed_bytes(K, rows)
-    return total_bytes / total_t / 1e9, total_bytes
+        orc.cpu_gemv_stage(W, x, K, N, 1, 0, N, threads)
+        best = min(best, time.perf_counter() - t0)
+    return packed_bytes(K, N) / best / 1e9, packed_bytes(K, N)
 
 
 def cpu_gemm_baseline(threads: int, rows: int = 512):
@@ -244,7 +245,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=2048)
     ap.add_argument("--graph", action="store_true",
                     help="replay each step's HIP graph instead of launching its GEMVs from Python")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer sweep and the M=7300 GEMMs")
@@ -397,6 +397,23 @@ def main():
         per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
                             "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
 
+    # ---- calibration (same protocol as per_matrix): the launch floor of an empty kernel at
+    # the GEMV's geometry and a plain streaming read at the sweep's sizes, over rotating
+    # buffers (>= 512 MB per size) so that reads come from HBM
+    calib = {}
+    cword = torch.zeros(4, dtype=torch.int32, device=dev)
+    calib["empty_us"] = round(time_reps(lambda r: ops.calib_empty(cword), args.reps), 3)
+    for label, nbytes in (("19.5MB", packed_bytes(5120, 17408)), ("39MB", 2 * packed_bytes(5120, 17408)),
+                          ("278MB", packed_bytes(5120, 248320))):
+        nb = max(2, -(-512 * 1024 * 1024 // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nb)]
+        for b_ in bufs:
+            b_.fill_(1)
+        us = time_reps(lambda r: ops.calib_read(bufs[r % nb], cword), args.reps if nbytes < 1e8 else 40)
+        calib[label] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        del bufs
+    calib["ffn_gate_vs_read_19.5MB"] = round(per_matrix["ffn_gate"]["us"] / calib["19.5MB"]["us"], 3)
+
     # ---- config 3: T=2 speculative-verify GEMV (two fp16 activation columns
     # shared per input) and the Q8_0 MTP-head GEMV (17408x5120 and 5120x17408, T=1)
     verify_t2 = {}
@@ -532,15 +549,21 @@ def main():
     # ---- CPU baseline (reference host arithmetic, bounded sample)
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        gbs, nbytes = cpu_baseline(args.cpu_rows, threads)
-        gbs1, nbytes1 = cpu_baseline(max(64, args.cpu_rows // 8), 1)
+        # all cores this process may use: the CPU affinity set, capped by the harness's per-GPU
+        # CPU share when one is set (OMP_NUM_THREADS)
+        nproc = os.cpu_count() or 1
+        avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        threads = min(avail, share) if share > 0 else avail
+        gbs, nbytes = cpu_baseline(threads)
+        gbs1, _ = cpu_baseline(1, reps=1)
         cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"first {args.cpu_rows} rows of each of the 10 sweep matrices "
-                         f"({nbytes/1e6:.1f} MB packed), fp32 decode+dot, OpenMP over rows",
+               "sample": f"BASELINE config 1 in full: 17408x5120 PTQ1_0 ({nbytes/1e6:.1f} MB packed), one fp32 "
+                         f"activation; stage-loop row dequantisation (dequantize_row_ptq1_0) + fp32 dot, "
+                         f"OpenMP over rows, best of 3; nproc={nproc}, affinity={avail}, "
+                         f"OMP_NUM_THREADS={share or 'unset'}",
                "single_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
-                                 "sample": f"first {max(64, args.cpu_rows // 8)} rows of each sweep matrix "
-                                           f"({nbytes1/1e6:.1f} MB)"},
+                                 "sample": "the same full matrix, one thread"},
                "prefill_gemm": cpu_gemm_baseline(threads)}
 
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary
@@ -578,6 +601,7 @@ def main():
         "one_launch_per_matrix": {"ms_per_step": round(ms_single / args.steps, 5),
                                   "GBps": round(set_bytes * args.steps / (ms_single * 1e-3) / 1e9, 1)},
         "per_matrix": per_matrix,
+        "calibration": calib,
         "verify_t2": verify_t2,
         "verify_wide": verify_wide,
         "q8_0_t1": q8,

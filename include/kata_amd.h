@@ -158,6 +158,15 @@ int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out
 int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype, int out_layout,
                   int W, int M, int mode, void* stream);
 
+/* Measurement helpers for the roofline figures; no counterpart in the reference (its
+ * benchmarks time Metal kernels only).  kata_calib_empty: an empty kernel of wgs
+ * 1024-thread workgroups (wgs <= 0: one per CU, the decode GEMV's geometry), the launch
+ * floor.  kata_calib_read: a plain streaming read of `bytes` bytes at p (16-byte aligned,
+ * < 2^31) at the same geometry, 16-byte loads, the achievable HBM read rate at that size;
+ * out (device, one word) is written only in a case that practically never happens. */
+int kata_calib_empty(uint32_t* out, int wgs, void* stream);
+int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* stream);
+
 /* Greedy argmax of n fp32 logits into *out (device int): an element counts only if strictly
  * greater than the best so far (NaN and -inf never do), lowest index on ties, 0x7fffffff
  * when none does.  x 16-byte aligned.  Deterministic; calls on one device must not overlap

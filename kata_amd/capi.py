@@ -78,6 +78,8 @@ SIGNATURES = {
     "kata_dispatch_in": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, I, P, I, I, P]),
     "kata_dispatch_out": (I, [P, I, U64, ctypes.c_char_p, P, P, I, P, P, P, I, I, I, P]),
     "kata_dispatch_work_bytes": (SZ, [I, I, I]),
+    "kata_calib_empty": (I, [P, I, P]),
+    "kata_calib_read": (I, [P, SZ, P, I, P]),
 }
 
 

@@ -266,6 +266,30 @@ int kata_argmax(const float* x, int n, int* out, void* stream) {
     return check_launch(kata::launch_argmax(x, n, out, (hipStream_t)stream), "argmax");
 }
 
+// ------------------------------------------------------------------ measurement helpers
+static int calib_wgs(int wgs) {
+    if (wgs > 0) return wgs;
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 256;
+    return n > 0 ? n : 256;
+}
+
+int kata_calib_empty(uint32_t* out, int wgs, void* stream) {
+    if (!out) return fail(KATA_EINVAL, "null pointer argument");
+    if (wgs > 65536) return fail(KATA_EINVAL, "wgs=%d", wgs);
+    return check_launch(kata::launch_calib_empty(out, calib_wgs(wgs), (hipStream_t)stream), "calib_empty");
+}
+
+int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* stream) {
+    if (!p || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (bytes == 0 || bytes > 0x7fffffffu) return fail(KATA_EINVAL, "bytes=%zu must be in 1..2^31-1", bytes);
+    if (!aligned(p, 16)) return fail(KATA_EINVAL, "p must be 16-byte aligned");
+    if (wgs > 65536) return fail(KATA_EINVAL, "wgs=%d", wgs);
+    return check_launch(kata::launch_calib_read((const uint8_t*)p, (uint32_t)bytes, out, calib_wgs(wgs), (hipStream_t)stream),
+                        "calib_read");
+}
+
 // ------------------------------------------------------------------ host packers
 // Byte encoding of the quantiser (docs/reference/prism_ptq1_0_quant_dequant.c:20-46):
 // stages of 16 and 8 bytes carry 5 digits each (most significant first, element

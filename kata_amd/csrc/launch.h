@@ -43,6 +43,10 @@ hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs
                             int out_layout, float* xnew, const float* gamma, void* hout, int flags, int W, int M,
                             int mode, hipStream_t s);
 
+// ---- measurement helpers (calib.hip): empty kernel and plain streaming read, wgs x 1024
+hipError_t launch_calib_empty(uint32_t* out, int wgs, hipStream_t s);
+hipError_t launch_calib_read(const uint8_t* p, uint32_t bytes, uint32_t* out, int wgs, hipStream_t s);
+
 // ---- argmax of the logits (argmax.hip)
 hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s);
 

@@ -224,6 +224,20 @@ def argmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     return o
 
 
+def calib_empty(out: torch.Tensor, wgs: int = 0) -> None:
+    """Empty kernel at the decode GEMV's launch geometry (the launch floor); out: int32 [>=1]."""
+    _need_gpu(out)
+    check(lib().kata_calib_empty(_ptr(out), wgs, _stream(out)))
+
+
+def calib_read(buf: torch.Tensor, out: torch.Tensor, nbytes: int | None = None, wgs: int = 0) -> None:
+    """Plain streaming read of nbytes (default: all) of buf at the decode GEMV's geometry."""
+    _need_gpu(buf, out)
+    n = _bytes(buf) if nbytes is None else nbytes
+    _need_bytes("buf", buf, n)
+    check(lib().kata_calib_read(_ptr(buf), n, _ptr(out), wgs, _stream(buf)))
+
+
 def _np_ptr(a: np.ndarray):
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(ctypes.c_void_p)

@@ -455,6 +455,35 @@ void orc_cpu_gemv_ptq1_f32(const uint8_t* W, const float* x, float* y, int K, in
     }
 }
 
+/* CPU baseline in the reference's own host form: each weight row is expanded to fp32 by
+ * the stage-loop dequantize_row_ptq1_0 (prism_ptq1_0_quant_dequant.c:54-84, restated in
+ * orc_ptq1_dequant_row above; d folded into every weight), then fp32 dots with the T
+ * activation rows.  OpenMP over rows, one row buffer per thread.                        */
+void orc_cpu_gemv_ptq1_stage(const uint8_t* W, const float* x, float* y, int K, int N, int T, int row0,
+                             int nrows, int nthreads) {
+    const int nb = K / ORC_GROUP;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        float* w = (float*)malloc((size_t)K * sizeof(float));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int r = row0; r < row0 + nrows; r++) {
+            orc_ptq1_dequant_row(W + (size_t)r * nb * ORC_BLOCK_BYTES, w, K);
+            for (int t = 0; t < T; t++) {
+                const float* xt = x + (size_t)t * K;
+                float s = 0.0f;
+                for (int k = 0; k < K; k++) s += w[k] * xt[k];
+                y[(size_t)t * N + r] = s;
+            }
+        }
+        free(w);
+    }
+}
+
 /* CPU baseline of the prefill GEMM (k_gemm_f16 semantics after k_expand_ptq1_v2,
  * shaders/prefill.metal:31-41,472-479): each weight row n in [row0, row0+nrows) is decoded
  * once to fp32 (half(t*d) is exact), then C[m][n] = sum_k A[m][k]*w[k] in fp32 for every A

@@ -56,6 +56,7 @@ def lib():
             "orc_expand_ptq1_i8": (None, [P, P, P, i, i]),
             "orc_gemm_i8": (None, [P, P, i, P, P, P, i, i, i]),
             "orc_cpu_gemv_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
+            "orc_cpu_gemv_ptq1_stage": (None, [P, P, P, i, i, i, i, i, i]),
             "orc_cpu_gemm_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
             "orc_norm_fwht": (None, [P, P, P, P, P, P, i, i, i, i]),
             "orc_omp_max_threads": (i, []),
@@ -188,6 +189,15 @@ def cpu_gemm_f32(A, W, M, K, N, row0, nrows, nthreads):
     C = np.zeros((M, N), np.float32)
     lib().orc_cpu_gemm_ptq1_f32(_p(A), _p(W), _p(C), M, K, N, row0, nrows, nthreads)
     return C
+
+
+def cpu_gemv_stage(W, x, K, N, T, row0, nrows, nthreads):
+    """CPU baseline in the reference's host form: stage-loop row dequantisation + fp32 dot."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(T, K)
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    y = np.zeros((T, N), np.float32)
+    lib().orc_cpu_gemv_ptq1_stage(_p(W), _p(x), _p(y), K, N, T, row0, nrows, nthreads)
+    return y
 
 
 def cpu_gemv_f32(W, x, K, N, T, row0, nrows, nthreads):

@@ -171,6 +171,8 @@ def test_cpu_baseline_matches_oracle():
     ref = orc.gemv_ptq1(W, x, 1024, 64, 2)
     got = orc.cpu_gemv_f32(W, x, 1024, 64, 2, 0, 64, 2)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-5
+    got = orc.cpu_gemv_stage(W, x, 1024, 64, 2, 0, 64, 2)     # the reference's host form
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-5
 
 
 # ------------------------------------------------------------------ prefill oracles
