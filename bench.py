@@ -27,7 +27,8 @@ Also reported (same JSON line):
   verify_wide  the wide verification GEMV (T = 4, 8 token rows) on the same shapes;
   q8_0_t1      config 3: the Q8_0 MTP-head GEMV, 17408x5120 and 5120x17408;
   prefill_gemm pp512 exact fp16 GEMM TFLOPS (M=512, 5120->17408 and 17408->5120),
-               vs 2.5 PFLOP/s dense fp16;
+               vs 2.5 PFLOP/s dense fp16, the int8 variant, and the Q8_0 MTP K/V catch-up
+               GEMM (eh_proj 10240->5120, wk 5120->1024, M=512);
   cpu_baseline the reference's host path for BASELINE config 1 (the full 17408x5120 matrix:
                stage-loop dequantize_row_ptq1_0 + fp32 dot,
                oracle/kata_oracle.c:orc_cpu_gemv_ptq1_stage) on all host cores this process
@@ -235,6 +236,31 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
         tops = 2.0 * M * N * K / (us_i * 1e-6) / 1e12
         gemm[name + "_i8"] = {"M": M, "K": K, "N": N, "quant_us": round(us_q, 1), "us": round(us_i, 1),
                               "TOPS": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+    # the MTP head's K/V catch-up over Q8_0 weights (eh_proj 10240 -> 5120, wk 5120 -> 1024),
+    # over two weight copies (eh_proj: 2 x 55.7 MB, past the L2s)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name, K, N in (("mtp_eh_proj_q8", 10240, 5120), ("mtp_wk_q8", 5120, 1024)):
+        rng = np.random.default_rng(K + N)
+        blk = rng.integers(-127, 128, size=(N, K // 32, 34), dtype=np.int64).astype(np.int8).view(np.uint8)
+        blk[:, :, 0:2] = np.abs(rng.normal(0.0, 0.02, size=(N, K // 32))).astype(np.float16).view(np.uint8).reshape(
+            N, K // 32, 2)
+        Wq = [torch.from_numpy(np.ascontiguousarray(blk).reshape(N, -1)).to(dev) for _ in range(2)]
+        Aq = torch.from_numpy(np.random.default_rng(K + 1).standard_normal((M, K)).astype(np.float16)).to(dev)
+        C = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for r in range(3):
+            ops.gemm_q8_f16(Aq, Wq[r % 2], K, N, out=C)
+        torch.cuda.synchronize()
+        nrep = 10
+        a.record(stream)
+        for r in range(nrep):
+            ops.gemm_q8_f16(Aq, Wq[r % 2], K, N, out=C)
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / nrep
+        tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        gemm[name] = {"M": M, "K": K, "N": N, "us": round(us, 1), "TFLOPS": round(tflops, 1),
+                      "frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+        del Wq
     return gemm
 
 

@@ -105,11 +105,19 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
  * 256x128 tile per CU), allocated on the device's first call that needs it and kept: calls
  * on one device must not overlap in time, and that first call must not be captured.  The
  * one workspace is shared by every entry point that uses it: kata_gemm_ptq1_f16,
- * kata_gemm_ptq1_i8, kata_gemv_ptq1_wide and the dispatcher's prefill and verification
+ * kata_gemm_q8_0_f16, kata_gemm_ptq1_i8, kata_gemv_ptq1_wide and the dispatcher's prefill and verification
  * calls (kata_dispatch_prefill, kata_dispatch_ffn_prefill, kata_dispatch_ffn_verify). 
  * Replaces Engine::dExpandGemm's fp16 path (src/engine.cpp:208-219: k_expand_ptq1_v2 into
  * a 178 MB stage, then Engine::dGemm / k_gemm_f16, shaders/prefill.metal:31-41). */
 int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
+                       int M, int K, int N, void* stream);
+
+/* The same exact fp16 GEMM over a Q8_0 matrix (34-byte blocks: fp16 d, 32 int8 q), decode
+ * fused: C[m][n] = sum_k A[m][k] * half(d[n][k/32] * q[n][k]) (half() rounds to nearest
+ * even), fp32 accumulation; K % 128 == 0, W 4-byte aligned, same A / C / workspace rules.
+ * Replaces the MTP K/V catch-up's k_expand_q8 + Engine::dGemm (src/engine.cpp:392-401,
+ * shaders/mtp.metal:24-33): eh_proj 10240 -> 5120, wk / wv 5120 -> 1024. */
+int kata_gemm_q8_0_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
                        int M, int K, int N, void* stream);
 
 /* Activation quantisation for the int8 prefill path: per (token m, 128-group g)

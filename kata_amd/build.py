@@ -17,11 +17,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkata_amd.so")
-SOURCES = ["gemv_ptq1.hip", "gemv_q8.hip", "gemm_f16.hip", "gemm_i8.hip", "expand.hip", "norm_fwht.hip", "argmax.hip", "calib.hip", "gguf.cpp", "capi.cpp"]
+SOURCES = ["gemv_ptq1.hip", "gemv_q8.hip", "gemm_f16.hip", "gemm_q8.hip", "gemm_i8.hip", "expand.hip", "norm_fwht.hip", "argmax.hip", "calib.hip", "gguf.cpp", "capi.cpp"]
 # Per-source extra flags.  The prefill GEMM keeps 144 fp32 accumulators per lane beside its
 # decode code; LLVM's iterative-ILP scheduler keeps them in place (the default one shuttles
 # them between register files every stage).
-EXTRA_FLAGS = {"gemm_f16.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
+EXTRA_FLAGS = {"gemm_f16.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+               "gemm_q8.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

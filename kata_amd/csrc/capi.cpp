@@ -160,6 +160,20 @@ int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, in
                         "gemm ptq1 f16");
 }
 
+int kata_gemm_q8_0_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M, int K,
+                       int N, void* stream) {
+    if (!A || !W || !C) return fail(KATA_EINVAL, "null pointer argument");
+    if (M <= 0 || N <= 0) return fail(KATA_EINVAL, "M=%d N=%d must be positive", M, N);
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (lda < K || lda % 8 != 0) return fail(KATA_EINVAL, "lda=%d must be >= K and a multiple of 8", lda);
+    if (ldc < N) return fail(KATA_EINVAL, "ldc=%d < N=%d", ldc, N);
+    if (c_dtype != KATA_F32 && c_dtype != KATA_F16) return fail(KATA_EINVAL, "c_dtype=%d", c_dtype);
+    if (!aligned(A, 16)) return fail(KATA_EINVAL, "A must be 16-byte aligned");
+    if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
+    return check_launch(kata::launch_gemm_q8(A, lda, W, C, c_dtype, ldc, M, K, N, (hipStream_t)stream),
+                        "gemm q8_0 f16");
+}
+
 int kata_quant_rows_i8(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS, void* stream) {
     if (!X || !Q || !SX) return fail(KATA_EINVAL, "null pointer argument");
     if (M <= 0) return fail(KATA_EINVAL, "M=%d must be positive", M);

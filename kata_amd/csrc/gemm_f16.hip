@@ -32,7 +32,7 @@
 #include "launch.h"
 
 #include <mutex>
-#include "gemm_sched.h"
+#include "gemm_tile.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -41,33 +41,11 @@ namespace kata {
 
 namespace {
 
-constexpr int BM = 256;          // rows of A / C per workgroup
-constexpr int BKS = 64;          // k per stage (halves)
-constexpr int ROWB = BKS * 2;    // LDS bytes per tile row
-constexpr int NT = 4;            // 32-column MFMA tiles per workgroup
-constexpr int BN = 32 * NT;      // columns per tile (128)
-constexpr int kABuf = 3;         // A stage buffers (DMA two stages ahead)
+using namespace gemm;
 constexpr int kWStage = BN * 32;    // staged packed bytes of one block of the tile rows, 32 B per row
-constexpr int kLdsBytes = kABuf * BM * ROWB + 2 * BN * ROWB + 2 * kWStage;
+constexpr int kLdsBytes = kTileBytes + 2 * kWStage;
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-
-__device__ inline uint32_t swz(int row, int chunk) { return (uint32_t)(row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4)); }
-
-// LDS DMA, 16 bytes per lane to lds + 16*lane (lds wave-uniform); issued through inline
-// assembly so that the compiler does not make later LDS accesses wait for every load in
-// flight; the kernel waits for these copies explicitly.  M0 is restored.
-__device__ inline void dma16(const void* g, uint32_t lds) {
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(g), "s"(lds)
-                 : "memory");
-}
-__device__ inline uint32_t lds_addr(const void* p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p);
-}
 
 // fp16 of (digit_n(b) - 1) * d for bytes in 16-bit lanes (b_lo, b_hi); lo = (-d, 0),
 // hi = (+d, +d) as fp16 bit pairs.  Returns the two halves as one dword.
@@ -111,8 +89,7 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
                                                        int ldc, float* __restrict__ ws, int M, int K, int N,
                                                        GemmJobs J) {
     extern __shared__ __align__(16) uint8_t smem[];
-    auto As = [&](int buf) { return smem + buf * (BM * ROWB); };
-    auto Bs = [&](int buf) { return smem + kABuf * BM * ROWB + buf * (BN * ROWB); };
+    auto Bs = [&](int buf) { return tile_b(smem, buf); };
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nbk = K >> 7;
@@ -124,108 +101,16 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
     const int nst = 2 * nb;                      // stages
     const uint32_t row_bytes = (uint32_t)nbk * kBlockBytes;
     A += (size_t)kb0 * 128;
-    auto barrier = [&]() {
-        __builtin_amdgcn_s_waitcnt((15 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-    };
+    auto barrier = [&]() { barrier_lds(); };
 
     if (wave < 4) {
-        // ================= consumers =================
-        const int l32 = lane & 31, lh = lane >> 5;
-        v16f acc[2][NT];
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < NT; j++)
-#pragma unroll
-                for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
-        // lane l reads row / column l % 32 of each 32-row tile at k = 16 kk + 8 (l / 32) .. +7,
-        // chunk 2 kk + l / 32; every tile row of this lane has the same swizzle term
-        const int xs = (l32 >> 1) & 7;
-        const uint32_t a_row = (uint32_t)(wave * 64 + l32) * ROWB, b_row = (uint32_t)l32 * ROWB;
-        auto load_frags = [&](int st, int kk, v8h (&af)[2], v8h (&bf)[NT]) {
-            const uint32_t c = (uint32_t)(((2 * kk + lh) ^ xs) << 4);
-            const uint8_t* at = As(st % kABuf) + a_row + c;
-            const uint8_t* bt = Bs(st & 1) + b_row + c;
-#pragma unroll
-            for (int i = 0; i < 2; i++) af[i] = *(const v8h*)(at + i * 32 * ROWB);
-#pragma unroll
-            for (int j = 0; j < NT; j++) bf[j] = *(const v8h*)(bt + j * 32 * ROWB);
-        };
-        auto mfmas = [&](v8h (&af)[2], v8h (&bf)[NT]) {
-#pragma unroll
-            for (int j = 0; j < NT; j++)
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        };
-        // fragments are loaded one k step ahead of the MFMAs that use them; the last step
-        // of a stage is loaded before the barrier that releases the stage's buffers
-        v8h a0[2], b0[NT], a1[2], b1[NT];
-        barrier();                               // the producers' first copies landed
-        barrier();                               // stage 0 produced
-        load_frags(0, 0, a0, b0);
-        for (int st = 0; st < nst; st++) {
-            load_frags(st, 1, a1, b1);
-            mfmas(a0, b0);
-            load_frags(st, 2, a0, b0);
-            mfmas(a1, b1);
-            load_frags(st, 3, a1, b1);
-            mfmas(a0, b0);
-            barrier();                           // stage st + 1 produced; stage st's buffers free
-            if (st + 1 < nst) load_frags(st + 1, 0, a0, b0);
-            mfmas(a1, b1);
-        }
-        // store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
-        if (job >= J.n_full) {
-            // piece: the whole fp32 tile, [256][128], into the job's workspace slot
-            float* P = ws + (size_t)(job - J.n_full) * (BM * BN);
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < NT; j++)
-#pragma unroll
-                    for (int q = 0; q < 16; q++)
-                        P[(wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3)) * BN + j * 32 + l32] = acc[i][j][q];
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < NT; j++) {
-                const int gc = j * 32 + l32;     // tile column
-                const int gn = n0 + gc;
-#pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const int gm = m0 + wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
-                    if (gm < M && gc < R) {
-                        if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][q];
-                        else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][q];
-                    }
-                }
-            }
+        consume<C_F16>(smem, wave, lane, nst, job, J, ws, C, ldc, M, m0, n0, R);
         return;
     }
 
     // ================= producers =================
     const int pw = wave - 4;
-    // ---- A: DMA instruction i of producer pw copies LDS bytes [1024 (4i + pw), +1024) of
-    // the stage's A tile: lane l -> tile row r = 8 (4i + pw) + l / 8, LDS slot l % 8, which
-    // holds global chunk (l % 8) ^ ((r >> 1) & 7) of that row (rows >= M read row M - 1)
-    const int ar_lo = 8 * pw + (lane >> 3);      // row for i = 0; + 32 i
-    const int aslot = lane & 7;
-    auto issue_a = [&](int st) {
-        const int s2 = min(st, nst - 1);         // stages past the end copy the last one
-        const int buf = st % kABuf;
-        const uint32_t base = lds_addr(As(buf)) + 1024 * pw;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int r = ar_lo + 32 * i;
-            const int chunk = aslot ^ ((r >> 1) & 7);
-            const _Float16* src = A + (size_t)min(m0 + r, M - 1) * lda + (size_t)s2 * BKS + chunk * 8;
-            dma16(src, base + 4096 * i);
-        }
-    };
+    auto issue_a = [&](int st) { gemm::issue_a(smem, pw, lane, A, lda, M, m0, st, nst); };
     // ---- weights: lane `lane` of producer pw decodes half q = pw & 1 of tile row
     // 64 (pw >> 1) + lane (q wave-uniform: no divergence).  The packed bytes of a block of
     // the tile's rows are copied into LDS by DMA (two 16-byte pieces per row, bytes 0..15

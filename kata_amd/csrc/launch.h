@@ -30,6 +30,8 @@ hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y
 // ---- prefill (gemm_f16.hip, gemm_i8.hip, expand.hip)
 hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
                            int M, int K, int N, hipStream_t s);
+hipError_t launch_gemm_q8(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M, int K,
+                          int N, hipStream_t s);
 hipError_t launch_quant_rows(const uint16_t* X, int8_t* Q, float* SX, int M, int K, int ldS,
                              hipStream_t s);
 hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C,

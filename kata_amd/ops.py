@@ -132,6 +132,24 @@ def gemm_ptq1_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=to
     return C
 
 
+def gemm_q8_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=torch.float32,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact fp16 GEMM over a Q8_0 matrix [N][K/32 * 34 B] (the MTP K/V catch-up)."""
+    if A.dtype != torch.float16:
+        raise ValueError("A must be fp16")
+    if A.dim() != 2 or A.shape[1] < K:
+        raise ValueError(f"A must be [M][lda] with lda >= K={K}")
+    M = A.shape[0]
+    _need_bytes("W", W, N * (K // Q8_GROUP) * Q8_BLOCK_BYTES)
+    if out is not None and (out.dim() != 2 or out.shape[0] < M or out.shape[1] < N):
+        raise ValueError(f"out must be [>= {M}][>= {N}]")
+    _need_gpu(A, W)
+    C = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=A.device)
+    cdt = KATA_F16 if C.dtype == torch.float16 else KATA_F32
+    check(lib().kata_gemm_q8_0_f16(_ptr(A), A.shape[1], _ptr(W), _ptr(C), cdt, C.shape[1], M, K, N, _stream(A)))
+    return C
+
+
 def quant_rows(X: torch.Tensor, ldS: int | None = None, out=None):
     """int8 rows and group scales of X; `out` = (Q, SX) to write into existing tensors."""
     M, K = X.shape

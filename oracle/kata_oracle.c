@@ -296,6 +296,41 @@ void orc_gemm_ptq1_f16(const uint16_t* A, const uint8_t* W, double* C, int M, in
     free(wexp); free(af); free(wf);
 }
 
+/* k_expand_q8 (shaders/mtp.metal:24-33): the fp16 weight of a Q8_0 element is
+ * half(d * float(q)), d the block's fp16 scale, rounded to nearest even.
+ * Pinned: numpy's float32 -> float16 conversion of d * q in tests.                       */
+void orc_expand_q8_f16(const uint8_t* W, uint16_t* out, int K, int N) {
+    const int nb = K / ORC_Q8_GROUP;
+    for (int n = 0; n < N; n++)
+        for (int b = 0; b < nb; b++) {
+            const uint8_t* blk = W + ((size_t)n * nb + b) * ORC_Q8_BLOCK_BYTES;
+            const float d = orc_half_to_float((uint16_t)(blk[0] | (blk[1] << 8)));
+            for (int i = 0; i < ORC_Q8_GROUP; i++)
+                out[(size_t)n * K + b * ORC_Q8_GROUP + i] = orc_float_to_half(d * (float)(int8_t)blk[2 + i]);
+        }
+}
+
+/* The MTP K/V catch-up GEMM, k_expand_q8 then dGemm (src/engine.cpp:392-401):
+ * C[m][n] = sum_k A[m][k] * Wexp[n][k], A and Wexp fp16, accumulated in double here.
+ * Pinned: textbook GEMM over orc_expand_q8_f16; tests compare a numpy matmul too.       */
+void orc_gemm_q8_f16(const uint16_t* A, const uint8_t* W, double* C, int M, int K, int N) {
+    uint16_t* wexp = (uint16_t*)malloc((size_t)N * K * 2);
+    float* af = (float*)malloc((size_t)M * K * 4);
+    float* wf = (float*)malloc((size_t)K * 4);
+    orc_expand_q8_f16(W, wexp, K, N);
+    for (size_t i = 0; i < (size_t)M * K; i++) af[i] = orc_half_to_float(A[i]);
+    for (int n = 0; n < N; n++) {
+        for (int k = 0; k < K; k++) wf[k] = orc_half_to_float(wexp[(size_t)n * K + k]);
+        for (int m = 0; m < M; m++) {
+            double s = 0.0;
+            const float* ar = af + (size_t)m * K;
+            for (int k = 0; k < K; k++) s += (double)ar[k] * (double)wf[k];
+            C[(size_t)m * N + n] = s;
+        }
+    }
+    free(wexp); free(af); free(wf);
+}
+
 /* Activation quantisation, k_quant_rows (shaders/prefill.metal:369-381):
  * per (token m, 128-group g): amax over the group, scale = amax > 0 ? amax/127 : 1,
  * q = clamp(rint(x * (1/scale)), -127, 127), sx[g*ldS + m] = scale.

@@ -56,6 +56,8 @@ def lib():
             "orc_expand_ptq1_i8": (None, [P, P, P, i, i]),
             "orc_gemm_i8": (None, [P, P, i, P, P, P, i, i, i]),
             "orc_cpu_gemv_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
+            "orc_expand_q8_f16": (None, [P, P, i, i]),
+            "orc_gemm_q8_f16": (None, [P, P, P, i, i, i]),
             "orc_cpu_gemv_ptq1_stage": (None, [P, P, P, i, i, i, i, i, i]),
             "orc_cpu_gemm_ptq1_f32": (None, [P, P, P, i, i, i, i, i, i]),
             "orc_norm_fwht": (None, [P, P, P, P, P, P, i, i, i, i]),
@@ -137,6 +139,23 @@ def gemm_f16(A, W, M, K, N) -> np.ndarray:
     W = np.ascontiguousarray(W, dtype=np.uint8)
     C = np.empty((M, N), np.float64)
     lib().orc_gemm_ptq1_f16(_p(A), _p(W), _p(C), M, K, N)
+    return C
+
+
+def expand_q8_f16(W, K, N) -> np.ndarray:
+    """k_expand_q8: fp16 half(d * q) of every Q8_0 element, [N][K]."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    out = np.empty((N, K), np.uint16)
+    lib().orc_expand_q8_f16(_p(W), _p(out), K, N)
+    return out.view(np.float16)
+
+
+def gemm_q8_f16(A, W, M, K, N) -> np.ndarray:
+    """MTP K/V catch-up GEMM: A fp16 [M][K] times the expanded Q8_0 matrix, double sums."""
+    A = np.ascontiguousarray(A, dtype=np.float16).view(np.uint16)
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    C = np.empty((M, N), np.float64)
+    lib().orc_gemm_q8_f16(_p(A), _p(W), _p(C), M, K, N)
     return C
 
 

@@ -295,3 +295,26 @@ def test_float_pipe_identity_exhaustive(golden):
     lhs = (digits * y).sum(axis=1)
     rhs = sum(g[k].astype(np.float64) * (y[:, k - 1] - 3 * y[:, k]) for k in range(1, 5)) + g[5] * y[:, 4]
     assert np.allclose(lhs, rhs, rtol=0, atol=1e-12)
+
+
+def test_expand_q8_matches_numpy():
+    """k_expand_q8: half(d * q) rounded to nearest even, incl. subnormal results and
+    overflow to infinity, bit for bit against numpy's float32 -> float16 conversion."""
+    rng = np.random.default_rng(21)
+    N, K = 6, 128
+    q = rng.integers(-128, 128, size=(N, K), dtype=np.int64).astype(np.int8)
+    d = (rng.choice([1e-7, 3e-5, 0.02, 1.0, 300.0, 700.0], size=(N, K // 32)) *
+         rng.choice([-1.0, 1.0], size=(N, K // 32))).astype(np.float16)
+    W = orc.q8_pack(q, d)
+    got = orc.expand_q8_f16(W, K, N)
+    with np.errstate(over="ignore"):
+        ref = (np.repeat(d.astype(np.float32), 32, axis=1) * q.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    assert np.isinf(got).any() and (np.abs(got[np.isfinite(got)]) < 6.1e-5).any()
+
+
+def test_gemm_q8_oracle_vs_numpy():
+    W, q, d = orc.synth_q8(9, 256, 22)
+    A = orc.synth_x(5, 256, 23)
+    wexp = orc.expand_q8_f16(W, 256, 9).astype(np.float64)
+    np.testing.assert_allclose(orc.gemm_q8_f16(A, W, 5, 256, 9), A.astype(np.float64) @ wexp.T, rtol=1e-12, atol=1e-12)
