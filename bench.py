@@ -264,6 +264,46 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
     return gemm
 
 
+def graph_time(torch, fn, nrep, stream, cap_stream):
+    """us per call of fn(r), r = 0..nrep-1, captured once into a graph and replayed: the
+    host's per-launch cost (a Python call each) stays out of the timed region."""
+    for r in range(3):
+        fn(r)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap_stream):
+        for r in range(nrep):
+            fn(r)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    g.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / nrep
+
+
+def run_calibration(torch, ops, dev, stream, cap_stream, reps):
+    """The launch floor of an empty kernel at the decode GEMV's geometry and a plain streaming
+    read at the sweep's sizes (same protocol as per_matrix), over rotating buffers (>= 512 MB
+    per size) so that reads come from HBM."""
+    calib = {}
+    cword = torch.zeros(4, dtype=torch.int32, device=dev)
+    calib["empty_us"] = round(graph_time(torch, lambda r: ops.calib_empty(cword), reps, stream, cap_stream), 3)
+    for label, nbytes in (("19.5MB", packed_bytes(5120, 17408)), ("39MB", 2 * packed_bytes(5120, 17408)),
+                          ("278MB", packed_bytes(5120, 248320))):
+        nb = max(2, -(-512 * 1024 * 1024 // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nb)]
+        for b_ in bufs:
+            b_.fill_(1)
+        us = graph_time(torch, lambda r: ops.calib_read(bufs[r % nb], cword), reps if nbytes < 1e8 else 40,
+                        stream, cap_stream)
+        calib[label] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        del bufs
+    return calib
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,6 +315,8 @@ def main():
                     help="replay each step's HIP graph instead of launching its GEMVs from Python")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer sweep and the M=7300 GEMMs")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN sublayer figures")
+    ap.add_argument("--calib-only", action="store_true",
+                    help="only the calibration kernels (launch floor, plain read), then print them and exit")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the pp512 prefill GEMMs (for counter runs), then exit")
     ap.add_argument("--step-only", action="store_true",
@@ -294,6 +336,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
+    if args.calib_only:
+        print(json.dumps({"calibration": run_calibration(torch, ops, dev, stream, torch.cuda.Stream(dev), args.reps)}))
+        return
 
     if args.calib_copy:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE readings give the
@@ -400,44 +445,14 @@ def main():
     # ---- per matrix kind (config 2: 200 repeats each over rotating copies)
     per_matrix = {}
     def time_reps(fn, nrep):
-        """us per call of fn(r), r = 0..nrep-1, captured once into a graph and replayed: the
-        host's per-launch cost (a Python call each) stays out of the timed region."""
-        for r in range(3):
-            fn(r)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cap_stream):
-            for r in range(nrep):
-                fn(r)
-        g.replay()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        g.replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) * 1e3 / nrep
+        return graph_time(torch, fn, nrep, stream, cap_stream)
 
     for j, (name, K, N, grp) in enumerate(SWEEP):
         us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], xs[grp], K, N, 1, out=ys[j]), args.reps)
         per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
                             "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
 
-    # ---- calibration (same protocol as per_matrix): the launch floor of an empty kernel at
-    # the GEMV's geometry and a plain streaming read at the sweep's sizes, over rotating
-    # buffers (>= 512 MB per size) so that reads come from HBM
-    calib = {}
-    cword = torch.zeros(4, dtype=torch.int32, device=dev)
-    calib["empty_us"] = round(time_reps(lambda r: ops.calib_empty(cword), args.reps), 3)
-    for label, nbytes in (("19.5MB", packed_bytes(5120, 17408)), ("39MB", 2 * packed_bytes(5120, 17408)),
-                          ("278MB", packed_bytes(5120, 248320))):
-        nb = max(2, -(-512 * 1024 * 1024 // nbytes))
-        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nb)]
-        for b_ in bufs:
-            b_.fill_(1)
-        us = time_reps(lambda r: ops.calib_read(bufs[r % nb], cword), args.reps if nbytes < 1e8 else 40)
-        calib[label] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
-        del bufs
+    calib = run_calibration(torch, ops, dev, stream, cap_stream, args.reps)
     calib["ffn_gate_vs_read_19.5MB"] = round(per_matrix["ffn_gate"]["us"] / calib["19.5MB"]["us"], 3)
 
     # ---- config 3: T=2 speculative-verify GEMV (two fp16 activation columns

@@ -67,9 +67,9 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
 /* Wide verification GEMV: the same y[t][n] for T in 1..8 token rows, x [T][K] fp16 or fp32
  * (16-byte aligned), y [T][N] fp32, any K % 128 == 0 (the activation is quantised per K
  * chunk in-kernel, same 16-bit block fixed point as above).  Every weight byte is read
- * once for all T rows.  When K is split over workgroups the partial sums use the per-device
- * workspace of kata_gemm_ptq1_f16 (same rules: calls on one device must not overlap, the
- * first such call must not be captured).  T <= 2 runs the decode GEMV above (same result
+ * once for all T rows.  When K is split over workgroups the partial sums use the
+ * per-stream workspace of kata_gemm_ptq1_f16 (same rules: the first such call on a stream
+ * must not be captured).  T <= 2 runs the decode GEMV above (same result
  * as kata_gemv_ptq1 with these rows, no workspace).
  * Replaces Engine::dWide / xWideGemv (src/engine.cpp:542-556, src/engine.h:109,140; kernel
  * k_wide_m16_n16_k128_g4, shaders/wide.metal:41-99, whose x is fp16 rows padded to 16). */
@@ -101,12 +101,14 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
  * C[m][n] = sum_k A[m][k] * half(trit[n][k] * d[n][k/128]), fp32 accumulation.
  * A is fp16 [M][lda] (lda >= K), C is [M][ldc] of c_dtype (KATA_F32 or KATA_F16).
  * K % 128 == 0; any M >= 1, N >= 1.
- * The K-pieces of the last round of tiles use a per-device workspace (at most one fp32
- * 256x128 tile per CU), allocated on the device's first call that needs it and kept: calls
- * on one device must not overlap in time, and that first call must not be captured.  The
- * one workspace is shared by every entry point that uses it: kata_gemm_ptq1_f16,
- * kata_gemm_q8_0_f16, kata_gemm_ptq1_i8, kata_gemv_ptq1_wide and the dispatcher's prefill and verification
- * calls (kata_dispatch_prefill, kata_dispatch_ffn_prefill, kata_dispatch_ffn_verify). 
+ * The K-pieces of the last round of tiles use a workspace of the calling (device, stream)
+ * (at most one fp32 256x128 tile per CU), allocated on the first call on that stream that
+ * needs it and kept until the process ends; that first call must not be captured.  Calls on
+ * different streams use different workspaces; calls on one stream are ordered by it.  The
+ * entry points that use it: kata_gemm_ptq1_f16, kata_gemm_q8_0_f16, kata_gemm_ptq1_i8,
+ * kata_gemv_ptq1_wide and the dispatcher's prefill and verification calls
+ * (kata_dispatch_prefill, kata_dispatch_ffn_prefill, kata_dispatch_ffn_verify, the prefill
+ * and verify forms of kata_dispatch_in / kata_dispatch_out).
  * Replaces Engine::dExpandGemm's fp16 path (src/engine.cpp:208-219: k_expand_ptq1_v2 into
  * a 178 MB stage, then Engine::dGemm / k_gemm_f16, shaders/prefill.metal:31-41). */
 int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
@@ -177,8 +179,9 @@ int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* s
 
 /* Greedy argmax of n fp32 logits into *out (device int): an element counts only if strictly
  * greater than the best so far (NaN and -inf never do), lowest index on ties, 0x7fffffff
- * when none does.  x 16-byte aligned.  Deterministic; calls on one device must not overlap
- * (module-scope partials).  Replaces k_argmax (shaders/ops.metal:66-78) after the lm_head
+ * when none does.  x 16-byte aligned.  Deterministic; the per-workgroup partials live in a
+ * 2 KB buffer of the calling (device, stream), allocated on its first call (which must not
+ * be captured).  Replaces k_argmax (shaders/ops.metal:66-78) after the lm_head
  * GEMV (src/engine.cpp:191-192). */
 int kata_argmax(const float* x, int n, int* out, void* stream);
 

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkata_amd.so")
-SOURCES = ["gemv_ptq1.hip", "gemv_q8.hip", "gemm_f16.hip", "gemm_q8.hip", "gemm_i8.hip", "expand.hip", "norm_fwht.hip", "argmax.hip", "calib.hip", "gguf.cpp", "capi.cpp"]
+SOURCES = ["gemv_ptq1.hip", "gemv_q8.hip", "gemm_f16.hip", "gemm_q8.hip", "gemm_i8.hip", "expand.hip", "norm_fwht.hip", "argmax.hip", "calib.hip", "workspace.cpp", "gguf.cpp", "capi.cpp"]
 # Per-source extra flags.  The prefill GEMM keeps 144 fp32 accumulators per lane beside its
 # decode code; LLVM's iterative-ILP scheduler keeps them in place (the default one shuttles
 # them between register files every stage).

@@ -3,12 +3,13 @@
 // are), lowest index on ties; with no such element the result is 0x7fffffff, as there.
 //
 // Design: a grid of up to 256 workgroups, each reducing a contiguous range (16-byte loads,
-// a fixed-order reduction across lanes and waves) to one (value, index) pair in a
-// module-scope device array, then a one-workgroup launch reduces those pairs in workgroup
+// a fixed-order reduction across lanes and waves) to one (value, index) pair in a device
+// array of the calling stream, then a one-workgroup launch reduces those pairs in workgroup
 // order and writes the index: deterministic, and nothing has to be cleared between calls.
 // (A last-arriving-workgroup reduction in one launch needs a device-scope release per
 // workgroup, an L2 write-back on this chip, which costs more than the second launch.)
-// Calls on one device must not overlap (the pairs are module-scope).
+// Each (device, stream) has its own pair array (allocated on its first call): calls on
+// different streams do not share it.
 #include "launch.h"
 
 #include <math.h>
@@ -20,8 +21,10 @@ namespace kata {
 namespace {
 
 constexpr int kMaxGroups = 256;
-__device__ float g_part_v[kMaxGroups];
-__device__ int g_part_i[kMaxGroups];
+struct Part {
+    float v[kMaxGroups];
+    int i[kMaxGroups];
+};
 
 // element b at index ib after the current best a (indices increasing): strictly greater
 __device__ inline void take(float& a, int& ia, float b, int ib) {
@@ -51,7 +54,7 @@ __device__ inline void block_best(float& v, int& i, float* sv, int* si) {
         for (int w = 1; w < (int)blockDim.x / 64; w++) better(v, i, sv[w], si[w]);
 }
 
-__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int n) {
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int n, Part* __restrict__ part) {
     __shared__ float sv[4];
     __shared__ int si[4];
     const int tid = threadIdx.x, G = gridDim.x;
@@ -71,18 +74,18 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int
     for (int k = a1 + tid; k < hi; k += 256) take(v, idx, x[k], k);
     block_best(v, idx, sv, si);
     if (tid == 0) {
-        g_part_v[blockIdx.x] = v;
-        g_part_i[blockIdx.x] = idx;
+        part->v[blockIdx.x] = v;
+        part->i[blockIdx.x] = idx;
     }
 }
 
-__global__ __launch_bounds__(256) void k_argmax_final(int G, int* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_argmax_final(int G, const Part* __restrict__ part, int* __restrict__ out) {
     __shared__ float sv[4];
     __shared__ int si[4];
     const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int g = tid; g < G; g += 256) better(bv, bi, g_part_v[g], g_part_i[g]);
+    for (int g = tid; g < G; g += 256) better(bv, bi, part->v[g], part->i[g]);
     block_best(bv, bi, sv, si);
     if (tid == 0) *out = bi;
 }
@@ -91,10 +94,12 @@ __global__ __launch_bounds__(256) void k_argmax_final(int G, int* __restrict__ o
 
 hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s) {
     const int G = std::max(1, std::min(kMaxGroups, n / 1024));
-    hipLaunchKernelGGL(k_argmax, dim3(G), dim3(256), 0, s, x, n);
-    hipError_t e = hipGetLastError();
+    void* part = nullptr;
+    hipError_t e = stream_buffer(kBufArgmax, sizeof(Part), s, &part);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, G, out);
+    hipLaunchKernelGGL(k_argmax, dim3(G), dim3(256), 0, s, x, n, (Part*)part);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, G, (const Part*)part, out);
     return hipGetLastError();
 }
 

@@ -198,35 +198,15 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_f16(const _Float16* __restric
 
 }  // namespace
 
-hipError_t gemm_device(bool need_ws, int* n_cu, float** ws) {
-    struct Dev {
-        int n_cu = 0;
-        float* ws = nullptr;
-    };
-    static Dev tab[64];
-    static std::mutex mu;            // first-time set-up from several host threads
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+hipError_t gemm_device(bool need_ws, hipStream_t s, int* n_cu, float** ws) {
+    hipError_t e = device_cu_count(n_cu);
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(mu);
-    Dev& D = tab[dev];
-    if (!D.n_cu) {
-        int n = 0;
-        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-        D.n_cu = n > 0 ? n : 256;
-    }
-    if (need_ws && !D.ws) {
-        e = hipMalloc((void**)&D.ws, (size_t)D.n_cu * 256 * 128 * sizeof(float));
-        if (e != hipSuccess) {
-            D.ws = nullptr;
-            return e;
-        }
-    }
-    *n_cu = D.n_cu;
-    *ws = D.ws;
-    return hipSuccess;
+    *ws = nullptr;
+    if (!need_ws) return hipSuccess;
+    void* p = nullptr;
+    e = stream_buffer(kBufGemmPieces, (size_t)*n_cu * 256 * 128 * sizeof(float), s, &p);
+    *ws = (float*)p;
+    return e;
 }
 
 hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
@@ -243,10 +223,10 @@ hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C
     }
     int n_cu = 0;
     float* ws = nullptr;
-    hipError_t e = gemm_device(false, &n_cu, &ws);
+    hipError_t e = gemm_device(false, s, &n_cu, &ws);
     if (e != hipSuccess) return e;
     const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, n_cu);   // one workgroup per CU
-    if (J.n_jobs > J.n_full && (e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
+    if (J.n_jobs > J.n_full && (e = gemm_device(true, s, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
         hipLaunchKernelGGL(k_gemm_ptq1_f16<true>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, (const _Float16*)A, lda, W,
                            C, ldc, ws, M, K, N, J);

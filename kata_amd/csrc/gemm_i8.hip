@@ -238,10 +238,10 @@ hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint
                           int ldc, int M, int K, int N, hipStream_t s) {
     int n_cu = 0;
     float* ws = nullptr;
-    hipError_t e = gemm_device(false, &n_cu, &ws);
+    hipError_t e = gemm_device(false, s, &n_cu, &ws);
     if (e != hipSuccess) return e;
     const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, 2 * n_cu);
-    if (J.n_jobs > J.n_full && (e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
+    if (J.n_jobs > J.n_full && (e = gemm_device(true, s, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
         hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, dim3(J.n_jobs), dim3(256), 0, s, A8, SX, ldS, W, C, ldc, ws, M, K, N,
                            J);

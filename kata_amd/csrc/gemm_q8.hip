@@ -158,10 +158,10 @@ hipError_t launch_gemm_q8(const uint16_t* A, int lda, const uint8_t* W, void* C,
     }
     int n_cu = 0;
     float* ws = nullptr;
-    hipError_t e = gemm_device(false, &n_cu, &ws);
+    hipError_t e = gemm_device(false, s, &n_cu, &ws);
     if (e != hipSuccess) return e;
     const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, n_cu);   // one workgroup per CU
-    if (J.n_jobs > J.n_full && (e = gemm_device(true, &n_cu, &ws)) != hipSuccess) return e;
+    if (J.n_jobs > J.n_full && (e = gemm_device(true, s, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
         hipLaunchKernelGGL(k_gemm_q8_f16<true>, dim3(J.n_jobs), dim3(512), kQ8LdsBytes, s, (const _Float16*)A, lda, W,
                            C, ldc, ws, M, K, N, J);

@@ -109,9 +109,9 @@ inline hipError_t launch_pieces_sum(const float* ws, void* C, int c_dtype, int l
     return hipGetLastError();
 }
 
-// The calling thread's device: its CU count and the prefill workspace (room for one
-// 256 x 128 fp32 tile per CU: 32 MB on MI355X), allocated on the device's first call that
-// asks for it (need_ws) and kept.  Calls on one device share it and must not overlap in time.
-hipError_t gemm_device(bool need_ws, int* n_cu, float** ws);
+// The calling thread's device: its CU count and (need_ws) the K-piece workspace of stream s
+// (room for one 256 x 128 fp32 tile per CU: 32 MB on MI355X), allocated on the first call on
+// that (device, stream) that asks for it and kept; calls on other streams use their own.
+hipError_t gemm_device(bool need_ws, hipStream_t s, int* n_cu, float** ws);
 
 }  // namespace kata

@@ -988,7 +988,7 @@ hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_
     return launch_gemv_ptq1_multi(1, &W, &y, &N, x, x_dtype, x_layout, K, T, s);
 }
 
-hipError_t gemm_device(bool need_ws, int* n_cu, float** ws);
+hipError_t gemm_device(bool need_ws, hipStream_t s, int* n_cu, float** ws);
 
 // Wide GEMV launches: row groups of 128 rows x K chunks of at most kWideKC blocks; more
 // chunks than needed until there are about two jobs per CU.  With several chunks the
@@ -1055,11 +1055,11 @@ hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float*
                             hipStream_t s) {
     int n_cu = 0;
     float* ws = nullptr;
-    hipError_t e = gemm_device(false, &n_cu, &ws);
+    hipError_t e = gemm_device(false, s, &n_cu, &ws);
     if (e != hipSuccess) return e;
     auto get_ws = [&](float** p) {
         int n = 0;
-        return gemm_device(true, &n, p);
+        return gemm_device(true, s, &n, p);
     };
     return wide_launches(W, x, x_dtype, y, K, N, T, n_cu, get_ws, (size_t)n_cu * 256 * 128, s);
 }

@@ -7,6 +7,12 @@
 
 namespace kata {
 
+// ---- scratch memory (workspace.cpp): the calling thread's device's CU count, and a device
+// buffer of at least `bytes` for (device, kind, stream), allocated on first use and kept
+enum { kBufGemmPieces = 0, kBufArgmax = 1 };
+hipError_t device_cu_count(int* n_cu);
+hipError_t stream_buffer(int kind, size_t bytes, hipStream_t s, void** p);
+
 // ---- PTQ1_0 GEMV (gemv_ptq1.hip); x 16-byte aligned, rows [T][K] or half2 [K][2] (T = 2)
 hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                             hipStream_t s);
