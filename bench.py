@@ -266,9 +266,12 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
 
 def graph_time(torch, fn, nrep, stream, cap_stream):
     """us per call of fn(r), r = 0..nrep-1, captured once into a graph and replayed: the
-    host's per-launch cost (a Python call each) stays out of the timed region."""
-    for r in range(3):
-        fn(r)
+    host's per-launch cost (a Python call each) stays out of the timed region.  The warm-up
+    calls run on the capture stream: scratch buffers are per stream and are allocated by a
+    stream's first call, which cannot happen inside the capture."""
+    with torch.cuda.stream(cap_stream):
+        for r in range(3):
+            fn(r)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=cap_stream):

@@ -44,6 +44,11 @@ hipError_t stream_buffer(int kind, size_t bytes, hipStream_t s, void** p) {
             if ((e = hipFree(ent.first)) != hipSuccess) return e;
             ent = {nullptr, 0};
         }
+        // an allocation cannot be recorded into a graph: the first call on a stream that
+        // needs this buffer (or a larger one) has to run outside capture
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(s, &cs)) != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
         void* q = nullptr;
         if ((e = hipMalloc(&q, bytes)) != hipSuccess) return e;
         ent = {q, bytes};
