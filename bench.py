@@ -484,6 +484,18 @@ def main():
             ent[f"t{T}_us"] = round(us, 3)
             ent[f"t{T}_GBps"] = round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
         verify_wide[name] = ent
+    # verifyWide's gate + up in one batched launch (one quantisation of the token rows)
+    jg, ju = [i for i, e in enumerate(SWEEP) if e[0] in ("ffn_gate", "ffn_up")]
+    K, N = SWEEP[jg][1], SWEEP[jg][2]
+    ent = {"K": K, "N": 2 * N}
+    for T in (4, 8):
+        xw = torch.from_numpy(np.random.default_rng(SEED + 360).standard_normal((T, K)).astype(np.float16)).to(dev)
+        ygu = [torch.empty((T, N), dtype=torch.float32, device=dev) for _ in range(2)]
+        us = time_reps(lambda r: ops.gemv_ptq1_wide_batch([copies[r % ncopies][jg], copies[r % ncopies][ju]], xw, K,
+                                                          [N, N], outs=ygu), args.reps)
+        ent[f"t{T}_us"] = round(us, 3)
+        ent[f"t{T}_GBps"] = round(2 * packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
+    verify_wide["ffn_gate_up_batched"] = ent
     q8 = {}
     for name, K, N in (("gate", 5120, 17408), ("down", 17408, 5120)):
         nb = N * (K // 32) * 34
@@ -567,6 +579,17 @@ def main():
                                                    work=fwork), 40)
         ffn = {"H": H, "F": F, "decode_us": round(us_d, 2),
                "decode_GBps": round(set_b / (us_d * 1e-6) / 1e9, 1)}
+        # T = 8 verification tokens: transform, batched gate + up, SwiGLU transform, down
+        Tv = 8
+        vx = torch.randn((Tv, H), generator=gen, device=dev)
+        vy = torch.randn((Tv, H), generator=gen, device=dev)
+        vxn = torch.empty((Tv, H), device=dev)
+        vout = torch.empty((Tv, H), device=dev)
+        vwork = torch.empty(int(ops.lib().kata_ffn_verify_work_bytes(H, F, Tv)), dtype=torch.uint8, device=dev)
+        us_v = time_reps(lambda r: disp.ffn_verify(*offs(r), vx, vy, gsi, gsd, H, F, out=vout, xnew=vxn,
+                                                   work=vwork), 40)
+        ffn["verify_t8_us"] = round(us_v, 2)
+        ffn["verify_t8_GBps"] = round(set_b / (us_v * 1e-6) / 1e9, 1)
         M = 512
         px = torch.randn((M, H), generator=gen, device=dev)
         py = torch.randn((M, H), generator=gen, device=dev)
@@ -631,6 +654,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
+        "numerics": ("fp16 activation -> per-128-block 16-bit fixed point as two int8 limbs; ternary weights as "
+                     "int8 trits; exact int32 block sums on the int8 matrix cores; fp32 scale (fp16 d x block "
+                     "scale) and fp32 accumulation; fp32 output"),
         "data": "synthetic (seeded trits/scales/activations)",
         "config": {"workload": "BASELINE configs[1]: bs=1 decode GEMV sweep, one layer of each kind "
                                "(10 matrices in 6 launches, matrices sharing an input batched)",

@@ -65,24 +65,35 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
                          const void* x, int x_dtype, int x_layout, int K, int T, void* stream);
 
 /* Wide verification GEMV: the same y[t][n] for T in 1..8 token rows, x [T][K] fp16 or fp32
- * (16-byte aligned), y [T][N] fp32, any K % 128 == 0 (the activation is quantised per K
- * chunk in-kernel, same 16-bit block fixed point as above).  Every weight byte is read
- * once for all T rows.  When K is split over workgroups the partial sums use the
- * per-stream workspace of kata_gemm_ptq1_f16 (same rules: the first such call on a stream
- * must not be captured).  T <= 2 runs the decode GEMV above (same result
- * as kata_gemv_ptq1 with these rows, no workspace).
+ * (16-byte aligned), y [T][N] fp32, any K % 128 == 0, W 4-byte aligned.  T >= 3: a prep
+ * launch quantises the token rows once (same 16-bit block fixed point as above) into an
+ * activation image held in a buffer of the calling (device, stream), allocated on that
+ * stream's first such call (which must not be captured; calls on one stream are ordered,
+ * calls on different streams use their own buffers), then one launch reads every weight
+ * byte once for all T rows.  T <= 2 runs the decode GEMV above (same result as
+ * kata_gemv_ptq1 with these rows, no buffer).
  * Replaces Engine::dWide / xWideGemv (src/engine.cpp:542-556, src/engine.h:109,140; kernel
  * k_wide_m16_n16_k128_g4, shaders/wide.metal:41-99, whose x is fp16 rows padded to 16). */
 int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                         void* stream);
 
+/* The wide verification GEMV for 1..4 matrices that multiply the same token rows (same K),
+ * in one launch after one quantisation of the rows: y[i][t][n] for W[i] with N[i] rows (W,
+ * y and N are HOST arrays of count device pointers / row counts).  Results equal
+ * kata_gemv_ptq1_wide's per matrix bit for bit.  No counterpart function in the reference,
+ * which issues one dWide per matrix; this batches verifyWide's gate + up
+ * (src/engine.cpp:627-629) and the matrices that read one transformed activation in the
+ * wide verification of the attention and GDN sublayers. */
+int kata_gemv_ptq1_wide_batch(int count, const uint8_t* const* W, float* const* y, const int* N,
+                              const void* x, int x_dtype, int K, int T, void* stream);
+
 /* The same wide verification GEMV, allocating nothing: no counterpart in the reference; for
  * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  Same arguments and results as kata_gemv_ptq1_wide (bit
- * for bit); the K-chunk partial sums go to a fixed per-device array of
+ * for bit); the activation image goes to a fixed per-device array of
  * kata_gemv_ptq1_wide_noalloc_scratch_bytes() bytes (4 MiB) held by each device the library
- * runs on until the process ends, instead of the workspace.  Rejects (KATA_EINVAL) a K and T
- * whose partial sums for one 128-row group would not fit it (K beyond ~786000 at T = 8).
+ * runs on until the process ends, instead of the stream's buffer.  Rejects (KATA_EINVAL) a K
+ * whose image would not fit it (K beyond 172 928: 3104 bytes per 128 weights of a row).
  * Calls that overlap in time on one device share the array and race. */
 int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                                 void* stream);
@@ -105,10 +116,9 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
  * (at most one fp32 256x128 tile per CU), allocated on the first call on that stream that
  * needs it and kept until the process ends; that first call must not be captured.  Calls on
  * different streams use different workspaces; calls on one stream are ordered by it.  The
- * entry points that use it: kata_gemm_ptq1_f16, kata_gemm_q8_0_f16, kata_gemm_ptq1_i8,
- * kata_gemv_ptq1_wide and the dispatcher's prefill and verification calls
- * (kata_dispatch_prefill, kata_dispatch_ffn_prefill, kata_dispatch_ffn_verify, the prefill
- * and verify forms of kata_dispatch_in / kata_dispatch_out).
+ * entry points that use it: kata_gemm_ptq1_f16, kata_gemm_q8_0_f16, kata_gemm_ptq1_i8 and
+ * the dispatcher's prefill calls (kata_dispatch_prefill, kata_dispatch_ffn_prefill, the
+ * prefill forms of kata_dispatch_in / kata_dispatch_out).
  * Replaces Engine::dExpandGemm's fp16 path (src/engine.cpp:208-219: k_expand_ptq1_v2 into
  * a 178 MB stage, then Engine::dGemm / k_gemm_f16, shaders/prefill.metal:31-41). */
 int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
@@ -257,8 +267,8 @@ int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp
                               float* out, int H, int F, int M, void* stream);
 size_t kata_ffn_prefill_work_bytes(int H, int F, int M);
 /* The same for T in 1..8 verification tokens (Engine::verifyWide's FFN block,
- * src/engine.cpp:627-629): fp16 token rows through kata_gemv_ptq1_wide (its workspace
- * rules apply).  x, y, xnew, out fp32 [T][H]; work of kata_ffn_verify_work_bytes(H, F, T)
+ * src/engine.cpp:627-629): fp16 token rows through the wide verification GEMV, gate and up
+ * as one kata_gemv_ptq1_wide_batch (its buffer rules apply).  x, y, xnew, out fp32 [T][H]; work of kata_ffn_verify_work_bytes(H, F, T)
  * bytes, 16-byte aligned. */
 int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
                              const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
@@ -280,7 +290,8 @@ size_t kata_ffn_verify_work_bytes(int H, int F, int T);
  * "down"; 2 GDN head order of src, W == 6144, before "ssmout"; 3 src before "wo"), then
  * out = W t (fp32 [M][H]).  src, src2 fp32 [M][W].
  * H, W multiples of 1024; work of kata_dispatch_work_bytes(form, H or W, M) bytes, 16-byte
- * aligned; the prefill and verify forms use the workspace of kata_gemm_ptq1_f16. */
+ * aligned; the prefill form uses the workspace of kata_gemm_ptq1_f16, the verify form the
+ * buffer of kata_gemv_ptq1_wide (its 1..4 input-half matrices in one batched launch). */
 #define KATA_FORM_DECODE 0
 #define KATA_FORM_PREFILL 1
 #define KATA_FORM_VERIFY 2

@@ -63,6 +63,7 @@ SIGNATURES = {
     "kata_gguf_free_device": (I, [P]),
     "kata_gemv_ptq1_wide": (I, [P, P, I, P, I, I, I, P]),
     "kata_gemv_ptq1_wide_noalloc": (I, [P, P, I, P, I, I, I, P]),
+    "kata_gemv_ptq1_wide_batch": (I, [I, P, P, P, P, I, I, I, P]),
     "kata_gemv_ptq1_wide_noalloc_scratch_bytes": (SZ, []),
     "kata_dispatch_create": (P, [P]),
     "kata_dispatch_destroy": (None, [P]),

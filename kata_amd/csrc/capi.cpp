@@ -111,6 +111,26 @@ int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, 
     return check_launch(kata::launch_gemv_wide(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv ptq1 wide");
 }
 
+int kata_gemv_ptq1_wide_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                              int x_dtype, int K, int T, void* stream) {
+    if (count < 1 || count > kata::gemv_max_mats()) return fail(KATA_EINVAL, "count=%d must be 1..%d", count, kata::gemv_max_mats());
+    if (!W || !y || !N || !x) return fail(KATA_EINVAL, "null argument");
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
+    for (int i = 0; i < count; i++) {
+        if (!W[i] || !y[i]) return fail(KATA_EINVAL, "null pointer in W[] or y[]");
+        if (N[i] <= 0) return fail(KATA_EINVAL, "N[%d]=%d must be positive", i, N[i]);
+        if (!aligned(W[i], 4)) return fail(KATA_EINVAL, "W[%d] must be 4-byte aligned", i);
+    }
+    if (T <= 2 && K <= kata::gemv_max_k(T))
+        return check_launch(kata::launch_gemv_ptq1_multi(count, W, y, N, x, x_dtype, KATA_X_ROWS, K, T, (hipStream_t)stream),
+                            "gemv ptq1 wide batch (T <= 2)");
+    return check_launch(kata::launch_gemv_wide_batch(count, W, y, N, x, x_dtype, K, T, (hipStream_t)stream),
+                        "gemv ptq1 wide batch");
+}
+
 int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                                 void* stream) {
     if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
@@ -125,7 +145,7 @@ int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, fl
         return check_launch(kata::launch_gemv_ptq1(W, x, x_dtype, KATA_X_ROWS, y, K, N, T, (hipStream_t)stream),
                             "gemv ptq1 wide no-alloc (T <= 2)");
     if (!kata::gemv_wide_noalloc_fits(K, T))
-        return fail(KATA_EINVAL, "K=%d, T=%d needs more than the %zu-byte no-allocation scratch", K, T,
+        return fail(KATA_EINVAL, "K=%d needs a larger activation image than the %zu-byte no-allocation scratch", K,
                     kata::gemv_wide_noalloc_scratch_bytes());
     return check_launch(kata::launch_gemv_wide_noalloc(W, x, x_dtype, y, K, N, T, (hipStream_t)stream),
                         "gemv ptq1 wide no-alloc");
@@ -497,7 +517,7 @@ int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp
 }
 
 // The sublayer for T <= 8 verification tokens (Engine::verifyWide's FFN, src/engine.cpp:
-// 627-629): fp16 token rows through the wide GEMV.  work: fp16 h [T][H], fp32 g, u [T][F],
+// 627-629): fp16 token rows through the wide GEMV, gate and up in one batched launch.  work: fp16 h [T][H], fp32 g, u [T][F],
 // fp16 t [T][F].
 int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
                              const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
@@ -511,8 +531,10 @@ int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp,
     uint16_t* t = (uint16_t*)(u + (size_t)T * F);
     int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_F16, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, T, stream);
     if (rc) return rc;
-    if ((rc = kata_gemv_ptq1_wide(d->wbase + offGate, h, KATA_F16, g, H, F, T, stream))) return rc;
-    if ((rc = kata_gemv_ptq1_wide(d->wbase + offUp, h, KATA_F16, u, H, F, T, stream))) return rc;
+    const uint8_t* Wgu[2] = {d->wbase + offGate, d->wbase + offUp};
+    float* ygu[2] = {g, u};
+    const int Ngu[2] = {F, F};
+    if ((rc = kata_gemv_ptq1_wide_batch(2, Wgu, ygu, Ngu, h, KATA_F16, H, T, stream))) return rc;
     if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_F16, KATA_X_ROWS, F, T, 1, stream))) return rc;
     return kata_gemv_ptq1_wide(d->wbase + offDown, t, KATA_F16, out, F, H, T, stream);
 }
@@ -592,10 +614,11 @@ int kata_dispatch_in(kata_dispatch* d, int form, int count, const uint64_t* offs
     const int act_dt = form == KATA_FORM_DECODE ? KATA_F32 : KATA_F16;
     int rc = kata_add_rms_fwht(x, y, gs, w.act, act_dt, KATA_X_ROWS, xnew, gamma, hout, hout_dtype, H, M, stream);
     if (rc) return rc;
-    if (form == KATA_FORM_DECODE) {                  // one launch for all matrices that read h
+    if (form != KATA_FORM_PREFILL) {                 // one launch for all matrices that read h
         const uint8_t* Wm[4];
         for (int i = 0; i < count; i++) Wm[i] = d->wbase + offs[i];
-        return kata_gemv_ptq1_batch(count, Wm, outs, N, w.act, KATA_F32, KATA_X_ROWS, H, 1, stream);
+        if (form == KATA_FORM_DECODE) return kata_gemv_ptq1_batch(count, Wm, outs, N, w.act, KATA_F32, KATA_X_ROWS, H, 1, stream);
+        return kata_gemv_ptq1_wide_batch(count, Wm, outs, N, w.act, KATA_F16, H, M, stream);
     }
     bool quantised = false;                          // prefill: quantise h once for its int8 matrices
     for (int i = 0; i < count; i++) {

@@ -593,33 +593,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 
 
 // ---------------------------------------------------------------------------------------
-// Wide verification GEMV: T <= 8 token rows against one read of the weights
-// (shaders/wide.metal:41-99, dispatched by Engine::dWide, src/engine.cpp:542-556).
-//
-// The same integer decode and 16-bit two-limb activation as k_gemv_ptq1, with the MFMA
-// operands laid out for many tokens instead of many blocks: B column x = weight row x of a
-// 16-row tile (lane group g decodes segment g of that row's block, no rotation), A row
-// i = (token i >> 1, limb i & 1) of the same block, so every product of the 16 x 16 result
-// is used: lane x + 16 g ends with the int32 sums of tokens 2g, 2g+1 for row x.
-//
-// Job = (row group of 128 rows, chunk of up to KC blocks): 4 waves, 2 tiles each.  At most
-// 3 workgroups per CU, each on a contiguous range of the chunk-major job list: it builds
-// the 16-replica trit table once, and per job issues all its weight loads (KC x 2 x 8 bytes
-// per lane), quantises the chunk's activation into the LDS image [block][mfma 3][g 4]
-// [A row 16][16 B] (padded) with per (block, token) scales only when the chunk changes,
-// then runs the tiles.
-// With several K chunks each writes fp32 partial sums [chunk][t][n] to a workspace and a
-// second launch adds them in chunk order: deterministic.  (A last-arriver reduction inside
-// the kernel needs a device-scope release per workgroup, an L2 write-back on this chip,
-// which costs far more than the extra launch.)
-constexpr int kWideRows = 128;              // rows per job: 4 waves x 2 tiles x 16
-// A image strides: per lane group 256 B of rows + 16 B, per MFMA 4 groups, per block 3
-// MFMAs.  The pads spread the quantiser's byte stores over the LDS banks (a store
-// instruction of the unpadded layout needs ~15 passes, this one ~1.25); the A reads stay
-// 256 contiguous bytes per 16 lanes.
+// Padded LDS image the wide quantiser scatters into: per lane group 256 B of A rows + 16 B,
+// per MFMA 4 groups, per block 3 MFMAs.  The pads spread the quantiser's byte stores over
+// the LDS banks (a store instruction of the unpadded layout needs ~15 passes, this one
+// ~1.25).  kWideOff[e]: offset of element e's high limb for token 0 in that layout.
 constexpr int kWideG = 272, kWideM = 4 * kWideG;
 constexpr int kWideBlkBytes = 3 * kWideM;
-constexpr int kWideLR = 4;                  // 16 trit-table replicas (16 KB)
 
 struct alignas(16) WideOffTable {
     uint16_t v[128];
@@ -634,57 +613,67 @@ constexpr WideOffTable make_wide_off_table() {
 }
 __constant__ WideOffTable kWideOff = make_wide_off_table();
 
-template <int KC, bool XF16>
-__global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W, const void* __restrict__ x,
-                                                   float* __restrict__ y, float* __restrict__ ws,
-                                                   int K, int N, int ldy, int T, int kcb, int nsplit, int groups) {
-    constexpr int REPS = 1 << kWideLR;
-    __shared__ uint4 lut[lut_bytes(kWideLR) / 16];
-    __shared__ __align__(16) uint8_t img[KC * kWideBlkBytes];
-    __shared__ float2 scl[KC][4];             // [block][token pair]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int xn = lane & 15, g = lane >> 4;
+// Wide verification GEMV for T = 3..8 token rows: the same integer arithmetic as the decode
+// GEMV (16-bit block fixed-point activation in two int8 limbs, exact int32 block sums,
+// fp32 scale and accumulate) with the MFMA operands laid out for tokens: B column = one of
+// 16 weight rows of a tile (lane group g decodes segment g of the row's block, no
+// rotation), A row i = (token i >> 1, limb i & 1) of the same block, so all 16 x 16
+// products are used (3 v_mfma_i32_16x16x64_i8 per 16 rows x 128 weights).
+//
+// Two launches.  k_gemv_vw_prep quantises the T token rows once into the A operand image
+// in device memory: [block][mfma 3][lane group 4][A row 16][16 B] (3072 B per block) and
+// the per (block, token) scales [block][token pair] (float2).  k_gemv_vw: one 512-thread
+// workgroup (8 waves) per CU owns a contiguous range of at most kVwTMax tiles of 16 rows
+// of the concatenated rows of 1..4 matrices that share the tokens (the batch form) and
+// all of K.  Per K chunk of at most kVwCBMax blocks wave w takes blocks [w cb / 8,
+// (w+1) cb / 8) of the chunk: it loads their A operands from the image (L2-resident, read by
+// every workgroup) into registers, issues the weight loads of those blocks for all the
+// workgroup's tiles, then runs the tiles in order, adding into one fp32 accumulator pair
+// per tile.  At the end the 8 waves' accumulators add in a fixed tree
+// order (waves 4..7 into 0..3, 2..3 into 0..1, 1 into 0) through LDS: deterministic, and
+// no K split over workgroups (no partial sums, no reduction launch).
+constexpr int kVwTMax = 9;                       // tiles per workgroup (the switch in k_gemv_vw)
+constexpr int kVwCBMax = 40;                     // blocks per K chunk (the waves' register share)
+constexpr int kVwWaves = 8;
+constexpr int kVwBB = kVwCBMax / kVwWaves;       // blocks of a wave per chunk
+constexpr int kVwLR = 4;                         // 16 trit-table replicas
+constexpr int kVwImgBlk = 3 * 4 * 16 * 16;       // image bytes per block (3072)
+constexpr int kVwPrepBlocks = 8;                 // blocks per prep workgroup
+
+struct VwMats {
+    const uint8_t* W[kMaxMats];
+    float* y[kMaxMats];
+    int N[kMaxMats];
+    int ldy[kMaxMats];
+    int t0[kMaxMats + 1];                        // first tile of matrix i in the concatenation
+    int count;
+};
+
+// Image of kVwPrepBlocks blocks per workgroup: task j = (token, block, 8-element chunk), 16
+// consecutive lanes per (token, block) for the amax; s = amax / 32639, q = rint(x * 32639 /
+// amax) (0 for amax = 0; a block holding NaN or an infinity gets s = NaN), limbs hi = (q +
+// 128) >> 8 at A row 2t and lo = q - 256 hi at row 2t + 1.  The bytes are scattered into a
+// padded LDS copy (strides kWideG: ~1.25 LDS passes per store instruction), then written
+// out unpadded with 16-byte stores.  Rows of tokens >= T and slots without an element are
+// zero, and so are the scales of tokens >= T.
+template <bool XF16>
+__global__ __launch_bounds__(256) void k_gemv_vw_prep(const void* __restrict__ x, int K, int T,
+                                                      uint8_t* __restrict__ img, float2* __restrict__ scl) {
+    __shared__ __align__(16) uint8_t im[kVwPrepBlocks * kWideBlkBytes];
+    const int tid = threadIdx.x;
     const int nb = K >> 7;
-    constexpr int QI = (8 * KC * 16 + 255) / 256;
+    const int blk0 = blockIdx.x * kVwPrepBlocks, cb = min(kVwPrepBlocks, nb - blk0);
+    constexpr int QI = 8 * kVwPrepBlocks * 16 / 256;
     constexpr int XW = XF16 ? 1 : 2;
-    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
-    const __amdgpu_buffer_rsrc_t wrsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
-    // this workgroup's jobs: a contiguous range of the chunk-major job list (job =
-    // kc * groups + rg), so consecutive jobs mostly share the K chunk and its quantised image
-    const int njobs = groups * nsplit;
-    const int j0 = (int)(((long long)blockIdx.x * njobs) / gridDim.x);
-    const int j1 = (int)(((long long)(blockIdx.x + 1) * njobs) / gridDim.x);
-
-    // trit table, once per workgroup (visible after the first job's barriers)
-#pragma unroll
-    for (int i = 0; i < lut_bytes(kWideLR) / 16 / 256; i++) {
-        const int o = tid + i * 256;
-        const uint32_t bv = (uint32_t)o / (REPS / 4);
-        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
-                       m4 = (m3 * 3u) & 0xffu;
-        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
-                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
-        lut[o] = make_uint4(e, e, e, e);
-    }
-    int kc_cur = -1;
-    for (int job = j0; job < j1; job++) {
-    const int kc = job / groups, rg = job - kc * groups;
-    const int b0 = kc * kcb, nblk = min(kcb, nb - b0);
-    const bool newk = kc != kc_cur;
-
-    // (1) for a new K chunk the activation chunks this thread quantises (task j = tid + 256 i
-    // = (token, block, 8-element chunk)), then all weight loads of the job, so both are in
-    // flight together
-    const int ntask = T * nblk * 16;
+    const int ntask = T * cb * 16;
     uint4 xr[QI][XW];
 #pragma unroll
     for (int i = 0; i < QI; i++) {
         const int j = tid + 256 * i;
-        if (newk && j < ntask) {
+        if (j < ntask) {
             const int ch = j & 15, bt = j >> 4;
-            const int t = bt / nblk, b = bt - t * nblk;
-            const size_t k0 = (size_t)t * K + (b0 + b) * 128 + ch * 8;
+            const int t = bt / cb, b = bt - t * cb;
+            const size_t k0 = (size_t)t * K + (size_t)(blk0 + b) * 128 + ch * 8;
             if constexpr (XF16) {
                 xr[i][0] = *(const uint4*)((const _Float16*)x + k0);
             } else {
@@ -693,156 +682,215 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const uint8_t* __restrict__ W
             }
         }
     }
-
-    // all weight loads of the job: row (rg, wave, tile, xn), block b0 + b, segment g
-    const int row0 = rg * kWideRows + wave * 32 + xn;
-    const uint32_t voff = (uint32_t)row0 * row_bytes + (uint32_t)b0 * kBlockBytes + (uint32_t)gemv_seg_byte0(g);
-    uint32_t wl[KC][2], wh[KC][2];
-#pragma unroll
-    for (int b = 0; b < KC; b++)
-#pragma unroll
-        for (int tl = 0; tl < 2; tl++) {
-            const uint32_t so = b < nblk ? (uint32_t)b * kBlockBytes + (uint32_t)tl * 16 * row_bytes : 0x80000000u;
-            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, (int)voff, (int)so, 0));
-            wl[b][tl] = w.x;
-            wh[b][tl] = w.y;
-        }
-
-    if (newk) {
-    // (2) a new chunk: after every wave is done with the previous image, clear it and the
-    // scales, then (3) quantise into it.  LDS-only barriers: the weight loads stay in flight
-    // (a fence would wait for them)
-    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    for (int o = tid; o < KC * kWideBlkBytes / 16; o += 256) ((uint4*)img)[o] = make_uint4(0, 0, 0, 0);
-    if (tid < KC * 4) (&scl[0][0])[tid] = make_float2(0.0f, 0.0f);
-    // LDS-only barrier: the weight loads stay in flight (a fence would wait for them)
-    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-
-    // (3) quantise: task j = (token, block, 8-element chunk), 16 consecutive lanes per
-    // (token, block) for the amax; s = amax / 32639, q = rint(x * 32639 / amax), limbs
-    // hi = (q + 128) >> 8 at A row 2t and lo = q - 256 hi at row 2t + 1
+    for (int o = tid; o < kVwPrepBlocks * kWideBlkBytes / 16; o += 256) ((uint4*)im)[o] = make_uint4(0, 0, 0, 0);
+    if (tid < cb * 4) scl[(size_t)(blk0 + tid / 4) * 4 + tid % 4] = make_float2(0.0f, 0.0f);
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < QI; i++) {
         const int j = tid + 256 * i;
-        if (j < ntask) {                          // whole 16-lane rows drop out together
-            const int ch = j & 15, bt = j >> 4;
-            const int t = bt / nblk, b = bt - t * nblk;
-            float v[8];
-            if constexpr (XF16) {
-                const uint32_t w4[4] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w};
+        if (j >= ntask) continue;                // whole 16-lane rows drop out together
+        const int ch = j & 15, bt = j >> 4;
+        const int t = bt / cb, b = bt - t * cb;
+        float v[8];
+        if constexpr (XF16) {
+            const uint32_t w4[4] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w};
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const v2h h = __builtin_bit_cast(v2h, w4[q]);
-                    v[2 * q] = (float)h[0];
-                    v[2 * q + 1] = (float)h[1];
-                }
-            } else {
-                const uint4 a = xr[i][0], c = xr[i][XW - 1];
-                v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
-                v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
-                v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
+            for (int q = 0; q < 4; q++) {
+                const v2h h = __builtin_bit_cast(v2h, w4[q]);
+                v[2 * q] = (float)h[0];
+                v[2 * q + 1] = (float)h[1];
             }
-            float a = 0.0f;
-            bool bad = false;
+        } else {
+            const uint4 a = xr[i][0], c = xr[i][XW - 1];
+            v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z);
+            v[3] = __uint_as_float(a.w); v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
+            v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
+        }
+        float a = 0.0f;
+        bool bad = false;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float av = fabsf(v[e]);
-                bad |= !(av <= 3.402823466e38f);   // NaN or infinity
-                a = fmaxf(a, av);
-            }
-            a = row16_max(bad ? __builtin_inff() : a);
-            const bool blk_bad = !(a <= 3.402823466e38f);
-            const float inv = (a > 0.0f && !blk_bad) ? kQMax / a : 0.0f;
-            if (ch == 0) {
-                float* sp = &scl[b][t >> 1].x;
-                sp[t & 1] = blk_bad ? __builtin_nanf("") : a * (1.0f / kQMax);
-            }
-            const uint4 ow4 = *(const uint4*)&kWideOff.v[8 * ch];
-            const uint32_t ow[4] = {ow4.x, ow4.y, ow4.z, ow4.w};
-            uint8_t* ib = img + b * kWideBlkBytes + 32 * t;
+        for (int e = 0; e < 8; e++) {
+            const float av = fabsf(v[e]);
+            bad |= !(av <= 3.402823466e38f);   // NaN or infinity
+            a = fmaxf(a, av);
+        }
+        a = row16_max(bad ? __builtin_inff() : a);
+        const bool blk_bad = !(a <= 3.402823466e38f);
+        const float inv = (a > 0.0f && !blk_bad) ? kQMax / a : 0.0f;
+        if (ch == 0) {
+            float* sp = &scl[(size_t)(blk0 + b) * 4 + (t >> 1)].x;
+            sp[t & 1] = blk_bad ? __builtin_nanf("") : a * (1.0f / kQMax);
+        }
+        const uint4 ow4 = *(const uint4*)&kWideOff.v[8 * ch];
+        const uint32_t ow[4] = {ow4.x, ow4.y, ow4.z, ow4.w};
+        uint8_t* ib = im + b * kWideBlkBytes + 32 * t;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int off = (int)((ow[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-                const int q = (int)rintf(v[e] * inv);
-                ib[off] = (uint8_t)((q + 128) >> 8);
-                ib[off + 16] = (uint8_t)q;
-            }
+        for (int e = 0; e < 8; e++) {
+            const int off = (int)((ow[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+            const int q = (int)rintf(v[e] * inv);
+            ib[off] = (uint8_t)((q + 128) >> 8);
+            ib[off + 16] = (uint8_t)q;
         }
     }
-    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    kc_cur = kc;
+    __syncthreads();
+    // unpadded copy out: 16-byte row r of lane group g of MFMA m of block b
+    for (int o = tid; o < cb * 3 * 4 * 16; o += 256) {
+        const int r = o & 15, g = (o >> 4) & 3, mb = o >> 6, m = mb % 3, b = mb / 3;
+        *(uint4*)(img + (size_t)blk0 * kVwImgBlk + o * 16) =
+            *(const uint4*)(im + b * kWideBlkBytes + m * kWideM + g * kWideG + r * 16);
     }
-
-    // (4) tiles: per block the A operand once, then the wave's two tiles
-    const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
-    lds_u8* lb = (lds_u8*)lut;
-    const uint8_t* xa = img + g * kWideG + xn * 16;
-    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
-#pragma unroll
-    for (int b = 0; b < KC; b++) {
-        if (b < nblk) {
-            v4i A[kMfmaPerBlock];
-#pragma unroll
-            for (int m = 0; m < kMfmaPerBlock; m++) A[m] = *(const v4i*)(xa + b * kWideBlkBytes + m * kWideM);
-            const float2 s = scl[b][g];
-#pragma unroll
-            for (int tl = 0; tl < 2; tl++) {
-                const uint32_t w0 = wl[b][tl], w1 = wh[b][tl];
-                v4i B[kMfmaPerBlock];
-                B[0] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 1, laneoff)),
-                           (int)lds_u32(lb, lut_addr<kWideLR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w0, 3, laneoff))};
-                B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 0, laneoff)),
-                           (int)lds_u32(lb, lut_addr<kWideLR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<kWideLR>(w1, 2, laneoff))};
-                B[2] = v4i{(int)lds_u32(lb, lut_addr<kWideLR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
-                v4i D = {0, 0, 0, 0};
-#pragma unroll
-                for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], D, 0, 0, 0);
-                // the row's scale sits in bytes 26..27, read by lane group 0
-                const uint32_t dbits = (uint32_t)__builtin_amdgcn_ds_bpermute(xn * 4, (int)w1) >> 16;
-                const float d = half_bits_to_float(dbits);
-                acc[tl][0] += (float)(D[0] * 256 + D[1]) * (d * s.x);
-                acc[tl][1] += (float)(D[2] * 256 + D[3]) * (d * s.y);
-            }
-        }
-    }
-
-    // (5) results: tokens 2g, 2g + 1 of rows row0 and row0 + 16
-    const int t0 = 2 * g;
-    if (nsplit == 1) {
-#pragma unroll
-        for (int tl = 0; tl < 2; tl++) {
-            const int row = row0 + 16 * tl;
-            if (row < N) {
-                if (t0 < T) y[(size_t)t0 * ldy + row] = acc[tl][0];
-                if (t0 + 1 < T) y[(size_t)(t0 + 1) * ldy + row] = acc[tl][1];
-            }
-        }
-    } else {
-        float* wp = ws + (size_t)kc * T * N;
-#pragma unroll
-        for (int tl = 0; tl < 2; tl++) {
-            const int row = row0 + 16 * tl;
-            if (row < N) {
-                if (t0 < T) wp[(size_t)t0 * N + row] = acc[tl][0];
-                if (t0 + 1 < T) wp[(size_t)(t0 + 1) * N + row] = acc[tl][1];
-            }
-        }
-    }
-    }   // job loop
 }
 
-// y[t][row] = sum of the K chunks' partial sums in chunk order (deterministic)
-__global__ __launch_bounds__(256) void k_gemv_wide_sum(const float* __restrict__ ws, float* __restrict__ y, int N,
-                                                       int ldy, int T, int nsplit) {
-    const int o = (int)blockIdx.x * 256 + (int)threadIdx.x;
-    if (o >= T * N) return;
-    const int t = o / N, row = o - t * N;
-    float sum = 0.0f;
-    for (int c = 0; c < nsplit; c++) sum += ws[(size_t)c * T * N + o];
-    y[(size_t)t * ldy + row] = sum;
+__global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __restrict__ ximg,
+                                                 const float2* __restrict__ xscl, int K, int T, int total_tiles) {
+    constexpr int REPS = 1 << kVwLR;
+    __shared__ uint4 lut[lut_bytes(kVwLR) / 16];
+    __shared__ float2 red[kVwWaves / 2][kVwTMax][64];   // the final tree
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int xn = lane & 15, g = lane >> 4;
+    const int nb = K >> 7;
+    const size_t row_bytes = (size_t)nb * kBlockBytes;
+    const int tw0 = (int)(((long long)blockIdx.x * total_tiles) / gridDim.x);
+    const int Tt = (int)(((long long)(blockIdx.x + 1) * total_tiles) / gridDim.x) - tw0;
+
+    // per tile slot: this lane's row (clamped to the matrix: rows past it read its last row,
+    // whose results are not stored) at its segment of block 0
+    const uint8_t* wp[kVwTMax];
+#pragma unroll
+    for (int t = 0; t < kVwTMax; t++) {
+        const int gt = tw0 + min(t, Tt - 1);
+        int mi = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxMats; i++) mi = (i < P.count && gt >= P.t0[i]) ? i : mi;
+        const int row = min((gt - P.t0[mi]) * 16 + xn, P.N[mi] - 1);
+        wp[t] = P.W[mi] + (size_t)row * row_bytes + gemv_seg_byte0(g);
+    }
+
+    // trit table (visible after the first chunk's barrier)
+#pragma unroll
+    for (int i = 0; i < lut_bytes(kVwLR) / 16 / 512; i++) {
+        const int o = tid + i * 512;
+        const uint32_t bv = (uint32_t)o / (REPS / 4);
+        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
+                       m4 = (m3 * 3u) & 0xffu;
+        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
+                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
+        lut[o] = make_uint4(e, e, e, e);
+    }
+
+    const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
+    lds_u8* lb = (lds_u8*)lut;
+    const uint8_t* xa = ximg + g * 256 + xn * 16;
+    float acc[kVwTMax][2];
+#pragma unroll
+    for (int t = 0; t < kVwTMax; t++) acc[t][0] = acc[t][1] = 0.0f;
+
+    for (int kb0 = 0; kb0 < nb; kb0 += kVwCBMax) {
+        const int cb = min(kVwCBMax, nb - kb0);
+        const int bw0 = (wave * cb) / kVwWaves, nbw = ((wave + 1) * cb) / kVwWaves - bw0;
+        // (1) the A operands and scales of the wave's blocks, straight from the image (in L2:
+        // every workgroup reads it) into registers, issued before the weight loads
+        v4i A[kVwBB][kMfmaPerBlock];
+        float2 sc[kVwBB];
+#pragma unroll
+        for (int bb = 0; bb < kVwBB; bb++) {
+            const int b = kb0 + min(bw0 + bb, cb - 1);
+#pragma unroll
+            for (int m = 0; m < kMfmaPerBlock; m++) A[bb][m] = *(const v4i*)(xa + (size_t)b * kVwImgBlk + m * 1024);
+            sc[bb] = xscl[(size_t)b * 4 + g];
+        }
+        // (3) every weight load of the wave's blocks for all TT tiles first (76 KB per CU for
+        // an FFN matrix: all of it in flight at once), then the tiles in order.  The tile loop
+        // is instantiated for each tile count (a switch on Tt), so it is straight-line code
+        // and each tile waits only for its own loads.  Blocks past the wave's (a ragged
+        // chunk) load a valid dummy address.
+        auto run = [&](auto ttc) {
+            constexpr int TT = decltype(ttc)::value;
+            uint32_t wl[TT][kVwBB], wh[TT][kVwBB];
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int bb = 0; bb < kVwBB; bb++) {
+                    const uint8_t* a = bb < nbw ? wp[t] + (size_t)(kb0 + bw0 + bb) * kBlockBytes : ximg;
+                    uint2 w;
+                    __builtin_memcpy(&w, a, 8);
+                    wl[t][bb] = w.x;
+                    wh[t][bb] = w.y;
+                }
+            static_for<TT>([&](auto tc) {
+                constexpr int t = decltype(tc)::value;
+#pragma unroll
+                for (int bb = 0; bb < kVwBB; bb++) {
+                    if (bb < nbw) {
+                        const uint32_t w0 = wl[t][bb], w1 = wh[t][bb];
+                        v4i B[kMfmaPerBlock];
+                        B[0] = v4i{(int)lds_u32(lb, lut_addr<kVwLR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<kVwLR>(w0, 1, laneoff)),
+                                   (int)lds_u32(lb, lut_addr<kVwLR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<kVwLR>(w0, 3, laneoff))};
+                        B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<kVwLR>(w1, 0, laneoff)),
+                                   (int)lds_u32(lb, lut_addr<kVwLR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<kVwLR>(w1, 2, laneoff))};
+                        B[2] = v4i{(int)lds_u32(lb, lut_addr<kVwLR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
+                        v4i D = {0, 0, 0, 0};
+#pragma unroll
+                        for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[bb][m], B[m], D, 0, 0, 0);
+                        // the row's scale sits in bytes 26..27, read by lane group 0
+                        const uint32_t dbits = (uint32_t)__builtin_amdgcn_ds_bpermute(xn * 4, (int)w1) >> 16;
+                        const float d = half_bits_to_float(dbits);
+                        acc[t][0] += (float)(D[0] * 256 + D[1]) * (d * sc[bb].x);
+                        acc[t][1] += (float)(D[2] * 256 + D[3]) * (d * sc[bb].y);
+                    }
+                }
+            });
+        };
+        switch (Tt) {
+            case 1: run(std::integral_constant<int, 1>{}); break;
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            case 4: run(std::integral_constant<int, 4>{}); break;
+            case 5: run(std::integral_constant<int, 5>{}); break;
+            case 6: run(std::integral_constant<int, 6>{}); break;
+            case 7: run(std::integral_constant<int, 7>{}); break;
+            case 8: run(std::integral_constant<int, 8>{}); break;
+            default: run(std::integral_constant<int, 9>{}); break;
+        }
+    }
+
+    // (3) fixed-order tree over the waves through LDS, then wave 0 stores tokens 2g, 2g + 1
+    // of row xn of each tile
+#pragma unroll
+    for (int step = kVwWaves / 2; step >= 1; step /= 2) {
+        __syncthreads();
+        if (wave >= step && wave < 2 * step) {
+#pragma unroll
+            for (int t = 0; t < kVwTMax; t++) red[wave - step][t][lane] = make_float2(acc[t][0], acc[t][1]);
+        }
+        __syncthreads();
+        if (wave < step) {
+#pragma unroll
+            for (int t = 0; t < kVwTMax; t++) {
+                const float2 o = red[wave][t][lane];
+                acc[t][0] += o.x;
+                acc[t][1] += o.y;
+            }
+        }
+    }
+    if (wave == 0) {
+#pragma unroll
+        for (int t = 0; t < kVwTMax; t++) {
+            if (t < Tt) {
+                const int gt = tw0 + t;
+                int mi = 0;
+#pragma unroll
+                for (int i = 1; i < kMaxMats; i++) mi = (i < P.count && gt >= P.t0[i]) ? i : mi;
+                const int row = (gt - P.t0[mi]) * 16 + xn;
+                if (row < P.N[mi]) {
+                    float* yy = P.y[mi];
+                    if (2 * g < T) yy[(size_t)(2 * g) * P.ldy[mi] + row] = acc[t][0];
+                    if (2 * g + 1 < T) yy[(size_t)(2 * g + 1) * P.ldy[mi] + row] = acc[t][1];
+                }
+            }
+        }
+    }
 }
 
 }  // namespace
@@ -988,93 +1036,71 @@ hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_
     return launch_gemv_ptq1_multi(1, &W, &y, &N, x, x_dtype, x_layout, K, T, s);
 }
 
-hipError_t gemm_device(bool need_ws, hipStream_t s, int* n_cu, float** ws);
+// ---- wide verification GEMV (T = 3..8): k_gemv_vw_prep writes the token rows' A image
+// and scales into `ximg` (nb * kVwImgBytesPerBlock bytes), then one k_gemv_vw launch runs
+// the 1..4 matrices sharing them: about one workgroup per CU (more when a CU would get more
+// than kVwTMax tiles).
+constexpr size_t kVwImgBytesPerBlock = kVwImgBlk + 4 * sizeof(float2);
+size_t gemv_wide_image_bytes(int K) { return (size_t)(K / kGroup) * kVwImgBytesPerBlock; }
 
-// Wide GEMV launches: row groups of 128 rows x K chunks of at most kWideKC blocks; more
-// chunks than needed until there are about two jobs per CU.  With several chunks the
-// partial sums go to the workspace `ws` (ws_floats floats; get_ws() supplies it the first
-// time it is needed); rows beyond what it holds go to further launches.
-constexpr int kWideKC = 11;   // 3 workgroups per CU: LDS 16 KB table + 11 x 3 KB image
-
-// K chunks of a launch over `rows` rows
-static int wide_nsplit(int nb, int rows, int n_cu) {
-    const int groups_all = (rows + kWideRows - 1) / kWideRows;
-    // up to one job per workgroup slot (3 per CU) when the rows allow it, chunks of at least
-    // 6 blocks (smaller jobs cost more in per-job setup than they gain in spread), else the
-    // fewest K chunks
-    const int slots = 3 * n_cu;
-    int nsplit = (nb + kWideKC - 1) / kWideKC;
-    if ((long long)groups_all * nsplit < slots) nsplit = std::max(nsplit, std::min(std::max(1, nb / 6), slots / groups_all));
-    const int kcb = (nb + nsplit - 1) / nsplit;
-    return (nb + kcb - 1) / kcb;
-}
-
-template <typename GetWs>
-static hipError_t wide_launches(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, int n_cu,
-                                GetWs get_ws, size_t ws_floats, hipStream_t s) {
+static hipError_t launch_gemv_vw(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                 int x_dtype, int K, int T, uint8_t* ximg, hipStream_t s) {
+    if (count < 1 || count > kMaxMats || T < 1 || T > 8) return hipErrorInvalidValue;
     const int nb = K / kGroup;
     const size_t row_bytes = (size_t)nb * kBlockBytes;
-    // rows per launch: 32-bit buffer offsets
-    const int max_rows = (int)((((size_t)1 << 31) / row_bytes) / kWideRows * kWideRows);
-    hipError_t e;
-    // one K chunking for the whole call: the result does not depend on how many launches
-    // the workspace size cuts the rows into
-    const int nsplit = wide_nsplit(nb, std::min(N, max_rows), n_cu);
-    const int kcb = (nb + nsplit - 1) / nsplit;
-    for (int n0 = 0; n0 < N;) {
-        int rows = std::min(N - n0, max_rows);
-        float* ws = nullptr;
-        if (nsplit > 1) {
-            if ((e = get_ws(&ws)) != hipSuccess) return e;
-            const size_t fit = ws_floats / ((size_t)nsplit * T) / kWideRows * kWideRows;
-            if (fit == 0) return hipErrorInvalidValue;
-            rows = (int)std::min<size_t>((size_t)rows, fit);
-        }
-        const int groups = (rows + kWideRows - 1) / kWideRows;
-        // persistent workgroups, at most 3 per CU, each on a contiguous range of the jobs
-        const int grid = std::min(groups * nsplit, 3 * n_cu);
-        if (x_dtype == 1)
-            hipLaunchKernelGGL((k_gemv_wide<kWideKC, true>), dim3(grid), dim3(256), 0, s,
-                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit, groups);
-        else
-            hipLaunchKernelGGL((k_gemv_wide<kWideKC, false>), dim3(grid), dim3(256), 0, s,
-                               W + (size_t)n0 * row_bytes, x, y + n0, ws, K, rows, N, T, kcb, nsplit, groups);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        if (nsplit > 1) {
-            hipLaunchKernelGGL(k_gemv_wide_sum, dim3((T * rows + 255) / 256), dim3(256), 0, s, ws, y + n0, rows, N, T,
-                               nsplit);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
-        n0 += rows;
+    VwMats P{};
+    P.count = count;
+    long long total = 0;
+    for (int i = 0; i < count; i++) {
+        P.W[i] = W[i];
+        P.y[i] = y[i];
+        P.N[i] = N[i];
+        P.ldy[i] = N[i];
+        P.t0[i] = (int)total;
+        total += (N[i] + 15) / 16;
+        if ((size_t)N[i] * row_bytes / row_bytes != (size_t)N[i]) return hipErrorInvalidValue;
     }
-    return hipSuccess;
+    for (int i = count; i <= kMaxMats; i++) P.t0[i] = (int)total;
+    if (total > 0x3fffffffLL) return hipErrorInvalidValue;
+    float2* xscl = (float2*)(ximg + (size_t)nb * kVwImgBlk);
+    const dim3 pgrid((nb + kVwPrepBlocks - 1) / kVwPrepBlocks);
+    if (x_dtype == 1)
+        hipLaunchKernelGGL(k_gemv_vw_prep<true>, pgrid, dim3(256), 0, s, x, K, T, ximg, xscl);
+    else
+        hipLaunchKernelGGL(k_gemv_vw_prep<false>, pgrid, dim3(256), 0, s, x, K, T, ximg, xscl);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int n_cu = device_cus();
+    const long long grid = std::min<long long>(total, std::max<long long>(n_cu, (total + kVwTMax - 1) / kVwTMax));
+    hipLaunchKernelGGL(k_gemv_vw, dim3((unsigned)grid), dim3(512), 0, s, P, ximg, xscl, K, T, (int)total);
+    return hipGetLastError();
 }
 
-// The library-owned per-device workspace of the prefill GEMM (allocated on first use).
+// the image in the calling stream's buffer (allocated on the stream's first wide call)
+hipError_t launch_gemv_wide_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                  int x_dtype, int K, int T, hipStream_t s) {
+    void* img = nullptr;
+    hipError_t e = stream_buffer(kBufWideImage, gemv_wide_image_bytes(K), s, &img);
+    if (e != hipSuccess) return e;
+    return launch_gemv_vw(count, W, y, N, x, x_dtype, K, T, (uint8_t*)img, s);
+}
+
 hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                             hipStream_t s) {
-    int n_cu = 0;
-    float* ws = nullptr;
-    hipError_t e = gemm_device(false, s, &n_cu, &ws);
-    if (e != hipSuccess) return e;
-    auto get_ws = [&](float** p) {
-        int n = 0;
-        return gemm_device(true, s, &n, p);
-    };
-    return wide_launches(W, x, x_dtype, y, K, N, T, n_cu, get_ws, (size_t)n_cu * 256 * 128, s);
+    return launch_gemv_wide_batch(1, &W, &y, &N, x, x_dtype, K, T, s);
 }
 
-// ---- the no-allocation form: partial sums in a fixed device array.  `scratch` is a
-// host-side stand-in for the array, never a device address: the address each device holds
-// its copy at comes from hipGetSymbolAddress once per device (with that device current) and
-// only that address is handed to kernels.  Calls that overlap on one device share the array
-// and race; nothing needs clearing (every partial sum is written before it is read).
-constexpr size_t kNoAllocFloats = (size_t)1 << 20;   // 4 MiB per device
-static __device__ __align__(256) float scratch[kNoAllocFloats];
+// ---- the no-allocation form: the image in a fixed device array.  `scratch` is a host-side
+// stand-in for the array, never a device address: the address each device holds its copy at
+// comes from hipGetSymbolAddress once per device (with that device current) and only that
+// address is handed to kernels.  Calls that overlap on one device share the array and race;
+// nothing needs clearing (the prep kernel writes every byte the main kernel reads).
+constexpr size_t kNoAllocBytes = (size_t)4 << 20;   // 4 MiB per device
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
-static hipError_t noalloc_scratch(float** p) {
+static hipError_t noalloc_scratch(uint8_t** p) {
     static std::mutex mu;
-    static float* addr[64] = {};
+    static uint8_t* addr[64] = {};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -1083,30 +1109,25 @@ static hipError_t noalloc_scratch(float** p) {
     if (!addr[dev]) {
         void* a = nullptr;
         if ((e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch))) != hipSuccess) return e;
-        addr[dev] = (float*)a;
+        addr[dev] = (uint8_t*)a;
     }
     *p = addr[dev];
     return hipSuccess;
 }
 
-size_t gemv_wide_noalloc_scratch_bytes() { return kNoAllocFloats * sizeof(float); }
+size_t gemv_wide_noalloc_scratch_bytes() { return kNoAllocBytes; }
 
-// true if one row group of a K x (any N) problem with T tokens fits the scratch
 bool gemv_wide_noalloc_fits(int K, int T) {
-    const int nsplit = wide_nsplit(K / kGroup, kWideRows, device_cus());
-    return nsplit == 1 || (size_t)nsplit * T * kWideRows <= kNoAllocFloats;
+    (void)T;
+    return gemv_wide_image_bytes(K) <= kNoAllocBytes;
 }
 
 hipError_t launch_gemv_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                                     hipStream_t s) {
-    float* ws = nullptr;
-    hipError_t e = noalloc_scratch(&ws);
+    uint8_t* img = nullptr;
+    hipError_t e = noalloc_scratch(&img);
     if (e != hipSuccess) return e;
-    auto get_ws = [&](float** p) {
-        *p = ws;
-        return hipSuccess;
-    };
-    return wide_launches(W, x, x_dtype, y, K, N, T, device_cus(), get_ws, kNoAllocFloats, s);
+    return launch_gemv_vw(1, &W, &y, &N, x, x_dtype, K, T, img, s);
 }
 
 int gemv_max_mats() { return kMaxMats; }

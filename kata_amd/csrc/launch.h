@@ -9,7 +9,7 @@ namespace kata {
 
 // ---- scratch memory (workspace.cpp): the calling thread's device's CU count, and a device
 // buffer of at least `bytes` for (device, kind, stream), allocated on first use and kept
-enum { kBufGemmPieces = 0, kBufArgmax = 1 };
+enum { kBufGemmPieces = 0, kBufArgmax = 1, kBufWideImage = 2 };
 hipError_t device_cu_count(int* n_cu);
 hipError_t stream_buffer(int kind, size_t bytes, hipStream_t s, void** p);
 
@@ -23,10 +23,13 @@ int gemv_max_mats();     // most matrices one launch takes
 // wide verification GEMV, T in 1..8 token rows x [T][K] (fp16 or fp32), y [T][N]
 hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                             hipStream_t s);
-// the same with its partial sums in a fixed per-device device array (no allocation)
+// the same with its activation image in a fixed per-device device array (no allocation)
 hipError_t launch_gemv_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                                     hipStream_t s);
 bool gemv_wide_noalloc_fits(int K, int T);
+// the same for 1..4 matrices sharing the token rows, one launch after the activation prep
+hipError_t launch_gemv_wide_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                  int x_dtype, int K, int T, hipStream_t s);
 size_t gemv_wide_noalloc_scratch_bytes();
 
 // ---- Q8_0 GEMV (gemv_q8.hip)

@@ -101,6 +101,26 @@ def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.
     return y
 
 
+def gemv_ptq1_wide_batch(Ws, x: torch.Tensor, K: int, Ns, outs=None):
+    """Wide verification GEMVs of up to 4 matrices sharing the token rows x [T][K] (fp16 or
+    fp32, T = x.shape[0] in 1..8), one launch: returns [y_i], y_i [T][N_i] fp32."""
+    T = x.shape[0]
+    if len(Ws) != len(Ns) or (outs is not None and len(outs) != len(Ns)):
+        raise ValueError("Ws, Ns (and outs) must have the same length")
+    for i, (W, N) in enumerate(zip(Ws, Ns)):
+        _need_bytes(f"Ws[{i}]", W, _ptq1_bytes(K, N))
+        _need_bytes(f"outs[{i}]", outs[i] if outs is not None else None, T * N * 4)
+    _need_bytes("x", x, T * K * x.element_size())
+    _need_gpu(x, *Ws)
+    n = len(Ws)
+    ys = outs if outs is not None else [torch.empty((T, N), dtype=torch.float32, device=x.device) for N in Ns]
+    Wa = (ctypes.c_void_p * n)(*[W.data_ptr() for W in Ws])
+    ya = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    Na = (ctypes.c_int * n)(*Ns)
+    check(lib().kata_gemv_ptq1_wide_batch(n, Wa, ya, Na, _ptr(x), _xdtype(x), K, T, _stream(x)))
+    return ys
+
+
 def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
             out: torch.Tensor | None = None) -> torch.Tensor:
     if K <= 0 or K % Q8_GROUP or N <= 0:

@@ -209,6 +209,29 @@ def test_gemv_wide_rejects():
     assert lib.kata_gemv_ptq1_wide(None, p, 1, p, 1024, 16, 4, None) == KATA_EINVAL
 
 
+def test_gemv_wide_batch_rejects():
+    lib = L.lib()
+    p = FAKE
+
+    def arr(ctype, vals):
+        return (ctype * len(vals))(*vals)
+
+    W2 = arr(ctypes.c_void_p, [FAKE.value, FAKE.value])
+    y2 = arr(ctypes.c_void_p, [FAKE.value, FAKE.value])
+    N2 = arr(ctypes.c_int, [16, 32])
+    call = lib.kata_gemv_ptq1_wide_batch
+    assert call(0, W2, y2, N2, p, 1, 1024, 4, None) == KATA_EINVAL            # count
+    assert call(5, W2, y2, N2, p, 1, 1024, 4, None) == KATA_EINVAL
+    assert call(2, W2, y2, N2, p, 1, 1024, 9, None) == KATA_EINVAL            # T
+    assert call(2, W2, y2, N2, p, 1, 1000, 4, None) == KATA_EINVAL            # K % 128
+    assert call(2, W2, y2, N2, p, 7, 1024, 4, None) == KATA_EINVAL            # x dtype
+    assert call(2, W2, y2, N2, ctypes.c_void_p(0x10008), 1, 1024, 4, None) == KATA_EINVAL
+    assert call(2, None, y2, N2, p, 1, 1024, 4, None) == KATA_EINVAL
+    assert call(2, W2, y2, arr(ctypes.c_int, [16, 0]), p, 1, 1024, 4, None) == KATA_EINVAL
+    assert call(2, arr(ctypes.c_void_p, [FAKE.value, 0x10002]), y2, N2, p, 1, 1024, 4, None) == KATA_EINVAL
+    assert call(2, W2, arr(ctypes.c_void_p, [FAKE.value, None]), N2, p, 1, 1024, 4, None) == KATA_EINVAL
+
+
 def test_fwht_rejects_aliasing():
     """An output overlapping an input is rejected before any launch (workgroups re-read their
     row while others write theirs); no GPU is needed for the argument checks."""

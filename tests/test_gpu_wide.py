@@ -4,8 +4,9 @@ src/engine.cpp:542-556; shaders/wide.metal:41-99) against the CPU oracle.
 Contract: relative L2 error <= 1e-3 per output vector; the kernel's only approximation is
 the 16-bit block-fixed-point activation, so the tests hold it to 2e-4.  Token rows are
 independent: row t of a T-row call (T >= 3) equals the same token in any other such call
-bit for bit (the K split, the per-(block, token) quantisation and the summation order do
-not depend on T); T = 1, 2 run the decode GEMV."""
+bit for bit (the per-(block, token) quantisation and the summation order do not depend on
+T); T = 1, 2 run the decode GEMV.  The batch form (1..4 matrices sharing the rows, one
+launch) equals single calls bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -87,8 +88,8 @@ def test_wide_full_shapes_t8(dev, K, N):
     assert rel_l2(y.cpu().numpy()[:, rows], ref_o).max() < TIGHT
 
 
-def test_wide_many_rows_workspace_chunks(dev):
-    """More rows than the K-split workspace holds at once (further launches by row chunk)."""
+def test_wide_many_rows(dev):
+    """600 000 rows (many workgroups per CU, each with its full tile count)."""
     K, N, T = 1664, 600000, 8
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
@@ -105,3 +106,41 @@ def test_wide_many_rows_workspace_chunks(dev):
     sub = W[torch.from_numpy(rows).to(dev)].cpu().numpy()
     ref = orc.gemv_ptq1(np.ascontiguousarray(sub), x_np.astype(np.float32), K, len(rows), T)
     assert rel_l2(y[:, rows], ref).max() < TIGHT
+
+
+@pytest.mark.parametrize("K,Ns,T,dtype", [
+    (5120, (17408, 17408), 8, np.float16),         # verifyWide's gate + up
+    (5120, (10240, 6144), 5, np.float16),          # GDN qkv + z
+    (5120, (12288, 1024, 1024), 3, np.float32),    # GQA q + k + v
+    (1024, (37, 300, 5, 129), 8, np.float16),      # four ragged matrices, tiles across boundaries
+    (6144, (5120, 5120), 2, np.float16),           # T = 2: the decode GEMV's batch form
+])
+def test_wide_batch_equals_single_calls(dev, K, Ns, T, dtype):
+    """One batched launch equals the per-matrix calls bit for bit, and the oracle on sampled
+    rows of every matrix."""
+    Ws_np = [orc.synth_ptq1(N, K, K + N + i)[0] for i, N in enumerate(Ns)]
+    x_np = orc.synth_x(T, K, K + T, dtype)
+    Ws = [torch.from_numpy(w).to(dev) for w in Ws_np]
+    x = torch.from_numpy(x_np).to(dev)
+    ys = ops.gemv_ptq1_wide_batch(Ws, x, K, list(Ns))
+    for W_np, W, N, y in zip(Ws_np, Ws, Ns, ys):
+        assert torch.equal(y, ops.gemv_ptq1_wide(W, x, K, N)), N
+        rows = np.unique(np.concatenate([np.arange(0, N, max(1, N // 53)), [N - 1]]))
+        ref = orc.gemv_ptq1(np.ascontiguousarray(W_np[rows]), x_np.astype(np.float32), K, len(rows), T)
+        assert rel_l2(y.cpu().numpy()[:, rows], ref).max() < TIGHT, N
+
+
+def test_wide_nonfinite_tokens(dev):
+    """A NaN or an infinity in a token's block makes that token's outputs NaN (as the
+    reference's fp32 sum does) and leaves the other tokens exact."""
+    K, N, T = 2048, 300, 4
+    W_np, _, _ = orc.synth_ptq1(N, K, 11)
+    x_np = orc.synth_x(T, K, 12)
+    x_np[1, 200] = np.nan
+    x_np[3, 1500] = np.inf
+    W = torch.from_numpy(W_np).to(dev)
+    y = ops.gemv_ptq1_wide(W, torch.from_numpy(x_np).to(dev), K, N).cpu().numpy()
+    assert np.isnan(y[1]).all() and np.isnan(y[3]).all()
+    ok = [0, 2]
+    ref = orc.gemv_ptq1(W_np, x_np[ok].astype(np.float32), K, N, 2)
+    assert rel_l2(y[ok], ref).max() < TIGHT
