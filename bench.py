@@ -14,8 +14,8 @@ synthetic PTQ1_0 (trits iid on {-1,0,1}, fp16 scales |N(0,0.02)|), activations f
 N(0,1).  Steps rotate over enough distinct weight copies (>= 512 MB) that no matrix is
 served from the 256 MB Infinity Cache.  `value` = packed weight bytes of all GEMVs of the
 timed steps / wall time of those steps (events on the launch stream), in GB/s; a step's 6
-launches are issued from Python (--graph replays a HIP graph of them instead, which measures
-slower here: a graph launch costs more than the host's lead over the GPU).
+launches are captured as HIP graphs, one per timed batch of steps, and replayed (--launch host
+issues every GEMV from Python instead; both figures are in the JSON line).
 
 Also reported (same JSON line):
   roofline     dominant kernel k_gemv_ptq1<1>: algorithmic bytes per launch (the packed
@@ -287,6 +287,38 @@ def graph_time(torch, fn, nrep, stream, cap_stream):
     return a.elapsed_time(b) * 1e3 / nrep
 
 
+def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
+    """The wide verification GEMV (Engine::dWide) at T = 4 and 8 token rows on the FFN and
+    attention shapes (one weight read for all rows), and verifyWide's gate + up batched."""
+    # wide verification GEMV (Engine::dWide): T = 4 and 8 token rows, one weight read
+    verify_wide = {}
+    for j, (name, K, N, grp) in enumerate(SWEEP):
+        if name not in ("gdn_qkv", "attn_q", "attn_o", "ffn_gate", "ffn_down"):
+            continue
+        ent = {"K": K, "N": N}
+        for T in (4, 8):
+            xw = torch.from_numpy(np.random.default_rng(SEED + 350 + j).standard_normal((T, K))
+                                  .astype(np.float16)).to(dev)
+            yw = torch.empty((T, N), dtype=torch.float32, device=dev)
+            us = time_reps(lambda r: ops.gemv_ptq1_wide(copies[r % ncopies][j], xw, K, N, out=yw), reps)
+            ent[f"t{T}_us"] = round(us, 3)
+            ent[f"t{T}_GBps"] = round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
+        verify_wide[name] = ent
+    # verifyWide's gate + up in one batched launch (one quantisation of the token rows)
+    jg, ju = [i for i, e in enumerate(SWEEP) if e[0] in ("ffn_gate", "ffn_up")]
+    K, N = SWEEP[jg][1], SWEEP[jg][2]
+    ent = {"K": K, "N": 2 * N}
+    for T in (4, 8):
+        xw = torch.from_numpy(np.random.default_rng(SEED + 360).standard_normal((T, K)).astype(np.float16)).to(dev)
+        ygu = [torch.empty((T, N), dtype=torch.float32, device=dev) for _ in range(2)]
+        us = time_reps(lambda r: ops.gemv_ptq1_wide_batch([copies[r % ncopies][jg], copies[r % ncopies][ju]], xw, K,
+                                                          [N, N], outs=ygu), reps)
+        ent[f"t{T}_us"] = round(us, 3)
+        ent[f"t{T}_GBps"] = round(2 * packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
+    verify_wide["ffn_gate_up_batched"] = ent
+    return verify_wide
+
+
 def run_calibration(torch, ops, dev, stream, cap_stream, reps):
     """The launch floor of an empty kernel at the decode GEMV's geometry and a plain streaming
     read at the sweep's sizes (same protocol as per_matrix), over rotating buffers (>= 512 MB
@@ -314,14 +346,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
-    ap.add_argument("--graph", action="store_true",
-                    help="replay each step's HIP graph instead of launching its GEMVs from Python")
+    ap.add_argument("--launch", choices=("graph", "host"), default="graph",
+                    help="graph: each timed batch of steps is captured once as one HIP graph and replayed "
+                         "(how a serving loop drives the decode step); host: every GEMV launched from Python")
     ap.add_argument("--no-config5", action="store_true", help="skip the 64-layer sweep and the M=7300 GEMMs")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN sublayer figures")
     ap.add_argument("--calib-only", action="store_true",
                     help="only the calibration kernels (launch floor, plain read), then print them and exit")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the pp512 prefill GEMMs (for counter runs), then exit")
+    ap.add_argument("--wide-only", action="store_true",
+                    help="only the wide verification GEMV figures (for profiler runs), then exit")
     ap.add_argument("--step-only", action="store_true",
                     help="only the timed decode-sweep steps (for counter runs), then print value and exit")
     ap.add_argument("--reps", type=int, default=200, help="repeats per matrix for the per-matrix tables")
@@ -370,6 +405,11 @@ def main():
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": run_gemm(torch, ops, dev, stream, copies, ncopies)}))
         return
+    if args.wide_only:
+        cs = torch.cuda.Stream(dev)
+        print(json.dumps({"verify_wide": run_verify_wide(torch, ops, dev, copies, ncopies,
+                                                         lambda fn, n: graph_time(torch, fn, n, stream, cs), args.reps)}))
+        return
 
     groups = {}
     for j, (name, K, N, grp) in enumerate(SWEEP):
@@ -387,49 +427,50 @@ def main():
         for j, (name, K, N, grp) in enumerate(SWEEP):
             ops.gemv_ptq1(ws[j], xs[grp], K, N, 1, out=ys[j])
 
-    # One HIP graph per (function, weight copy): replaying graph i % ncopies is step i, so
-    # exactly K steps are timed, each with the per-launch overhead of a graph launch.
-    use_graph = args.graph
+    # The timed steps run either as captured HIP graphs (default: a batch of consecutive steps
+    # per graph, step i on weight copy i % ncopies, captured before the timed region and
+    # replayed inside it) or as host launches from Python, one call per GEMV launch.
     cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
-    runners = {}
-    for fname, fn in (("step", step),) if args.step_only else (("step", step), ("single", step_single)):
+    fns = {"step": step} if args.step_only else {"step": step, "single": step_single}
+    for fn in fns.values():
         for i in range(2):
             fn(i)                                 # first calls set kernel attributes
-        torch.cuda.synchronize()
-        if use_graph:
-            graphs = []
-            for i in range(ncopies):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, stream=cap_stream):
-                    fn(i)
-                graphs.append(g)
-            runners[fname] = lambda i, graphs=graphs: graphs[i % ncopies].replay()
-        else:
-            runners[fname] = fn
+    torch.cuda.synchronize()
 
     batch_ms = []
 
-    def timed(fname, n_steps, nbatch=1):
+    def timed(fname, n_steps, nbatch=1, launch=args.launch):
         """ms of n_steps steps; with nbatch > 1 also events between nbatch equal batches of
         them (batch_ms), for the best / median batch figures."""
-        run = runners[fname]
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(nbatch + 1)]
+        fn = fns[fname]
         cuts = [(b * n_steps) // nbatch for b in range(nbatch + 1)]
+        graphs = []
+        if launch == "graph":
+            for b in range(nbatch):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=cap_stream):
+                    for i in range(cuts[b], cuts[b + 1]):
+                        fn(i)
+                graphs.append(g)
+            for g in graphs:                      # a first replay uploads each graph (untimed)
+                g.replay()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(nbatch + 1)]
         torch.cuda.synchronize()
         ev[0].record(stream)
-        b = 1
-        for i in range(n_steps):
-            run(i)
-            while b <= nbatch and cuts[b] == i + 1:
-                ev[b].record(stream)
-                b += 1
+        for b in range(nbatch):
+            if launch == "graph":
+                graphs[b].replay()
+            else:
+                for i in range(cuts[b], cuts[b + 1]):
+                    fn(i)
+            ev[b + 1].record(stream)
         torch.cuda.synchronize()
         if nbatch > 1:
             batch_ms[:] = [ev[j].elapsed_time(ev[j + 1]) / max(1, cuts[j + 1] - cuts[j]) for j in range(nbatch)]
         return ev[0].elapsed_time(ev[nbatch])
 
     for i in range(args.warmup):
-        runners["step"](i)
+        fns["step"](i)
     torch.cuda.synchronize()
     ms_total = timed("step", args.steps, nbatch=8 if args.steps >= 8 else 1)
     ms_step = ms_total / args.steps
@@ -442,6 +483,8 @@ def main():
     launches = len(group_list)
     gemv_launch_us = ms_total * 1e3 / (args.steps * launches)
     ms_single = timed("single", args.steps)
+    other = "host" if args.launch == "graph" else "graph"
+    ms_other = timed("step", args.steps, launch=other)
     bytes_per_launch = set_bytes / launches
     achieved = bytes_per_launch / (gemv_launch_us * 1e-6) / 1e9
 
@@ -470,32 +513,8 @@ def main():
         us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], x2, K, N, 2, out=y2), args.reps)
         verify_t2[name] = {"K": K, "N": N, "us": round(us, 3),
                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
-    # wide verification GEMV (Engine::dWide): T = 4 and 8 token rows, one weight read
-    verify_wide = {}
-    for j, (name, K, N, grp) in enumerate(SWEEP):
-        if name not in ("gdn_qkv", "attn_q", "attn_o", "ffn_gate", "ffn_down"):
-            continue
-        ent = {"K": K, "N": N}
-        for T in (4, 8):
-            xw = torch.from_numpy(np.random.default_rng(SEED + 350 + j).standard_normal((T, K))
-                                  .astype(np.float16)).to(dev)
-            yw = torch.empty((T, N), dtype=torch.float32, device=dev)
-            us = time_reps(lambda r: ops.gemv_ptq1_wide(copies[r % ncopies][j], xw, K, N, out=yw), args.reps)
-            ent[f"t{T}_us"] = round(us, 3)
-            ent[f"t{T}_GBps"] = round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
-        verify_wide[name] = ent
-    # verifyWide's gate + up in one batched launch (one quantisation of the token rows)
-    jg, ju = [i for i, e in enumerate(SWEEP) if e[0] in ("ffn_gate", "ffn_up")]
-    K, N = SWEEP[jg][1], SWEEP[jg][2]
-    ent = {"K": K, "N": 2 * N}
-    for T in (4, 8):
-        xw = torch.from_numpy(np.random.default_rng(SEED + 360).standard_normal((T, K)).astype(np.float16)).to(dev)
-        ygu = [torch.empty((T, N), dtype=torch.float32, device=dev) for _ in range(2)]
-        us = time_reps(lambda r: ops.gemv_ptq1_wide_batch([copies[r % ncopies][jg], copies[r % ncopies][ju]], xw, K,
-                                                          [N, N], outs=ygu), args.reps)
-        ent[f"t{T}_us"] = round(us, 3)
-        ent[f"t{T}_GBps"] = round(2 * packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
-    verify_wide["ffn_gate_up_batched"] = ent
+    verify_wide = run_verify_wide(torch, ops, dev, copies, ncopies,
+                                  lambda fn, n: graph_time(torch, fn, n, stream, cap_stream), args.reps)
     q8 = {}
     for name, K, N in (("gate", 5120, 17408), ("down", 17408, 5120)):
         nb = N * (K // 32) * 34
@@ -660,7 +679,7 @@ def main():
         "data": "synthetic (seeded trits/scales/activations)",
         "config": {"workload": "BASELINE configs[1]: bs=1 decode GEMV sweep, one layer of each kind "
                                "(10 matrices in 6 launches, matrices sharing an input batched)",
-                   "weight_copies": ncopies, "bytes_per_step": set_bytes},
+                   "weight_copies": ncopies, "bytes_per_step": set_bytes, "launch": args.launch},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_ptq1<1>", "avg_launch_us": round(gemv_launch_us, 3),
@@ -668,6 +687,8 @@ def main():
         "step_batches": ({"n": len(batch_ms), "best_GBps": round(set_bytes / (min(batch_ms) * 1e-3) / 1e9, 1),
                           "median_GBps": round(set_bytes / (float(np.median(batch_ms)) * 1e-3) / 1e9, 1)}
                          if batch_ms else None),
+        f"{other}_launch": {"ms_per_step": round(ms_other / args.steps, 5),
+                            "GBps": round(set_bytes * args.steps / (ms_other * 1e-3) / 1e9, 1)},
         "one_launch_per_matrix": {"ms_per_step": round(ms_single / args.steps, 5),
                                   "GBps": round(set_bytes * args.steps / (ms_single * 1e-3) / 1e9, 1)},
         "per_matrix": per_matrix,
