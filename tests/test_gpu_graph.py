@@ -1,0 +1,79 @@
+"""The GEMVs and the prefill GEMM inside HIP graphs (the bench times its decode steps as graph
+replays; serving loops capture them the same way): a graph of several launches is replayed
+several times with other eager work and synchronisations between the replays, and every
+replay's outputs equal the eager launches' bit for bit.  The first call on the capture
+stream runs eagerly (scratch buffers are per stream and cannot be allocated under capture)."""
+import numpy as np
+import pytest
+import torch
+
+from kata_amd import ops
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _replays_equal_eager(dev, fn, outs, n_replays=4):
+    """fn() launches into `outs` (a list of tensors); eager result vs each replay."""
+    cs = torch.cuda.Stream(dev)
+    with torch.cuda.stream(cs):
+        fn()                                         # first call on this stream: eager
+    torch.cuda.synchronize()
+    ref = [o.clone() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        fn()
+    junk = torch.randn(1 << 20, device=dev)
+    for r in range(n_replays):
+        for o in outs:
+            o.fill_(float("nan"))                    # eager work between the replays
+        junk.mul_(1.0001)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, ref):
+            assert torch.equal(o, e), f"replay {r}"
+
+
+def test_graph_decode_step(dev):
+    """The bench's decode step shape: batched GEMVs sharing an input, then single ones,
+    several weight sets in one graph."""
+    specs = [(5120, (1024, 512)), (6144, (640,)), (5120, (2048, 2048)), (17408, (512,))]
+    Ws, xs, ys = [], [], []
+    for i, (K, Ns) in enumerate(specs):
+        Ws.append([torch.from_numpy(orc.synth_ptq1(N, K, 10 * i + j)[0]).to(dev) for j, N in enumerate(Ns)])
+        xs.append(torch.from_numpy(orc.synth_x(1, K, i)).to(dev))
+        ys.append([torch.empty((1, N), device=dev) for N in Ns])
+
+    def step():
+        for (K, Ns), W, x, y in zip(specs, Ws, xs, ys):
+            ops.gemv_ptq1_batch(W, x, K, list(Ns), 1, outs=y)
+
+    _replays_equal_eager(dev, step, [t for y in ys for t in y])
+
+
+def test_graph_wide_batch_and_t2(dev):
+    """The wide verification GEMV (prep + main launch, the stream's image buffer) and the
+    T = 2 verify GEMV in one graph."""
+    K, Ns = 5120, (3000, 1700)
+    Ws = [torch.from_numpy(orc.synth_ptq1(N, K, 40 + j)[0]).to(dev) for j, N in enumerate(Ns)]
+    x8 = torch.from_numpy(orc.synth_x(8, K, 41)).to(dev)
+    x2 = torch.from_numpy(orc.synth_x(2, K, 42)).to(dev)
+    y8 = [torch.empty((8, N), device=dev) for N in Ns]
+    y2 = torch.empty((2, Ns[0]), device=dev)
+
+    def calls():
+        ops.gemv_ptq1_wide_batch(Ws, x8, K, list(Ns), outs=y8)
+        ops.gemv_ptq1(Ws[0], x2, K, Ns[0], 2, out=y2)
+
+    _replays_equal_eager(dev, calls, y8 + [y2])
+
+
+def test_graph_prefill_gemm_with_pieces(dev):
+    """The fp16 prefill GEMM whose last tile round is split into K pieces (the stream's
+    workspace and the piece-sum launch) inside a graph."""
+    M, K, N = 300, 2048, 4000
+    W = torch.from_numpy(orc.synth_ptq1(N, K, 50)[0]).to(dev)
+    A = torch.from_numpy(orc.synth_x(M, K, 51)).to(dev)
+    C = torch.empty((M, N), dtype=torch.float16, device=dev)
+    _replays_equal_eager(dev, lambda: ops.gemm_ptq1_f16(A, W, K, N, out=C), [C])
