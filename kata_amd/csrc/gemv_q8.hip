@@ -3,7 +3,10 @@
 // Semantics (shaders/mtp.metal:5-20): y[t][n] = sum_b d[n,b] * (sum_i q[n,b,i] * x[t][32b+i]),
 // per block the int8 x activation dot in fp32, then acc += d * s.
 //
-// Design: HBM-bound (1.0625 bytes per weight); plain VALU fp32 FMAs keep up.  A lane owns
+// Design: HBM-bound (1.0625 bytes per weight).  One fp16 activation row: each pair of quants
+// becomes an exact fp16 pair (a byte permute and a packed add) and v_dot2_f32_f16 multiplies
+// it with the activation pair, accumulating in fp32 (27.4 -> 26.4 us at 17408 x 5120; for two
+// rows this form was slower, 28.8 -> 35.5 us); otherwise fp32 FMAs per quant.  A lane owns
 // whole 34-byte blocks and consecutive lanes own consecutive blocks of a row, so each load
 // instruction of a wave covers 2176 contiguous bytes.  A block is read from its
 // dword-aligned start as two 16-byte loads, one dword and one 16-bit load (blocks sit at
@@ -100,17 +103,61 @@ __global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t* __restrict__ W, 
             s[r][7] = __builtin_amdgcn_alignbyte(w8, w[7], sh);
             s[r][8] = h16;
         }
-        float xv[T][32];
-        load_x32<T, XH>(x, K, b, xv);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            d[r] = half_bits_to_float(s[r][0] & 0xffffu);
+        if constexpr (XH && T == 1) {
+            // fp16 activations: pairs of quants as exact fp16 pairs and v_dot2_f32_f16 (the
+            // fp16 products are exact in fp32).  Pair m = (q 2m, q 2m+1) sits in bytes 2, 3 of
+            // s[0] (m = 0), bytes 0, 1 / 2, 3 of s[i] (m = 2i-1 / 2i) and bytes 0, 1 of s[8]
+            // (m = 15).  A byte u = q ^ 0x80 under a 0x64 high byte is the fp16 1152 + q.
+            uint32_t xp[T][16];
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                float sum = 0.0f;
+                const uint4* p = (const uint4*)((const _Float16*)x + (size_t)t * K + (size_t)b * 32);
 #pragma unroll
-                for (int k = 0; k < 32; k++) sum += byte_s8(s[r][(k + 2) >> 2], (k + 2) & 3) * xv[t][k];
-                acc[t][r] += d[r] * sum;
+                for (int c = 0; c < 4; c++) {
+                    const uint4 u = p[c];
+                    xp[t][4 * c] = u.x;
+                    xp[t][4 * c + 1] = u.y;
+                    xp[t][4 * c + 2] = u.z;
+                    xp[t][4 * c + 3] = u.w;
+                }
+            }
+            const v2h off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+            auto pair = [&](uint32_t w, bool hi) {
+                const uint32_t v = __builtin_amdgcn_perm(0x64646464u, w ^ 0x80808080u, hi ? 0x04030402u : 0x04010400u);
+                return __builtin_bit_cast(v2h, v) + off;
+            };
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                d[r] = half_bits_to_float(s[r][0] & 0xffffu);
+                v2h qp[16];
+                qp[0] = pair(s[r][0], true);
+#pragma unroll
+                for (int i = 1; i < 8; i++) {
+                    qp[2 * i - 1] = pair(s[r][i], false);
+                    qp[2 * i] = pair(s[r][i], true);
+                }
+                qp[15] = pair(s[r][8], false);
+#pragma unroll
+                for (int t = 0; t < T; t++) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int m = 0; m < 16; m++) sum = __builtin_amdgcn_fdot2(qp[m], __builtin_bit_cast(v2h, xp[t][m]), sum, false);
+                    acc[t][r] += d[r] * sum;
+                }
+            }
+        } else {
+            float xv[T][32];
+            load_x32<T, XH>(x, K, b, xv);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                d[r] = half_bits_to_float(s[r][0] & 0xffffu);
+#pragma unroll
+                for (int t = 0; t < T; t++) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 32; k++) sum += byte_s8(s[r][(k + 2) >> 2], (k + 2) & 3) * xv[t][k];
+                    acc[t][r] += d[r] * sum;
+                }
             }
         }
     }
