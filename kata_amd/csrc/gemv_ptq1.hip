@@ -636,7 +636,7 @@ constexpr int kVwTMax = 9;                       // tiles per workgroup (the swi
 constexpr int kVwCBMax = 40;                     // blocks per K chunk (the waves' register share)
 constexpr int kVwWaves = 8;
 constexpr int kVwBB = kVwCBMax / kVwWaves;       // blocks of a wave per chunk
-constexpr int kVwLR = 4;                         // 16 trit-table replicas
+constexpr int kVwLR = 6;                         // 64 trit-table replicas (conflict-free lookups)
 constexpr int kVwImgBlk = 3 * 4 * 16 * 16;       // image bytes per block (3072)
 constexpr int kVwPrepBlocks = 8;                 // blocks per prep workgroup
 
