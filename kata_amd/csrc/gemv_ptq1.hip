@@ -291,7 +291,7 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
 // Dynamic LDS: A image (384*T B per virtual block, quarters 64 B apart), (scale, 0)
 // pairs [vb][t], the scatter offsets (1 KB), a scratch slot for the off-diagonal lanes
 // (512 B), then item sums [S][T][16] floats, which with XS first hold the raw activation.
-template <int T, int LR, int D, bool PAD, bool XS, bool MULTI>
+template <int T, int LR, int D, bool PAD, bool XS, bool MULTI, bool STRIDE>
 __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __restrict__ x, int x_dtype, int x_layout,
                                                     int K, int nq) {
 #pragma clang fp contract(off)
@@ -345,7 +345,15 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const int Tt = min(tiles, wt0 + tpw) - wt0;
     const int S = nq * Tt;                       // nq is even: whole pairs of block steps
     const int s0 = ((wave * S) / kWaves) & ~1, s1 = wave == kWaves - 1 ? S : (((wave + 1) * S) / kWaves) & ~1;
-    const int n = s1 - s0;                       // this wave's run length (even, wave-uniform)
+    // STRIDE (chosen for long tile ranges with few step pairs per row): tile-strided order,
+    // wave w takes pair w % np for tiles h, h + G, h + 2G, ... (h = w / np, G = 16 / np
+    // phases), so at any time the waves read neighbouring pieces of the same few tiles; the
+    // waves past G np stay idle.  Same items and slots as the run order: the same results.
+    const int np = nq >> 1, G = kWaves / np;
+    const bool strided = STRIDE && Tt >= 2 * G;
+    const int sp = strided ? wave % np : 0, sh = strided ? wave / np : 0;
+    const int n = !strided ? s1 - s0                     // this wave's run length (even, wave-uniform)
+                           : (wave < G * np && sh < Tt ? 2 * ((Tt - sh + G - 1) / G) : 0);
     const int qbytes = nq * BLK;                 // A image bytes per quarter
     uint8_t* As = smem;
     uint8_t* Ss = smem + gemv_a_lds_bytes(qbytes, T);            // (scale, 0) pairs [vb][t]
@@ -404,11 +412,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const uint32_t voff = (uint32_t)r * row_bytes + (uint32_t)kq * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
     // item s = (c/2, tile, c%2): pair index s / (2 Tt), tile (s % (2 Tt)) / 2, block step
     // parity s % 2; runs start at even s, so the ring slot's parity is the item's
-    int lt = (s0 % (2 * Tt)) >> 1;               // load cursor: tile, item offset, items left
-    uint32_t lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(2 * (s0 / (2 * Tt))) * 4 * kBlockBytes;
+    int lt = strided ? sh : (s0 % (2 * Tt)) >> 1;   // load cursor: tile, item offset, items left
+    uint32_t lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(2 * (strided ? sp : s0 / (2 * Tt))) * 4 * kBlockBytes;
     int lrem = n;
+    const int Tw = strided ? 0x7fffffff : Tt;    // the pair changes after tile Tw - 1 (strided: never)
     const uint32_t cstep = 4 * kBlockBytes;      // even c -> c + 1, same tile
-    const uint32_t tnext = tstep - cstep;        // odd c -> c - 1, next tile
+    const uint32_t tnext = (strided ? G : 1) * tstep - cstep;    // odd c -> c - 1, next tile
     const uint32_t cwrap = cstep - (uint32_t)(Tt - 1) * tstep;   // odd c, last tile -> next pair
     uint32_t wl[D], wh[D];
     auto load_next = [&](int slot) {
@@ -417,7 +426,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         wl[slot] = w.x;
         wh[slot] = w.y;
         if (slot & 1) {
-            const bool wrap = ++lt == Tt;
+            const bool wrap = ++lt == Tw;
             lt = wrap ? 0 : lt;
             lso += wrap ? cwrap : tnext;
         } else {
@@ -501,8 +510,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // pcur + 64 T (u/2) (an immediate offset); after a pass pcur advances by 64 T D/2 on the
     // diagonal lanes and stays on the others, whose scratch words stay inside the 1 KB area.
     const uint32_t diag = g == kq ? 1u : 0u;
-    uint8_t* pcur = diag ? (uint8_t*)part + (g * 4 + r) * 4 + (uint32_t)(s0 >> 1) * T * 64 : Js + lane * 4;
-    const uint32_t pinc = diag * (uint32_t)(D / 2 * T * 64);
+    // (strided: the pair slots of a wave are G tiles apart, at most 5 x 128 B: the scratch
+    // words of the other lanes still stay inside the 1 KB area)
+    const uint32_t pstep = (uint32_t)(strided ? G : 1) * T * 64;
+    uint8_t* pcur = diag ? (uint8_t*)part + (g * 4 + r) * 4 + (uint32_t)(strided ? sp * Tt + sh : s0 >> 1) * T * 64
+                         : Js + lane * 4;
+    const uint32_t pinc = diag * (D / 2) * pstep;
     float vprev[T];
     v4i A[2][kMfmaPerBlock];                     // block steps 2 cp and 2 cp + 1
     float sc[2][T];
@@ -524,7 +537,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         B[2][0] = (int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff));   // B[2][2..3] stay zero
         B[2][1] = (int)trit0_word(w1);
     };
-    int ct = (s0 % (2 * Tt)) >> 1, cp = s0 / (2 * Tt);   // compute cursor: tile, pair
+    int ct = strided ? 0 : (s0 % (2 * Tt)) >> 1, cp = strided ? sp : s0 / (2 * Tt);   // compute cursor: tile, pair
     v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
     B0[2] = v4i{0, 0, 0, 0};
     B1[2] = v4i{0, 0, 0, 0};
@@ -538,7 +551,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
         float d = half_bits_to_float(wh[u] >> 16);
         if (PAD && 4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
-        float* dst = (float*)(pcur + (u >> 1) * T * 64);
+        float* dst = (float*)(pcur + (u >> 1) * pstep);
 #pragma unroll
         for (int t = 0; t < T; t++) {
             // explicit fma, contraction off (below): every instantiation (one matrix or a
@@ -549,7 +562,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
             else
                 vprev[t] = fi * fs;
         }
-        if ((u & 1) && ++ct == Tt) {
+        if ((u & 1) && ++ct == Tw) {
             ct = 0;
             ++cp;
             if (next) load_a(cp);
@@ -924,20 +937,28 @@ static int device_cus() {
     return n_cu;
 }
 
-template <int T, int LR, bool PAD, bool XS, bool MULTI>
+template <int T, int LR, bool PAD, bool XS, bool MULTI, bool STRIDE = false>
 static hipError_t launch_gemv_cfg(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
                                   hipStream_t s) {
     static bool attr_done = false;
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            kLdsMax - gemv_static_lds_bytes(LR));
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI>), dim3(P.wg0[P.count]), dim3(1024),
+    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>), dim3(P.wg0[P.count]), dim3(1024),
                        lds - gemv_static_lds_bytes(LR), s, P, x, x_dtype, x_layout, K, gemv_nq(K));
     return hipGetLastError();
+}
+
+// The tile-strided order pays off for one matrix with long tile ranges (the 248320-row
+// lm_head: 88 -> 78 us) and rows of few step pairs that fill the 16 waves (5 pairs: 15
+// waves busy); for the sweep's 6-34 tiles per workgroup it was slower.
+static bool gemv_strided(const GemvMats& P, int K) {
+    const int np = gemv_nq(K) / 2, G = 16 / np;
+    return P.count == 1 && np > 0 && G >= 2 && G * np >= 15 && P.tpw[0] >= 64;
 }
 
 template <int T, int LR, bool XS>
@@ -946,6 +967,8 @@ static hipError_t launch_gemv_pad(const GemvMats& P, const void* x, int x_dtype,
     if (P.count > 1)
         return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XS, true>(P, x, x_dtype, x_layout, K, lds, s)
                                 : launch_gemv_cfg<T, LR, false, XS, true>(P, x, x_dtype, x_layout, K, lds, s);
+    if ((K / kGroup) % 8 == 0 && gemv_strided(P, K))
+        return launch_gemv_cfg<T, LR, false, XS, false, true>(P, x, x_dtype, x_layout, K, lds, s);
     return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XS, false>(P, x, x_dtype, x_layout, K, lds, s)
                             : launch_gemv_cfg<T, LR, false, XS, false>(P, x, x_dtype, x_layout, K, lds, s);
 }

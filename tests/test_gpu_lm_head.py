@@ -57,3 +57,23 @@ def test_lm_head_gemv_then_argmax(dev):
     ref = orc.gemv_ptq1(np.ascontiguousarray(W_np[rows]), x.cpu().numpy(), K, len(rows), 1)
     assert rel_l2(y.cpu().numpy()[:, rows], ref).max() < 2e-4
     assert ops.argmax(y).item() == ref_argmax(y.cpu().numpy()[0])
+
+
+def test_lm_head_strided_order_equals_run_order(dev):
+    """The 248320-row lm_head alone runs the tile-strided work order; inside a two-matrix
+    batch it runs the contiguous one: the same items and slots, so the same result bit for bit."""
+    K, N = 5120, 248320
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    nb = K // 128
+    blk = torch.empty((N, nb, 28), dtype=torch.uint8, device=dev)
+    blk[:, :, :24] = torch.randint(0, 243, (N, nb, 24), generator=gen, device=dev, dtype=torch.uint8)
+    blk[:, :, 24:26] = torch.randint(0, 81, (N, nb, 2), generator=gen, device=dev, dtype=torch.uint8)
+    blk[:, :, 26:28] = (torch.randn((N, nb), generator=gen, device=dev) * 0.02).abs().half() \
+        .view(torch.uint8).view(N, nb, 2)
+    W = blk.view(N, nb * 28)
+    W2 = W[:64].clone()
+    x = torch.randn((1, K), generator=gen, device=dev).half()
+    y = ops.gemv_ptq1(W, x, K, N, 1)
+    yb, _ = ops.gemv_ptq1_batch([W, W2], x, K, [N, 64], 1)
+    assert torch.equal(y, yb)
