@@ -7,13 +7,17 @@
 // gemm (shaders/prefill.metal:382-415): I = sum_{k in g} A8[m][k]*trit[n][k] (exact int32),
 //   C[m][n] = sum_g float(I) * (d[n][g] * SX[g][m]) in fp32, groups ascending.
 //
-// Design: 128x128 C tile per 256-thread workgroup, one K-step per 128-group; A8 tile
-// copied to LDS, W tile decoded to int8 trits in LDS (two adjacent-k trits per 16-bit
-// store).  Each wave runs 4x4 tiles of v_mfma_i32_16x16x64_i8 (two per group) and folds
-// the group's int32 result into fp32 accumulators with the row/column scales.
+// Design: the tile machinery of the fp16 GEMM (256 x 128 C tiles, 8 waves: 4 consumers
+// on v_mfma_i32_32x32x32_i8, 4 producers copying A by DMA and decoding weights into LDS,
+// whole tiles per CU then K pieces summed by a second kernel).  A stage is one 128-group:
+// an int8 A row of 128 k is 128 bytes, the byte layout of an fp16 stage row of 64 k, so the
+// A copies, swizzle and fragment reads are the fp16 kernel's, with half the stages.  The
+// producers also stage the group's row scales (A side) and column scales (decoded weights)
+// in LDS; consumers fold each 32 x 32 tile's exact group sum into fp32 right after its
+// four MFMAs, groups ascending.
 #include "common.h"
 #include "launch.h"
-#include "gemm_sched.h"
+#include "gemm_tile.h"
 
 namespace kata {
 
@@ -83,145 +87,220 @@ __device__ inline uint32_t trits4(uint32_t w, uint32_t p3lo, uint32_t p3hi) {
     return __builtin_amdgcn_perm(0u, 0x000100ffu, dg);
 }
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDB_S = BK + 16;   // bytes per LDS row
+using namespace gemm;
+constexpr int kWStage = BN * 32;                     // staged packed bytes of one block of the tile rows
+constexpr int kSxOff = kTileBytes + 2 * kWStage;     // [kABuf][BM] fp32 row scales (with the A buffers)
+constexpr int kSwOff = kSxOff + kABuf * BM * 4;      // [2][BN] fp32 column scales (with the B buffers)
+constexpr int kLdsBytes = kSwOff + 2 * BN * 4;
 
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// LDS DMA of one dword per lane to lds + 4*lane (lds wave-uniform); see dma16
+__device__ inline void dma4(const void* g, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(lds)
+                 : "memory");
+}
+
+// Consumer waves (wave < 4): wave w owns rows 64w..64w+63 and all 128 columns, 2 x 4 tiles of
+// 32 x 32.  Per stage (one group of 128 k) the A fragments of both row tiles stay in
+// registers; for each column tile j the two tiles' int32 sums are 4 dependent
+// v_mfma_i32_32x32x32_i8 each, then folded: acc += float(I) * (sw[n] * sx[m]).
+// Barriers as in the fp16 consumer: two before the first stage, one per stage (after the
+// stage's last LDS read).
 template <bool C_F16>
-__global__ __launch_bounds__(256) void k_gemm_ptq1_i8(const int8_t* __restrict__ A8, const float* __restrict__ SX,
-                                                      int ldS, const uint8_t* __restrict__ W, void* __restrict__ C,
-                                                      int ldc, float* __restrict__ ws, int M, int K, int N,
-                                                      GemmJobs J) {
-    __shared__ int8_t As[BM * LDB_S];
-    __shared__ int8_t Bs[BN * LDB_S];
-    __shared__ float sws[BN];
-    __shared__ float sxs[BM];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int nb = K / kGroup;
-    int job, tile, kb_lo, kb_n;
-    gemm_job(J, nb, job, tile, kb_lo, kb_n);
-    const int m0 = (tile / J.G) * BM, n0 = (tile % J.G) * BN;
-    const int l16 = lane & 15, lg = lane >> 4;
-
-    v4f acc[4][4];
+__device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int job, const GemmJobs& J, float* ws,
+                                  void* C, int ldc, int M, int m0, int n0, int R) {
+    const int l32 = lane & 31, lh = lane >> 5;
+    v16f acc[2][NT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int jx = 0; jx < 4; jx++) acc[i][jx] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    // the operands of the next group are loaded into registers while the matrix cores work
-    // on the current one: thread -> 64 bytes of A row tid / 2 and the 7 dwords of W row
-    // tid / 2's block (thread tid < BM also the row scale of A row tid)
-    const int lr = tid >> 1, lh = tid & 1;
-    const bool a_ok = m0 + lr < M, w_ok = n0 + lr < N, s_ok = tid < BM && m0 + tid < M;
-    const uint4* asrc = (const uint4*)(A8 + (size_t)min(m0 + lr, M - 1) * K + lh * 64);
-    const uint32_t* wsrc = (const uint32_t*)(W + (size_t)min(n0 + lr, N - 1) * nb * kBlockBytes);   // 4-byte aligned
-    uint4 pa[4];
-    uint32_t pw[7];
-    float psx = 0.0f;
-    auto fetch = [&](int kb) {
+        for (int j = 0; j < NT; j++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) pa[c] = asrc[kb * (BK / 16) + c];
+            for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
+    // lane l holds row / column l % 32 of each 32-row tile at k = 32 kk + 16 (l / 32) .. +15,
+    // chunk 2 kk + l / 32 (the same byte positions as the fp16 fragments)
+    const int xs = (l32 >> 1) & 7;
+    const uint32_t a_row = (uint32_t)(wave * 64 + l32) * ROWB, b_row = (uint32_t)l32 * ROWB;
+    const float* sxs = (const float*)(smem + kSxOff) + wave * 64 + 4 * lh;
+    const float* sws = (const float*)(smem + kSwOff) + l32;
+    barrier_lds();                           // the producers' first copies landed
+    barrier_lds();                           // stage 0 produced
+    for (int st = 0; st < nb; st++) {
+        const uint8_t* at = tile_a(smem, st % kABuf) + a_row;
+        const uint8_t* bt = tile_b(smem, st & 1) + b_row;
+        v4i af[2][4];
 #pragma unroll
-        for (int i = 0; i < 7; i++) pw[i] = wsrc[kb * 7 + i];
-        if (tid < BM) psx = SX[(size_t)kb * ldS + min(m0 + tid, M - 1)];
-    };
-    fetch(kb_lo);
-    for (int kb = kb_lo; kb < kb_lo + kb_n; ++kb) {
-        __syncthreads();                         // the previous group's LDS tiles are consumed
-        {
-            uint4* dst = (uint4*)(As + lr * LDB_S + lh * 64);
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) dst[c] = a_ok ? pa[c] : make_uint4(0, 0, 0, 0);
-            if (tid < BM) sxs[tid] = s_ok ? psx : 0.0f;
-        }
-        // B tile: thread -> 4 of the 8 16-byte chunks (16 k each) of tile row tid / 2
-        {
-            uint4* brow = (uint4*)(Bs + lr * LDB_S);
-            if (w_ok) {
-                const uint32_t w0 = pw[0], w1 = pw[1], w2 = pw[2], w3 = pw[3], w4 = pw[4], w5 = pw[5], w6 = pw[6];
-                if (lh == 0) {
-                    // chunks 0..3: dwords 0..3 at digit c
+            for (int kk = 0; kk < 4; kk++) af[i][kk] = *(const v4i*)(at + i * 32 * ROWB + (((2 * kk + lh) ^ xs) << 4));
+        // row scales of the lane's output rows 8 (q / 4) + 4 (l / 32) + q % 4 of each row tile
+        float sx[2][16];
 #pragma unroll
-                    for (int c = 0; c < 4; c++)
-                        brow[c] = make_uint4(trits4(w0, p3x2(c), p3x2(c)), trits4(w1, p3x2(c), p3x2(c)),
-                                             trits4(w2, p3x2(c), p3x2(c)), trits4(w3, p3x2(c), p3x2(c)));
-                    sws[lr] = half_bits_to_float(w6 >> 16);
-                } else {
-                    brow[4] = make_uint4(trits4(w0, p3x2(4), p3x2(4)), trits4(w1, p3x2(4), p3x2(4)),
-                                         trits4(w2, p3x2(4), p3x2(4)), trits4(w3, p3x2(4), p3x2(4)));
-                    brow[5] = make_uint4(trits4(w4, p3x2(0), p3x2(0)), trits4(w5, p3x2(0), p3x2(0)),
-                                         trits4(w4, p3x2(1), p3x2(1)), trits4(w5, p3x2(1), p3x2(1)));
-                    brow[6] = make_uint4(trits4(w4, p3x2(2), p3x2(2)), trits4(w5, p3x2(2), p3x2(2)),
-                                         trits4(w4, p3x2(3), p3x2(3)), trits4(w5, p3x2(3), p3x2(3)));
-                    const uint32_t qh = __builtin_amdgcn_perm(0u, w6, 0x01000100u);   // (qh0, qh1, qh0, qh1)
-                    brow[7] = make_uint4(trits4(w4, p3x2(4), p3x2(4)), trits4(w5, p3x2(4), p3x2(4)),
-                                         trits4(qh, p3x2(0), p3x2(1)), trits4(qh, p3x2(2), p3x2(3)));
-                }
-            } else {
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int c = 0; c < 4; c++) brow[4 * lh + c] = make_uint4(0, 0, 0, 0);
-                if (lh == 0) sws[lr] = 0.0f;
+            for (int r4 = 0; r4 < 4; r4++) {
+                const v4f v = *(const v4f*)(sxs + (st % kABuf) * BM + i * 32 + 8 * r4);
+#pragma unroll
+                for (int c = 0; c < 4; c++) sx[i][4 * r4 + c] = v[c];
             }
-        }
-        if (kb + 1 < kb_lo + kb_n) fetch(kb + 1);
-        __syncthreads();
-        v4i ia[4][4];
+        float sw[NT];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int j = 0; j < NT; j++) sw[j] = sws[(st & 1) * BN + j * 32];
 #pragma unroll
-            for (int jx = 0; jx < 4; jx++) ia[i][jx] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < NT; j++) {
+            v4i bf[4];
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            v4i af[4], bf[4];
+            for (int kk = 0; kk < 4; kk++) bf[kk] = *(const v4i*)(bt + j * 32 * ROWB + (((2 * kk + lh) ^ xs) << 4));
+            if (j == NT - 1) barrier_lds();  // stage st + 1 produced; stage st's buffers free
+            v16i I[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As + (wm * 64 + i * 16 + l16) * LDB_S + kk * 64 + lg * 16);
+            for (int i = 0; i < 2; i++) {
 #pragma unroll
-            for (int jx = 0; jx < 4; jx++) bf[jx] = *(const v4i*)(Bs + (wn * 64 + jx * 16 + l16) * LDB_S + kk * 64 + lg * 16);
+                for (int q = 0; q < 16; q++) I[i][q] = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int kk = 0; kk < 4; kk++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][kk], bf[kk], I[i], 0, 0, 0);
+            }
 #pragma unroll
-                for (int jx = 0; jx < 4; jx++)
-                    ia[i][jx] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[jx], ia[i][jx], 0, 0, 0);
-        }
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int jx = 0; jx < 4; jx++) {
-            const float sw = sws[wn * 64 + jx * 16 + l16];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc[i][jx][r] += (float)ia[i][jx][r] * (sw * sxs[wm * 64 + i * 16 + lg * 4 + r]);
+                for (int q = 0; q < 16; q++) acc[i][j][q] += (float)I[i][q] * (sw[j] * sx[i][q]);
         }
     }
+    // store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
     if (job >= J.n_full) {
-        // a piece: the whole fp32 tile, [128][128], into its workspace slot
         float* P = ws + (size_t)(job - J.n_full) * (BM * BN);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int jx = 0; jx < 4; jx++)
+            for (int j = 0; j < NT; j++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float v = acc[i][jx][r];
-                    P[(wm * 64 + i * 16 + lg * 4 + r) * BN + wn * 64 + jx * 16 + l16] = v;
-                }
+                for (int q = 0; q < 16; q++)
+                    P[(wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3)) * BN + j * 32 + l32] = acc[i][j][q];
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int jx = 0; jx < 4; jx++) {
-            const int gn = n0 + wn * 64 + jx * 16 + l16;
+        for (int j = 0; j < NT; j++) {
+            const int gc = j * 32 + l32;
+            const int gn = n0 + gc;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int gm = m0 + wm * 64 + i * 16 + lg * 4 + r;
-                if (gm < M && gn < N) {
-                    if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][jx][r];
-                    else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][jx][r];
+            for (int q = 0; q < 16; q++) {
+                const int gm = m0 + wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
+                if (gm < M && gc < R) {
+                    if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][q];
+                    else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][q];
                 }
             }
         }
+}
+
+// Stage = one PTQ1_0 block (128 k).  Producer waves 4..7: A stage copies (8 DMA per wave)
+// plus the stage's row scales (one dword DMA per wave, rows 64 pw .. +63, clamped to M - 1),
+// two stages ahead into three buffers; packed weight bytes of a block staged by DMA two
+// blocks ahead; decode of the next stage into one of two B buffers.  Producer lane decodes
+// half q = pw & 1 of tile row 64 (pw >> 1) + lane: chunks 0..3 (q = 0: dwords 0..3 at digits
+// 0..3) or chunks 4..7 (q = 1: digit 4 of dwords 0..3, dwords 4, 5, the qh bytes).
+template <bool C_F16>
+__global__ __launch_bounds__(512) void k_gemm_ptq1_i8(const int8_t* __restrict__ A8, const float* __restrict__ SX,
+                                                      int ldS, const uint8_t* __restrict__ W, void* __restrict__ C,
+                                                      int ldc, float* __restrict__ ws, int M, int K, int N,
+                                                      GemmJobs J) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nbk = K >> 7;
+    int job, tile, kb0, nb;
+    gemm_job(J, nbk, job, tile, kb0, nb);
+    const int m0 = (tile / J.G) * BM;
+    const int n0 = (tile % J.G) * BN;
+    const int R = min(BN, N - n0);
+    const uint32_t row_bytes = (uint32_t)nbk * kBlockBytes;
+
+    if (wave < 4) {
+        consume_i8<C_F16>(smem, wave, lane, nb, job, J, ws, C, ldc, M, m0, n0, R);
+        return;
+    }
+
+    // ================= producers =================
+    const int pw = wave - 4;
+    // an int8 row of 128 k has the byte layout of an fp16 stage row of 64 k
+    const _Float16* Ah = (const _Float16*)(A8 + (size_t)kb0 * kGroup);
+    const float* sxsrc = SX + (size_t)kb0 * ldS + min(m0 + 64 * pw + lane, M - 1);
+    const uint32_t sx_lds = lds_addr(smem + kSxOff) + 256 * pw;
+    auto issue_a = [&](int st) {
+        gemm::issue_a(smem, pw, lane, Ah, K >> 1, M, m0, st, nb);
+        dma4(sxsrc + (size_t)min(st, nb - 1) * ldS, sx_lds + (st % kABuf) * (BM * 4));
+    };
+    const int wrow = 64 * (pw >> 1) + lane, q = pw & 1;
+    const bool wactive = wrow < R;
+    uint8_t* Ws = smem + kTileBytes;                                  // [2 slots][2][BN][16 B]
+    float* sws = (float*)(smem + kSwOff);
+    const uint8_t* wsrc = W + (size_t)min(n0 + min(wrow, R - 1), N - 1) * row_bytes + (size_t)kb0 * kBlockBytes + 12 * q;
+    auto issue_w = [&](int blk) {
+        dma16(wsrc + (size_t)min(blk, nb - 1) * kBlockBytes,
+              lds_addr(Ws + (blk & 1) * kWStage + q * (BN * 16) + (pw >> 1) * 1024));
+    };
+    uint32_t w[7];
+    auto read_w = [&](int blk) {
+        const uint8_t* slot = Ws + (blk & 1) * kWStage;
+        const uint4 a = *(const uint4*)(slot + wrow * 16);           // bytes 0..15
+        const uint4 c = *(const uint4*)(slot + BN * 16 + wrow * 16); // bytes 12..27
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = c.y; w[5] = c.z; w[6] = c.w;
+    };
+    auto decode = [&](int buf) {
+        uint8_t* bt = tile_b(smem, buf);
+        auto put = [&](int chunk, uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3) {
+            *(uint4*)(bt + swz(wrow, chunk)) = make_uint4(x0, x1, x2, x3);
+        };
+        if (!wactive) {
+            if (q == 0) sws[buf * BN + wrow] = 0.0f;
+            return;
+        }
+        if (q == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                put(c, trits4(w[0], p3x2(c), p3x2(c)), trits4(w[1], p3x2(c), p3x2(c)), trits4(w[2], p3x2(c), p3x2(c)),
+                    trits4(w[3], p3x2(c), p3x2(c)));
+            sws[buf * BN + wrow] = half_bits_to_float(w[6] >> 16);
+        } else {
+            put(4, trits4(w[0], p3x2(4), p3x2(4)), trits4(w[1], p3x2(4), p3x2(4)), trits4(w[2], p3x2(4), p3x2(4)),
+                trits4(w[3], p3x2(4), p3x2(4)));
+            put(5, trits4(w[4], p3x2(0), p3x2(0)), trits4(w[5], p3x2(0), p3x2(0)), trits4(w[4], p3x2(1), p3x2(1)),
+                trits4(w[5], p3x2(1), p3x2(1)));
+            put(6, trits4(w[4], p3x2(2), p3x2(2)), trits4(w[5], p3x2(2), p3x2(2)), trits4(w[4], p3x2(3), p3x2(3)),
+                trits4(w[5], p3x2(3), p3x2(3)));
+            const uint32_t qh = __builtin_amdgcn_perm(0u, w[6], 0x01000100u);   // (qh0, qh1, qh0, qh1)
+            put(7, trits4(w[4], p3x2(4), p3x2(4)), trits4(w[5], p3x2(4), p3x2(4)), trits4(qh, p3x2(0), p3x2(1)),
+                trits4(qh, p3x2(2), p3x2(3)));
+        }
+    };
+    // Vector-memory order of a producer (all LDS copies, counted by the waits below):
+    // W(b+2) then A(b+2) (9 copies) per iteration; the wait before the barrier that ends
+    // iteration b leaves only A(b+2) in flight, so batch b+1 and block b+2 have landed.
+    issue_w(0);
+    issue_w(1);
+    issue_a(0);
+    issue_a(1);
+    __builtin_amdgcn_s_waitcnt((9 & 15) | ((9 >> 4) << 14) | (7 << 4) | (15 << 8));       // blocks 0, 1, batch 0
+    barrier_lds();
+    read_w(0);
+    decode(0);
+    barrier_lds();
+    for (int b = 0; b < nb; b++) {
+        // consumers on stage b; produce stage b + 1 into B buffer (b + 1) & 1
+        if (b + 1 < nb) read_w(b + 1);
+        issue_w(b + 2);                          // into the slot read_w(b) freed
+        issue_a(b + 2);
+        if (b + 1 < nb) decode((b + 1) & 1);
+        __builtin_amdgcn_s_waitcnt((9 & 15) | ((9 >> 4) << 14) | (7 << 4) | (15 << 8));   // batch b+1, block b+2
+        barrier_lds();
+    }
 }
 
 }  // namespace
@@ -233,21 +312,30 @@ hipError_t launch_quant_rows(const uint16_t* X, int8_t* Q, float* SX, int M, int
     return hipGetLastError();
 }
 
-// Two workgroups are resident per CU (their registers), so the schedule fills 2 n_cu slots.
 hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint8_t* W, void* C, int c_dtype,
                           int ldc, int M, int K, int N, hipStream_t s) {
+    static bool attr_done = false;
+    if (!attr_done) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_ptq1_i8<true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_i8<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    kLdsBytes);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
     int n_cu = 0;
     float* ws = nullptr;
     hipError_t e = gemm_device(false, s, &n_cu, &ws);
     if (e != hipSuccess) return e;
-    const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, 2 * n_cu);
+    const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, n_cu);   // one workgroup per CU
     if (J.n_jobs > J.n_full && (e = gemm_device(true, s, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
-        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, dim3(J.n_jobs), dim3(256), 0, s, A8, SX, ldS, W, C, ldc, ws, M, K, N,
-                           J);
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, A8, SX, ldS, W, C, ldc, ws,
+                           M, K, N, J);
     else
-        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, dim3(J.n_jobs), dim3(256), 0, s, A8, SX, ldS, W, C, ldc, ws, M, K,
-                           N, J);
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, A8, SX, ldS, W, C, ldc,
+                           ws, M, K, N, J);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_pieces_sum<BM, BN>(ws, C, c_dtype, ldc, M, N, J, s);

@@ -198,7 +198,7 @@ def test_gemm_i8_golden_and_random(dev, golden):
 
 # ----------------------------------------------------------------------------- dispatcher
 def test_gemm_i8_tile_schedules(dev):
-    """int8 GEMM over whole tiles plus K-pieces (513 tiles of 128x128 on 2 x 256 slots) and
+    """int8 GEMM over whole tiles plus K-pieces (513 tiles of 256x128 on 256 slots) and
     pieces only, back to back; vs the oracle's int8 path."""
     for M, K, N in ((128, 256, 128 * 513 - 7), (200, 1280, 300)):
         W_np, _, _ = orc.synth_ptq1(N, K, M + K + N + 5)
