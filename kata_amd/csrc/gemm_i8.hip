@@ -18,6 +18,7 @@
 #include "common.h"
 #include "launch.h"
 #include "gemm_tile.h"
+#include <utility>
 
 namespace kata {
 
@@ -94,6 +95,17 @@ constexpr int kSwOff = kSxOff + kABuf * BM * 4;      // [2][BN] fp32 column scal
 constexpr int kLdsBytes = kSwOff + 2 * BN * 4;
 
 typedef int v16i __attribute__((ext_vector_type(16)));
+// the value v of lane Q of the caller's 16-lane row (DPP row_newbcast)
+template <int Q>
+__device__ inline float row_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + Q, 0xf, 0xf, true));
+}
+// acc[q] += float(I[q]) * (w * sx[row of output q]), where lane 16 R + Q of the caller's
+// 16-lane row R holds the row scale of output q = Q
+template <int... Q>
+__device__ inline void fold_tile(v16f& acc, const v16i& I, float w, float sxv, std::integer_sequence<int, Q...>) {
+    ((acc[Q] += (float)I[Q] * (w * row_bcast<Q>(sxv))), ...);
+}
 
 // LDS DMA of one dword per lane to lds + 4*lane (lds wave-uniform); see dma16
 __device__ inline void dma4(const void* g, uint32_t lds) {
@@ -107,7 +119,8 @@ __device__ inline void dma4(const void* g, uint32_t lds) {
 // Consumer waves (wave < 4): wave w owns rows 64w..64w+63 and all 128 columns, 2 x 4 tiles of
 // 32 x 32.  Per stage (one group of 128 k) the A fragments of both row tiles stay in
 // registers; for each column tile j the two tiles' int32 sums are 4 dependent
-// v_mfma_i32_32x32x32_i8 each, then folded: acc += float(I) * (sw[n] * sx[m]).
+// v_mfma_i32_32x32x32_i8 each, then folded: acc += float(I) * (sw[n] * sx[m]), the row
+// scale spread across the lanes by DPP.
 // Barriers as in the fp16 consumer: two before the first stage, one per stage (after the
 // stage's last LDS read).
 template <bool C_F16>
@@ -125,7 +138,9 @@ __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int
     // chunk 2 kk + l / 32 (the same byte positions as the fp16 fragments)
     const int xs = (l32 >> 1) & 7;
     const uint32_t a_row = (uint32_t)(wave * 64 + l32) * ROWB, b_row = (uint32_t)l32 * ROWB;
-    const float* sxs = (const float*)(smem + kSxOff) + wave * 64 + 4 * lh;
+    // lane 16 R + p reads the row scale of output p of a lane in 16-lane row R: output row
+    // 8 (p / 4) + 4 (R / 2) + p % 4 of the 32-row tile (one LDS read per row tile and stage)
+    const float* sxs = (const float*)(smem + kSxOff) + wave * 64 + 8 * ((lane & 15) >> 2) + 4 * lh + (lane & 3);
     const float* sws = (const float*)(smem + kSwOff) + l32;
     barrier_lds();                           // the producers' first copies landed
     barrier_lds();                           // stage 0 produced
@@ -138,15 +153,9 @@ __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) af[i][kk] = *(const v4i*)(at + i * 32 * ROWB + (((2 * kk + lh) ^ xs) << 4));
         // row scales of the lane's output rows 8 (q / 4) + 4 (l / 32) + q % 4 of each row tile
-        float sx[2][16];
+        float sxv[2];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const v4f v = *(const v4f*)(sxs + (st % kABuf) * BM + i * 32 + 8 * r4);
-#pragma unroll
-                for (int c = 0; c < 4; c++) sx[i][4 * r4 + c] = v[c];
-            }
+        for (int i = 0; i < 2; i++) sxv[i] = sxs[(st % kABuf) * BM + i * 32];
         float sw[NT];
 #pragma unroll
         for (int j = 0; j < NT; j++) sw[j] = sws[(st & 1) * BN + j * 32];
@@ -165,9 +174,7 @@ __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int
                 for (int kk = 0; kk < 4; kk++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][kk], bf[kk], I[i], 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int q = 0; q < 16; q++) acc[i][j][q] += (float)I[i][q] * (sw[j] * sx[i][q]);
+            for (int i = 0; i < 2; i++) fold_tile(acc[i][j], I[i], sw[j], sxv[i], std::make_integer_sequence<int, 16>());
         }
     }
     // store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
