@@ -211,16 +211,15 @@ hipError_t gemm_device(bool need_ws, hipStream_t s, int* n_cu, float** ws) {
 
 hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,
                            int M, int K, int N, hipStream_t s) {
-    static bool attr_done = false;
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    // the dynamic-LDS limit of both instantiations, raised once per process (a function-local
+    // static: thread-safe initialisation)
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
         if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    kLdsBytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+            e = hipFuncSetAttribute((const void*)k_gemm_ptq1_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
     int n_cu = 0;
     float* ws = nullptr;
     hipError_t e = gemm_device(false, s, &n_cu, &ws);

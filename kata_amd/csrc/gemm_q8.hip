@@ -146,16 +146,15 @@ __global__ __launch_bounds__(512) void k_gemm_q8_f16(const _Float16* __restrict_
 
 hipError_t launch_gemm_q8(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M, int K,
                           int N, hipStream_t s) {
-    static bool attr_done = false;
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q8_f16<true>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kQ8LdsBytes);
+    // the dynamic-LDS limit of both instantiations, raised once per process (a function-local
+    // static: thread-safe initialisation)
+    static const hipError_t attr = [] {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q8_f16<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8LdsBytes);
         if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_gemm_q8_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    kQ8LdsBytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+            e = hipFuncSetAttribute((const void*)k_gemm_q8_f16<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8LdsBytes);
+        return e;
+    }();
+    if (attr != hipSuccess) return attr;
     int n_cu = 0;
     float* ws = nullptr;
     hipError_t e = gemm_device(false, s, &n_cu, &ws);

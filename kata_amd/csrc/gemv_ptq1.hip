@@ -926,28 +926,20 @@ static int gemv_lds_bytes(int K, int T, int LR, int tpw, int xbytes) {
            std::max(nq / 2 * tpw * T * 16 * 4, (xbytes + 1023) & ~1023);
 }
 
+// the current device's CU count (per device; 256 if it cannot be read)
 static int device_cus() {
-    static int n_cu = 0;
-    if (!n_cu) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-            n_cu = 256;
-    }
-    return n_cu;
+    int n_cu = 0;
+    return device_cu_count(&n_cu) == hipSuccess ? n_cu : 256;
 }
 
 template <int T, int LR, bool PAD, bool XS, bool MULTI, bool STRIDE = false>
 static hipError_t launch_gemv_cfg(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
                                   hipStream_t s) {
-    static bool attr_done = false;
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           kLdsMax - gemv_static_lds_bytes(LR));
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+    // raised once per process (a function-local static: thread-safe initialisation)
+    static const hipError_t attr = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       kLdsMax - gemv_static_lds_bytes(LR));
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>), dim3(P.wg0[P.count]), dim3(1024),
                        lds - gemv_static_lds_bytes(LR), s, P, x, x_dtype, x_layout, K, gemv_nq(K));
     return hipGetLastError();
