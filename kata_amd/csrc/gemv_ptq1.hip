@@ -651,7 +651,8 @@ constexpr int kVwWaves = 8;
 constexpr int kVwBB = kVwCBMax / kVwWaves;       // blocks of a wave per chunk
 constexpr int kVwLR = 6;                         // 64 trit-table replicas (conflict-free lookups)
 constexpr int kVwImgBlk = 3 * 4 * 16 * 16;       // image bytes per block (3072)
-constexpr int kVwPrepBlocks = 8;                 // blocks per prep workgroup
+constexpr int kVwPrepBlocks = 1;                 // blocks per prep workgroup (one: the shortest chain)
+constexpr int kVwPrepThreads = kVwPrepBlocks >= 2 ? 256 : 128;   // 8 tokens x 16 chunks per block
 
 struct VwMats {
     const uint8_t* W[kMaxMats];
@@ -670,19 +671,19 @@ struct VwMats {
 // out unpadded with 16-byte stores.  Rows of tokens >= T and slots without an element are
 // zero, and so are the scales of tokens >= T.
 template <bool XF16>
-__global__ __launch_bounds__(256) void k_gemv_vw_prep(const void* __restrict__ x, int K, int T,
+__global__ __launch_bounds__(kVwPrepThreads) void k_gemv_vw_prep(const void* __restrict__ x, int K, int T,
                                                       uint8_t* __restrict__ img, float2* __restrict__ scl) {
     __shared__ __align__(16) uint8_t im[kVwPrepBlocks * kWideBlkBytes];
     const int tid = threadIdx.x;
     const int nb = K >> 7;
     const int blk0 = blockIdx.x * kVwPrepBlocks, cb = min(kVwPrepBlocks, nb - blk0);
-    constexpr int QI = 8 * kVwPrepBlocks * 16 / 256;
+    constexpr int QI = 8 * kVwPrepBlocks * 16 / kVwPrepThreads;
     constexpr int XW = XF16 ? 1 : 2;
     const int ntask = T * cb * 16;
     uint4 xr[QI][XW];
 #pragma unroll
     for (int i = 0; i < QI; i++) {
-        const int j = tid + 256 * i;
+        const int j = tid + kVwPrepThreads * i;
         if (j < ntask) {
             const int ch = j & 15, bt = j >> 4;
             const int t = bt / cb, b = bt - t * cb;
@@ -695,12 +696,12 @@ __global__ __launch_bounds__(256) void k_gemv_vw_prep(const void* __restrict__ x
             }
         }
     }
-    for (int o = tid; o < kVwPrepBlocks * kWideBlkBytes / 16; o += 256) ((uint4*)im)[o] = make_uint4(0, 0, 0, 0);
+    for (int o = tid; o < kVwPrepBlocks * kWideBlkBytes / 16; o += kVwPrepThreads) ((uint4*)im)[o] = make_uint4(0, 0, 0, 0);
     if (tid < cb * 4) scl[(size_t)(blk0 + tid / 4) * 4 + tid % 4] = make_float2(0.0f, 0.0f);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < QI; i++) {
-        const int j = tid + 256 * i;
+        const int j = tid + kVwPrepThreads * i;
         if (j >= ntask) continue;                // whole 16-lane rows drop out together
         const int ch = j & 15, bt = j >> 4;
         const int t = bt / cb, b = bt - t * cb;
@@ -747,7 +748,7 @@ __global__ __launch_bounds__(256) void k_gemv_vw_prep(const void* __restrict__ x
     }
     __syncthreads();
     // unpadded copy out: 16-byte row r of lane group g of MFMA m of block b
-    for (int o = tid; o < cb * 3 * 4 * 16; o += 256) {
+    for (int o = tid; o < cb * 3 * 4 * 16; o += kVwPrepThreads) {
         const int r = o & 15, g = (o >> 4) & 3, mb = o >> 6, m = mb % 3, b = mb / 3;
         *(uint4*)(img + (size_t)blk0 * kVwImgBlk + o * 16) =
             *(const uint4*)(im + b * kWideBlkBytes + m * kWideM + g * kWideG + r * 16);
@@ -1080,9 +1081,9 @@ static hipError_t launch_gemv_vw(int count, const uint8_t* const* W, float* cons
     float2* xscl = (float2*)(ximg + (size_t)nb * kVwImgBlk);
     const dim3 pgrid((nb + kVwPrepBlocks - 1) / kVwPrepBlocks);
     if (x_dtype == 1)
-        hipLaunchKernelGGL(k_gemv_vw_prep<true>, pgrid, dim3(256), 0, s, x, K, T, ximg, xscl);
+        hipLaunchKernelGGL(k_gemv_vw_prep<true>, pgrid, dim3(kVwPrepThreads), 0, s, x, K, T, ximg, xscl);
     else
-        hipLaunchKernelGGL(k_gemv_vw_prep<false>, pgrid, dim3(256), 0, s, x, K, T, ximg, xscl);
+        hipLaunchKernelGGL(k_gemv_vw_prep<false>, pgrid, dim3(kVwPrepThreads), 0, s, x, K, T, ximg, xscl);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int n_cu = device_cus();
