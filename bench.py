@@ -152,8 +152,7 @@ def run_config5(torch, ops, dev, stream):
         SX = torch.empty((K // 128, M), dtype=torch.float32, device=dev)
 
         def timed(fn, nrep=5):
-            fn()
-            torch.cuda.synchronize()
+            sustain(torch, fn, stream)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
             for _ in range(nrep):
@@ -212,19 +211,34 @@ def cpu_gemm_baseline(threads: int, rows: int = 512):
     return out
 
 
+def sustain(torch, fn, stream, ms=200.0):
+    """Calls fn until the GPU has run it for `ms` milliseconds (event-timed).  Under sustained
+    matrix-core load the clock settles over tens of milliseconds: a GEMM timed after a few
+    warm-up calls reads about 15 % slower than the steady state a prefill runs at (the
+    memory-bound GEMVs show no such effect)."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    total, n = 0.0, 1
+    while total < ms:
+        a.record(stream)
+        for _ in range(n):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        total += a.elapsed_time(b)
+        n = min(2 * n, 64)
+
+
 def run_gemm(torch, ops, dev, stream, copies, ncopies):
-    """pp512 exact fp16 prefill GEMM (config 4): us and TFLOPS per shape, 10 calls over
-    rotating weight copies between two events."""
+    """pp512 exact fp16 prefill GEMM (config 4): us and TFLOPS per shape, 30 calls over
+    rotating weight copies between two events, after 200 ms of sustained calls."""
     gemm = {}
     M = 512
     A = {K: torch.from_numpy(np.random.default_rng(K).standard_normal((M, K)).astype(np.float16)).to(dev)
          for K in (5120, 17408)}
     for name, K, N, j in (("ffn_gate", 5120, 17408, 7), ("ffn_down", 17408, 5120, 9)):
         C = torch.empty((M, N), dtype=torch.float16, device=dev)
-        for r in range(3):
-            ops.gemm_ptq1_f16(A[K], copies[r % ncopies][j], K, N, out=C)
-        torch.cuda.synchronize()
-        nrep = 10
+        sustain(torch, lambda: ops.gemm_ptq1_f16(A[K], copies[0][j], K, N, out=C), stream)
+        nrep = 30
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for r in range(nrep):
@@ -237,9 +251,7 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
                       "frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
         # the int8 FFN variant (config 5): activation quantisation + int8 GEMM
         Q, SX = ops.quant_rows(A[K])
-        for r in range(3):
-            ops.gemm_ptq1_i8(Q, SX, copies[r % ncopies][j], K, N, out=C)
-        torch.cuda.synchronize()
+        sustain(torch, lambda: ops.gemm_ptq1_i8(Q, SX, copies[0][j], K, N, out=C), stream)
         a.record(stream)
         for r in range(nrep):
             ops.quant_rows(A[K], out=(Q, SX))
@@ -266,10 +278,8 @@ def run_gemm(torch, ops, dev, stream, copies, ncopies):
         Wq = [torch.from_numpy(np.ascontiguousarray(blk).reshape(N, -1)).to(dev) for _ in range(2)]
         Aq = torch.from_numpy(np.random.default_rng(K + 1).standard_normal((M, K)).astype(np.float16)).to(dev)
         C = torch.empty((M, N), dtype=torch.float16, device=dev)
-        for r in range(3):
-            ops.gemm_q8_f16(Aq, Wq[r % 2], K, N, out=C)
-        torch.cuda.synchronize()
-        nrep = 10
+        sustain(torch, lambda: ops.gemm_q8_f16(Aq, Wq[0], K, N, out=C), stream)
+        nrep = 30
         a.record(stream)
         for r in range(nrep):
             ops.gemm_q8_f16(Aq, Wq[r % 2], K, N, out=C)
@@ -636,6 +646,8 @@ def main():
         pwork = torch.empty(ffn_prefill_work_bytes(H, F, M), dtype=torch.uint8, device=dev)
         for spec in ("none", "ffn"):
             disp.set_i8(spec)
+            sustain(torch, lambda: disp.ffn_prefill(*offs(0), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
+                                                    work=pwork), stream)
             us_p = time_reps(lambda r: disp.ffn_prefill(*offs(r), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
                                                         work=pwork), 10)
             ffn[f"prefill_m512_i8_{spec}_us"] = round(us_p, 1)
