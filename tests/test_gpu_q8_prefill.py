@@ -196,6 +196,21 @@ def test_gemm_i8_golden_and_random(dev, golden):
     assert rel_l2(Cg, orc.gemm_i8(Q, SX, W_np, M, K, N)).max() < 1e-6
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 128, 1), (1, 128, 129), (3, 256, 5), (257, 128, 130), (300, 384, 257)])
+def test_gemm_i8_edge_shapes(dev, M, K, N):
+    """int8 GEMM at edge shapes: one token row, one 128-group (a single stage), one output
+    column, ragged row and column tiles, and a scale row stride wider than M (ldS = M + 7),
+    with fp32 and fp16 outputs; vs the oracle's int8 path on the same Q and SX."""
+    W_np, _, _ = orc.synth_ptq1(N, K, M * 31 + K + N)
+    Q, SX = orc.quant_rows(orc.synth_x(M, K, M + 77), M, K, M + 7)
+    ref = orc.gemm_i8(Q, SX, W_np, M, K, N)
+    args = (torch.from_numpy(Q).to(dev), torch.from_numpy(SX).to(dev), torch.from_numpy(W_np).to(dev), K, N)
+    C = ops.gemm_ptq1_i8(*args).cpu().numpy()
+    assert rel_l2(C, ref).max() < 1e-6, (M, K, N)
+    C16 = ops.gemm_ptq1_i8(*args, out_dtype=torch.float16).cpu().numpy().astype(np.float32)
+    assert rel_l2(C16, ref).max() < 1e-3, (M, K, N)        # fp16 rounding: <= 2^-11 per element
+
+
 # ----------------------------------------------------------------------------- dispatcher
 def test_gemm_i8_tile_schedules(dev):
     """int8 GEMM over whole tiles plus K-pieces (513 tiles of 256x128 on 256 slots) and
