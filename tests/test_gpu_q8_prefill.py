@@ -211,6 +211,29 @@ def test_gemm_i8_edge_shapes(dev, M, K, N):
     assert rel_l2(C16, ref).max() < 1e-3, (M, K, N)        # fp16 rounding: <= 2^-11 per element
 
 
+def test_gemm_i8_pp512_and_tail_tiles(dev):
+    """Shapes just past one round of whole tiles (M = 512, 16384 < N: 256 whole tiles and a
+    tail split into K pieces): a ragged case (300 x 256 x 17000) vs the oracle, and the pp512
+    gate shape vs per-group fp32 matmuls (exact integer sums) folded in ascending group order."""
+    M, K, N = 300, 256, 17000
+    W_np, _, _ = orc.synth_ptq1(N, K, 4401)
+    Q, SX = orc.quant_rows(orc.synth_x(M, K, 4402), M, K)
+    C = ops.gemm_ptq1_i8(torch.from_numpy(Q).to(dev), torch.from_numpy(SX).to(dev),
+                         torch.from_numpy(W_np).to(dev), K, N).cpu().numpy()
+    assert rel_l2(C, orc.gemm_i8(Q, SX, W_np, M, K, N)).max() < 1e-6
+    M, K, N = 512, 5120, 17408
+    W = torch.from_numpy(orc.synth_ptq1(N, K, 4403)[0]).to(dev)
+    A = torch.from_numpy(orc.synth_x(M, K, 4404)).to(dev)
+    Q, SX = ops.quant_rows(A)
+    C8 = ops.gemm_ptq1_i8(Q, SX, W, K, N)
+    T8, SW = ops.expand_i8(W, K, N)
+    ref8 = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    for g in range(K // 128):
+        I = Q[:, 128 * g:128 * (g + 1)].float() @ T8[:, 128 * g:128 * (g + 1)].float().T
+        ref8 += I * (SW[:, g][None, :] * SX[g, :M][:, None])
+    assert rel_l2(C8.cpu().numpy(), ref8.cpu().numpy()).max() < 1e-5
+
+
 # ----------------------------------------------------------------------------- dispatcher
 def test_gemm_i8_tile_schedules(dev):
     """int8 GEMM over whole tiles plus K-pieces (513 tiles of 256x128 on 256 slots) and
