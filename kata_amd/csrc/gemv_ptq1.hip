@@ -653,6 +653,7 @@ constexpr int kVwLR = 6;                         // 64 trit-table replicas (conf
 constexpr int kVwImgBlk = 3 * 4 * 16 * 16;       // image bytes per block (3072)
 constexpr int kVwPrepBlocks = 1;                 // blocks per prep workgroup (one: the shortest chain)
 constexpr int kVwPrepThreads = kVwPrepBlocks >= 2 ? 256 : 128;   // 8 tokens x 16 chunks per block
+static_assert(8 * kVwPrepBlocks * 16 % kVwPrepThreads == 0, "whole quantisation tasks per prep thread");
 
 struct VwMats {
     const uint8_t* W[kMaxMats];
