@@ -25,7 +25,9 @@ def test_q8_golden(dev, golden):
 
 
 @pytest.mark.parametrize("K,N,T,dtype", [
-    (64, 1, 1, np.float32), (96, 7, 2, np.float16),       # odd block count: 16-bit path
+    (64, 1, 1, np.float32), (96, 7, 2, np.float16),       # odd block count: one-block tail
+    (32, 5, 1, np.float16), (8224, 9, 1, np.float16),     # one block; odd count, sliced rows
+    (8224, 6, 2, np.float32),
     (5120, 40, 1, np.float16), (5120, 33, 2, np.float32),
     (17408, 24, 2, np.float16), (10240, 16, 1, np.float32),
 ])
@@ -37,7 +39,7 @@ def test_q8_random(dev, K, N, T, dtype):
     assert rel_l2(y, ref).max() < 1e-5
 
 
-@pytest.mark.parametrize("K,N,T", [(64, 5, 1), (8192, 9, 2), (96, 3, 1)])
+@pytest.mark.parametrize("K,N,T", [(64, 5, 1), (8192, 9, 2), (96, 3, 1), (8224, 5, 1), (32, 3, 2)])
 def test_q8_unaligned_weight_base(dev, K, N, T):
     """Weights at a 2-byte (not 4-byte) aligned address: every block changes alignment."""
     W_np, _, _ = orc.synth_q8(N, K, 7 * K + N)
