@@ -10,9 +10,10 @@
 // whole 34-byte blocks and consecutive lanes own consecutive blocks of a row, so each load
 // instruction of a wave covers 2176 contiguous bytes.  A block is read from its
 // dword-aligned start as two 16-byte loads, one dword and one 16-bit load (blocks sit at
-// 2-byte granularity) and realigned with v_alignbyte.  A wave owns R = 4 rows and one of KS slices of K, and reuses each block's
-// activations (loaded once into registers) for its 4 rows; the KS waves of a workgroup
-// that share rows add their partial sums through LDS in a fixed order (deterministic).
+// 2-byte granularity) and realigned with v_alignbyte.  A wave owns R rows (2 for one
+// activation row, 4 for two) and one of KS slices of K, and reuses each block's activations
+// (loaded once into registers) for its R rows; the KS waves of a workgroup that share rows
+// add their partial sums through LDS in a fixed order (deterministic).
 #include "common.h"
 #include "launch.h"
 
@@ -20,7 +21,6 @@ namespace kata {
 
 namespace {
 
-constexpr int kRowsPerWave = 4;
 
 __device__ inline float byte_s8(uint32_t w, int k) { return (float)(int8_t)(uint8_t)(w >> (8 * k)); }
 
@@ -57,10 +57,9 @@ __device__ inline void load_x32(const void* x, int K, int b, float (&xv)[T][32])
 }
 
 // Workgroup = 4 waves = (4 / KS) row groups x KS slices of the row's blocks.
-template <int T, bool XH, int KS>
+template <int T, bool XH, int KS, int R>
 __global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t* __restrict__ W, uint32_t w_off, uint32_t w_bytes,
                                                  const void* __restrict__ x, float* __restrict__ y, int K, int N) {
-    constexpr int R = kRowsPerWave;
     constexpr int GROUPS = 4 / KS;
     __shared__ float red[4][T][R];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -200,19 +199,28 @@ __global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t* __restrict__ W, 
     }
 }
 
+template <int T, bool XH, int KS, int R>
+void launch_q8_k(const uint8_t* W, uint32_t w_off, uint32_t w_bytes, const void* x, float* y, int K, int N,
+                 hipStream_t s) {
+    const int groups = (N + R - 1) / R;
+    const int wgs = (groups + 4 / KS - 1) / (4 / KS);
+    hipLaunchKernelGGL((k_gemv_q8<T, XH, KS, R>), dim3(wgs), dim3(256), 0, s, W, w_off, w_bytes, x, y, K, N);
+}
+
 template <int T, bool XH>
 hipError_t launch_q8_t(const uint8_t* W, const void* x, float* y, int K, int N, hipStream_t s) {
     const int nb = K / kQ8Group;
     const uint32_t w_off = (uint32_t)((uintptr_t)W & 3);
     const uint32_t w_bytes = w_off + (uint32_t)N * (uint32_t)nb * kQ8BlockBytes;
-    const int groups = (N + kRowsPerWave - 1) / kRowsPerWave;
-    // long rows: four waves share a row group (one K slice each); short rows: one each
-    if (nb >= 256) {
-        hipLaunchKernelGGL((k_gemv_q8<T, XH, 4>), dim3(groups), dim3(256), 0, s, W, w_off, w_bytes, x, y, K, N);
-    } else {
-        hipLaunchKernelGGL((k_gemv_q8<T, XH, 1>), dim3((groups + 3) / 4), dim3(256), 0, s, W, w_off, w_bytes, x, y, K,
-                           N);
-    }
+    // one fp16 row (v_dot2 form, little VALU per byte): 2 rows per wave, twice the waves of
+    // 4 (17408 x 5120: 26.1 -> 20.9 us); two rows (fp32 FMAs per quant and token) keep 4 rows
+    // per wave to reuse each block's activations (2 rows per wave: 28.5 -> 32.2 us).  Rows
+    // of >= 256 blocks, and of >= 128 blocks when the one-slice grid would be small (few rows,
+    // or two activation rows), are split over 4 waves (5120 x 1024: 6.7 -> 3.7 us at T = 1).
+    constexpr int R = T == 1 ? 2 : 4;
+    const bool ks4 = nb >= 256 || (nb >= 128 && (T == 2 || N < 8192));
+    if (ks4) launch_q8_k<T, XH, 4, R>(W, w_off, w_bytes, x, y, K, N, s);
+    else launch_q8_k<T, XH, 1, R>(W, w_off, w_bytes, x, y, K, N, s);
     return hipGetLastError();
 }
 
