@@ -316,6 +316,34 @@ def graph_time(torch, fn, nrep, stream, cap_stream):
     return a.elapsed_time(b) * 1e3 / nrep
 
 
+def run_q8(torch, ops, dev, time_reps, reps):
+    """Config 3: the Q8_0 MTP-head GEMV at 17408x5120 and 5120x17408, one and two activation
+    rows, over rotating weight copies (> 512 MB)."""
+    q8 = {}
+    for name, K, N in (("gate", 5120, 17408), ("down", 17408, 5120)):
+        nb = N * (K // 32) * 34
+        nq8 = max(2, -(-512 * 1024 * 1024 // nb))
+        rng = np.random.default_rng(SEED + 400 + K)
+        blk = rng.integers(-127, 128, size=(N, K // 32, 34), dtype=np.int64).astype(np.int8).view(np.uint8)
+        d = np.abs(rng.normal(0.0, 0.02, size=(N, K // 32))).astype(np.float16).view(np.uint8).reshape(N, K // 32, 2)
+        blk[:, :, 0:2] = d
+        Wq = torch.from_numpy(np.ascontiguousarray(blk).reshape(N, -1)).to(dev)
+        Wqs = [Wq] + [Wq.clone() for _ in range(nq8 - 1)]
+        xq = torch.from_numpy(np.random.default_rng(SEED + 500 + K).standard_normal((1, K))
+                              .astype(np.float16)).to(dev)
+        yq = torch.empty((1, N), dtype=torch.float32, device=dev)
+        us = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq, K, N, 1, out=yq), max(20, reps // 4))
+        q8[name] = {"K": K, "N": N, "us": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
+        # the MTP head's two-row form (mtpRows, R = 2): both rows per weight read
+        xq2 = torch.from_numpy(np.random.default_rng(SEED + 600 + K).standard_normal((2, K))
+                               .astype(np.float16)).to(dev)
+        yq2 = torch.empty((2, N), dtype=torch.float32, device=dev)
+        us2 = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq2, K, N, 2, out=yq2), max(20, reps // 4))
+        q8[name].update({"t2_us": round(us2, 3), "t2_GBps": round(nb / (us2 * 1e-6) / 1e9, 1)})
+        del Wqs, Wq
+    return q8
+
+
 def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
     """The wide verification GEMV (Engine::dWide) at T = 4 and 8 token rows on the FFN and
     attention shapes (one weight read for all rows), and verifyWide's gate + up batched."""
@@ -386,6 +414,8 @@ def main():
                     help="only the pp512 prefill GEMMs (for counter runs), then exit")
     ap.add_argument("--wide-only", action="store_true",
                     help="only the wide verification GEMV figures (for profiler runs), then exit")
+    ap.add_argument("--q8-only", action="store_true",
+                    help="only the Q8_0 MTP-head GEMV figures (for profiler runs), then exit")
     ap.add_argument("--step-only", action="store_true",
                     help="only the timed decode-sweep steps (for counter runs), then print value and exit")
     ap.add_argument("--reps", type=int, default=200, help="repeats per matrix for the per-matrix tables")
@@ -433,6 +463,11 @@ def main():
 
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": run_gemm(torch, ops, dev, stream, copies, ncopies)}))
+        return
+    if args.q8_only:
+        cs = torch.cuda.Stream(dev)
+        print(json.dumps({"q8_0_t1": run_q8(torch, ops, dev, lambda fn, n: graph_time(torch, fn, n, stream, cs),
+                                            args.reps)}))
         return
     if args.wide_only:
         cs = torch.cuda.Stream(dev)
@@ -544,28 +579,7 @@ def main():
                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
     verify_wide = run_verify_wide(torch, ops, dev, copies, ncopies,
                                   lambda fn, n: graph_time(torch, fn, n, stream, cap_stream), args.reps)
-    q8 = {}
-    for name, K, N in (("gate", 5120, 17408), ("down", 17408, 5120)):
-        nb = N * (K // 32) * 34
-        nq8 = max(2, -(-512 * 1024 * 1024 // nb))
-        rng = np.random.default_rng(SEED + 400 + K)
-        blk = rng.integers(-127, 128, size=(N, K // 32, 34), dtype=np.int64).astype(np.int8).view(np.uint8)
-        d = np.abs(rng.normal(0.0, 0.02, size=(N, K // 32))).astype(np.float16).view(np.uint8).reshape(N, K // 32, 2)
-        blk[:, :, 0:2] = d
-        Wq = torch.from_numpy(np.ascontiguousarray(blk).reshape(N, -1)).to(dev)
-        Wqs = [Wq] + [Wq.clone() for _ in range(nq8 - 1)]
-        xq = torch.from_numpy(np.random.default_rng(SEED + 500 + K).standard_normal((1, K))
-                              .astype(np.float16)).to(dev)
-        yq = torch.empty((1, N), dtype=torch.float32, device=dev)
-        us = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq, K, N, 1, out=yq), max(20, args.reps // 4))
-        q8[name] = {"K": K, "N": N, "us": round(us, 3), "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
-        # the MTP head's two-row form (mtpRows, R = 2): both rows per weight read
-        xq2 = torch.from_numpy(np.random.default_rng(SEED + 600 + K).standard_normal((2, K))
-                               .astype(np.float16)).to(dev)
-        yq2 = torch.empty((2, N), dtype=torch.float32, device=dev)
-        us2 = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq2, K, N, 2, out=yq2), max(20, args.reps // 4))
-        q8[name].update({"t2_us": round(us2, 3), "t2_GBps": round(nb / (us2 * 1e-6) / 1e9, 1)})
-        del Wqs, Wq
+    q8 = run_q8(torch, ops, dev, time_reps, args.reps)
 
     # ---- lm_head (5120 -> 248320 PTQ1_0 GEMV, 278 MB) and the greedy argmax of its logits
     gen = torch.Generator(device=dev)
