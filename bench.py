@@ -316,6 +316,66 @@ def graph_time(torch, fn, nrep, stream, cap_stream):
     return a.elapsed_time(b) * 1e3 / nrep
 
 
+def run_ffn(torch, ops, dev, stream, time_reps):
+    """The FFN sublayer at the 27B shapes (H=5120, F=17408) through the dispatcher: decode
+    (4 launches) over 8 rotating weight sets (470 MB, past the MALL), T=8 verification,
+    pp512 prefill."""
+    from kata_amd.engine import Dispatch, ffn_prefill_work_bytes
+    H, F = 5120, 17408
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 800)
+    nset = 8
+    mats = []
+    for _ in range(nset):
+        mats += [device_weights(torch, dev, H, F, gen), device_weights(torch, dev, H, F, gen),
+                 device_weights(torch, dev, F, H, gen)]
+    wbuf = torch.cat([m.reshape(-1) for m in mats])
+    del mats
+    msz = [packed_bytes(H, F), packed_bytes(H, F), packed_bytes(F, H)]
+    set_b = sum(msz)
+    disp = Dispatch(wbuf)
+    offs = lambda r: (set_b * (r % nset), set_b * (r % nset) + msz[0], set_b * (r % nset) + msz[0] + msz[1])
+    fx = torch.randn(H, generator=gen, device=dev)
+    fy = torch.randn(H, generator=gen, device=dev)
+    fxn = torch.empty(H, device=dev)
+    gsi = torch.randn(H, generator=gen, device=dev).sign()
+    gsd = torch.randn(F, generator=gen, device=dev).sign()
+    fout = torch.empty(H, device=dev)
+    fwork = torch.empty(H + 3 * F, device=dev)
+    us_d = time_reps(lambda r: disp.ffn_decode(*offs(r), fx, fy, gsi, gsd, H, F, out=fout, xnew=fxn,
+                                               work=fwork), 40)
+    ffn = {"H": H, "F": F, "decode_us": round(us_d, 2),
+           "decode_GBps": round(set_b / (us_d * 1e-6) / 1e9, 1)}
+    # T = 8 verification tokens: transform, batched gate + up, SwiGLU transform, down
+    Tv = 8
+    vx = torch.randn((Tv, H), generator=gen, device=dev)
+    vy = torch.randn((Tv, H), generator=gen, device=dev)
+    vxn = torch.empty((Tv, H), device=dev)
+    vout = torch.empty((Tv, H), device=dev)
+    vwork = torch.empty(int(ops.lib().kata_ffn_verify_work_bytes(H, F, Tv)), dtype=torch.uint8, device=dev)
+    us_v = time_reps(lambda r: disp.ffn_verify(*offs(r), vx, vy, gsi, gsd, H, F, out=vout, xnew=vxn,
+                                               work=vwork), 40)
+    ffn["verify_t8_us"] = round(us_v, 2)
+    ffn["verify_t8_GBps"] = round(set_b / (us_v * 1e-6) / 1e9, 1)
+    M = 512
+    px = torch.randn((M, H), generator=gen, device=dev)
+    py = torch.randn((M, H), generator=gen, device=dev)
+    pxn = torch.empty((M, H), device=dev)
+    pout = torch.empty((M, H), device=dev)
+    pwork = torch.empty(ffn_prefill_work_bytes(H, F, M), dtype=torch.uint8, device=dev)
+    for spec in ("none", "ffn"):
+        disp.set_i8(spec)
+        sustain(torch, lambda: disp.ffn_prefill(*offs(0), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
+                                                work=pwork), stream)
+        us_p = time_reps(lambda r: disp.ffn_prefill(*offs(r), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
+                                                    work=pwork), 10)
+        ffn[f"prefill_m512_i8_{spec}_us"] = round(us_p, 1)
+        ffn[f"prefill_m512_i8_{spec}_TFLOPS"] = round(2 * M * 3 * H * F / (us_p * 1e-6) / 1e12, 1)
+    disp.close()
+    del wbuf, disp
+    return ffn
+
+
 def run_q8(torch, ops, dev, time_reps, reps):
     """Config 3: the Q8_0 MTP-head GEMV at 17408x5120 and 5120x17408, one and two activation
     rows, over rotating weight copies (> 512 MB)."""
@@ -414,6 +474,8 @@ def main():
                     help="only the pp512 prefill GEMMs (for counter runs), then exit")
     ap.add_argument("--wide-only", action="store_true",
                     help="only the wide verification GEMV figures (for profiler runs), then exit")
+    ap.add_argument("--ffn-only", action="store_true",
+                    help="only the FFN sublayer figures (for profiler runs), then exit")
     ap.add_argument("--q8-only", action="store_true",
                     help="only the Q8_0 MTP-head GEMV figures (for profiler runs), then exit")
     ap.add_argument("--step-only", action="store_true",
@@ -463,6 +525,11 @@ def main():
 
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": run_gemm(torch, ops, dev, stream, copies, ncopies)}))
+        return
+    if args.ffn_only:
+        cs = torch.cuda.Stream(dev)
+        print(json.dumps({"ffn_sublayer": run_ffn(torch, ops, dev, stream,
+                                                  lambda fn, n: graph_time(torch, fn, n, stream, cs))}))
         return
     if args.q8_only:
         cs = torch.cuda.Stream(dev)
@@ -611,63 +678,8 @@ def main():
         nbytes = M * W * (4 + 4 + 4 + 2)              # x, y in; xnew fp32, out fp16 out
         xform[label] = {"M": M, "W": W, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
-    # ---- layer level: the FFN sublayer (27B shapes H=5120, F=17408) through the dispatcher,
-    # decode (4 launches) over 8 rotating weight sets (470 MB, past the MALL) and pp512 prefill
-    ffn = None
-    if not args.no_ffn:
-        from kata_amd.engine import Dispatch, ffn_prefill_work_bytes
-        H, F = 5120, 17408
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(SEED + 800)
-        nset = 8
-        mats = []
-        for _ in range(nset):
-            mats += [device_weights(torch, dev, H, F, gen), device_weights(torch, dev, H, F, gen),
-                     device_weights(torch, dev, F, H, gen)]
-        wbuf = torch.cat([m.reshape(-1) for m in mats])
-        del mats
-        msz = [packed_bytes(H, F), packed_bytes(H, F), packed_bytes(F, H)]
-        set_b = sum(msz)
-        disp = Dispatch(wbuf)
-        offs = lambda r: (set_b * (r % nset), set_b * (r % nset) + msz[0], set_b * (r % nset) + msz[0] + msz[1])
-        fx = torch.randn(H, generator=gen, device=dev)
-        fy = torch.randn(H, generator=gen, device=dev)
-        fxn = torch.empty(H, device=dev)
-        gsi = torch.randn(H, generator=gen, device=dev).sign()
-        gsd = torch.randn(F, generator=gen, device=dev).sign()
-        fout = torch.empty(H, device=dev)
-        fwork = torch.empty(H + 3 * F, device=dev)
-        us_d = time_reps(lambda r: disp.ffn_decode(*offs(r), fx, fy, gsi, gsd, H, F, out=fout, xnew=fxn,
-                                                   work=fwork), 40)
-        ffn = {"H": H, "F": F, "decode_us": round(us_d, 2),
-               "decode_GBps": round(set_b / (us_d * 1e-6) / 1e9, 1)}
-        # T = 8 verification tokens: transform, batched gate + up, SwiGLU transform, down
-        Tv = 8
-        vx = torch.randn((Tv, H), generator=gen, device=dev)
-        vy = torch.randn((Tv, H), generator=gen, device=dev)
-        vxn = torch.empty((Tv, H), device=dev)
-        vout = torch.empty((Tv, H), device=dev)
-        vwork = torch.empty(int(ops.lib().kata_ffn_verify_work_bytes(H, F, Tv)), dtype=torch.uint8, device=dev)
-        us_v = time_reps(lambda r: disp.ffn_verify(*offs(r), vx, vy, gsi, gsd, H, F, out=vout, xnew=vxn,
-                                                   work=vwork), 40)
-        ffn["verify_t8_us"] = round(us_v, 2)
-        ffn["verify_t8_GBps"] = round(set_b / (us_v * 1e-6) / 1e9, 1)
-        M = 512
-        px = torch.randn((M, H), generator=gen, device=dev)
-        py = torch.randn((M, H), generator=gen, device=dev)
-        pxn = torch.empty((M, H), device=dev)
-        pout = torch.empty((M, H), device=dev)
-        pwork = torch.empty(ffn_prefill_work_bytes(H, F, M), dtype=torch.uint8, device=dev)
-        for spec in ("none", "ffn"):
-            disp.set_i8(spec)
-            sustain(torch, lambda: disp.ffn_prefill(*offs(0), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
-                                                    work=pwork), stream)
-            us_p = time_reps(lambda r: disp.ffn_prefill(*offs(r), px, py, gsi, gsd, H, F, out=pout, xnew=pxn,
-                                                        work=pwork), 10)
-            ffn[f"prefill_m512_i8_{spec}_us"] = round(us_p, 1)
-            ffn[f"prefill_m512_i8_{spec}_TFLOPS"] = round(2 * M * 3 * H * F / (us_p * 1e-6) / 1e12, 1)
-        disp.close()
-        del wbuf, disp
+    # ---- layer level: the FFN sublayer (27B shapes) through the dispatcher
+    ffn = None if args.no_ffn else run_ffn(torch, ops, dev, stream, time_reps)
 
     # ---- pp512 prefill GEMM (config 4), fp16 exact path
     gemm = None if args.no_gemm else run_gemm(torch, ops, dev, stream, copies, ncopies)
