@@ -215,11 +215,13 @@ hipError_t launch_q8_t(const uint8_t* W, const void* x, float* y, int K, int N, 
     // one fp16 row (v_dot2 form, little VALU per byte): 2 rows per wave, twice the waves of
     // 4 (17408 x 5120: 26.1 -> 20.9 us); two rows (fp32 FMAs per quant and token) keep 4 rows
     // per wave to reuse each block's activations (2 rows per wave: 28.5 -> 32.2 us).  Rows
-    // of >= 256 blocks, and of >= 128 blocks when the one-slice grid would be small (few rows,
-    // or two activation rows), are split over 4 waves (5120 x 1024: 6.7 -> 3.7 us at T = 1).
+    // are split over K slices: at T = 1 rows of >= 256 blocks over 2 waves (5120 x 17408:
+    // 22.1 us with 4 slices, 22.9 with 1, 20.9 with 2) and rows of >= 128 blocks over 4 when
+    // the one-slice grid would be small (5120 x 1024: 6.7 -> 3.7 us); at T = 2 rows of >= 128
+    // blocks over 4.
     constexpr int R = T == 1 ? 2 : 4;
-    const bool ks4 = nb >= 256 || (nb >= 128 && (T == 2 || N < 8192));
-    if (ks4) launch_q8_k<T, XH, 4, R>(W, w_off, w_bytes, x, y, K, N, s);
+    if (T == 1 && nb >= 256) launch_q8_k<T, XH, 2, R>(W, w_off, w_bytes, x, y, K, N, s);
+    else if (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) launch_q8_k<T, XH, 4, R>(W, w_off, w_bytes, x, y, K, N, s);
     else launch_q8_k<T, XH, 1, R>(W, w_off, w_bytes, x, y, K, N, s);
     return hipGetLastError();
 }
