@@ -42,13 +42,34 @@ __device__ inline void fwht1024(float (&v)[4], int tid, float* xs) {
     v[1] = b + d;
     v[2] = a - c;
     v[3] = b - d;
+    // the partner lane l ^ m: m = 1, 2 by DPP quad permutations, m = 4, 8 by DPP row shifts
+    // (the partner is in the lane's row of 16: l + m when bit m is clear, l - m when set;
+    // bound_ctrl reads 0 for sources outside the row, so the unselected shift is harmless),
+    // m = 16, 32 by a cross-lane permute
 #pragma unroll
     for (int k = 0; k < 6; k++) {
         const int m = 1 << k;
         const bool hi = lane & m;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float p = __shfl_xor(v[r], m);
+            const int iv = __builtin_bit_cast(int, v[r]);
+            int pv;
+            if (k == 0) {
+                pv = __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xf, 0xf, true);   // quad_perm [1, 0, 3, 2]
+            } else if (k == 1) {
+                pv = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xf, 0xf, true);   // quad_perm [2, 3, 0, 1]
+            } else if (k == 2) {
+                const int up = __builtin_amdgcn_mov_dpp(iv, 0x104, 0xf, 0xf, true);   // row_shl:4
+                const int dn = __builtin_amdgcn_mov_dpp(iv, 0x114, 0xf, 0xf, true);   // row_shr:4
+                pv = hi ? dn : up;
+            } else if (k == 3) {
+                const int up = __builtin_amdgcn_mov_dpp(iv, 0x108, 0xf, 0xf, true);   // row_shl:8
+                const int dn = __builtin_amdgcn_mov_dpp(iv, 0x118, 0xf, 0xf, true);   // row_shr:8
+                pv = hi ? dn : up;
+            } else {
+                pv = __shfl_xor(iv, m);
+            }
+            const float p = __builtin_bit_cast(float, pv);
             v[r] = hi ? p - v[r] : v[r] + p;
         }
     }
