@@ -45,7 +45,9 @@ __device__ inline void fwht1024(float (&v)[4], int tid, float* xs) {
     // the partner lane l ^ m: m = 1, 2 by DPP quad permutations, m = 4, 8 by DPP row shifts
     // (the partner is in the lane's row of 16: l + m when bit m is clear, l - m when set;
     // bound_ctrl reads 0 for sources outside the row, so the unselected shift is harmless),
-    // m = 16, 32 by a cross-lane permute
+    // m = 16, 32 by a cross-lane permute.  Both shifts are computed in every lane before the
+    // select: a conditional expression with the DPP moves as operands evaluates one per lane,
+    // which becomes a branch in which the moves read disabled source lanes (zeros).
 #pragma unroll
     for (int k = 0; k < 6; k++) {
         const int m = 1 << k;
