@@ -114,7 +114,9 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
  * K % 128 == 0; any M >= 1, N >= 1.
  * The K-pieces of the last round of tiles use a workspace of the calling (device, stream)
  * (at most one fp32 256x128 tile per CU), allocated on the first call on that stream that
- * needs it and kept until the process ends; that first call must not be captured.  Calls on
+ * needs it and kept until kata_release_stream; a call that needs a larger buffer than the
+ * stream holds must not be captured, and the outgrown buffer stays allocated (graphs captured
+ * earlier may still use it).  Calls on
  * different streams use different workspaces; calls on one stream are ordered by it.  The
  * entry points that use it: kata_gemm_ptq1_f16, kata_gemm_q8_0_f16, kata_gemm_ptq1_i8 and
  * the dispatcher's prefill calls (kata_dispatch_prefill, kata_dispatch_ffn_prefill, the
@@ -194,6 +196,16 @@ int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* s
  * be captured).  Replaces k_argmax (shaders/ops.metal:66-78) after the lm_head
  * GEMV (src/engine.cpp:191-192). */
 int kata_argmax(const float* x, int n, int* out, void* stream);
+
+/* Frees the scratch buffers the library holds for the calling device and `stream` (the
+ * prefill GEMMs' K pieces, the wide GEMV's activation image, the argmax partials) after
+ * synchronising the stream.  Those buffers are kept for the stream's later calls, and a
+ * buffer outgrown by a larger call is kept too (not freed), since a HIP graph captured
+ * earlier on the stream still holds its address.  Call this before hipStreamDestroy, once
+ * no graph that recorded the stream's calls will be replayed again; a new stream that
+ * reused a destroyed one's handle would otherwise inherit its buffers.  No counterpart in
+ * the reference (its engine allocates every buffer once in load(), src/engine.cpp:48-84). */
+int kata_release_stream(void* stream);
 
 /* ---------------------------------------------------------------- HOST packers -------
  * HOST: quantize_row_ptq1_0_ref over nrow rows of k floats (k % 128 == 0)

@@ -48,6 +48,7 @@ SIGNATURES = {
     "kata_add_rms_fwht": (I, [P, P, P, P, I, I, P, P, P, I, I, I, P]),
     "kata_rms_fwht": (I, [P, P, P, P, I, I, I, I, I, P]),
     "kata_argmax": (I, [P, I, P, P]),
+    "kata_release_stream": (I, [P]),
     "kata_quantize_ptq1_0": (I, [P, P, I64, I64]),
     "kata_pack_ptq1_0": (I, [P, P, P, I64, I64]),
     "kata_gguf_open": (P, [ctypes.c_char_p]),

@@ -300,6 +300,11 @@ int kata_argmax(const float* x, int n, int* out, void* stream) {
     return check_launch(kata::launch_argmax(x, n, out, (hipStream_t)stream), "argmax");
 }
 
+// ------------------------------------------------------------------ scratch lifetime
+int kata_release_stream(void* stream) {
+    return check_launch(kata::release_stream((hipStream_t)stream), "release stream");
+}
+
 // ------------------------------------------------------------------ measurement helpers
 static int calib_wgs(int wgs) {
     if (wgs > 0) return wgs;

@@ -8,10 +8,12 @@
 namespace kata {
 
 // ---- scratch memory (workspace.cpp): the calling thread's device's CU count, and a device
-// buffer of at least `bytes` for (device, kind, stream), allocated on first use and kept
+// buffer of at least `bytes` for (device, kind, stream), allocated on first use; a buffer
+// outgrown by a larger call is retired, never freed, until release_stream(s)
 enum { kBufGemmPieces = 0, kBufArgmax = 1, kBufWideImage = 2 };
 hipError_t device_cu_count(int* n_cu);
 hipError_t stream_buffer(int kind, size_t bytes, hipStream_t s, void** p);
+hipError_t release_stream(hipStream_t s);   // synchronises s, frees every buffer of (device, s)
 
 // ---- PTQ1_0 GEMV (gemv_ptq1.hip); x 16-byte aligned, rows [T][K] or half2 [K][2] (T = 2)
 hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,

@@ -3,6 +3,8 @@ replays; serving loops capture them the same way): a graph of several launches i
 several times with other eager work and synchronisations between the replays, and every
 replay's outputs equal the eager launches' bit for bit.  The first call on the capture
 stream runs eagerly (scratch buffers are per stream and cannot be allocated under capture)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -77,3 +79,42 @@ def test_graph_prefill_gemm_with_pieces(dev):
     A = torch.from_numpy(orc.synth_x(M, K, 51)).to(dev)
     C = torch.empty((M, N), dtype=torch.float16, device=dev)
     _replays_equal_eager(dev, lambda: ops.gemm_ptq1_f16(A, W, K, N, out=C), [C])
+
+
+def test_graph_replay_after_scratch_grows(dev):
+    """A graph captured with a small wide-GEMV image (K = 5120), then an eager call on the same
+    stream that needs a larger image (K = 17408): the replays still read the buffer the graph
+    recorded (the outgrown buffer is retired, not freed) and equal the eager results bit for
+    bit; kata_release_stream then frees the stream's buffers and a later call reallocates."""
+    from kata_amd.capi import check, lib
+    Ks, Ns = (5120, 17408), (2000, 1100)
+    Ws = [torch.from_numpy(orc.synth_ptq1(N, K, 60 + i)[0]).to(dev) for i, (K, N) in enumerate(zip(Ks, Ns))]
+    xs = [torch.from_numpy(orc.synth_x(8, K, 62 + i)).to(dev) for i, K in enumerate(Ks)]
+    ys = [torch.empty((8, N), device=dev) for N in Ns]
+    cs = torch.cuda.Stream(dev)
+    with torch.cuda.stream(cs):
+        ops.gemv_ptq1_wide(Ws[0], xs[0], Ks[0], Ns[0], out=ys[0])      # eager: image for K = 5120
+    torch.cuda.synchronize()
+    ref_small = ys[0].clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        ops.gemv_ptq1_wide(Ws[0], xs[0], Ks[0], Ns[0], out=ys[0])
+    for r in range(3):
+        with torch.cuda.stream(cs):
+            ops.gemv_ptq1_wide(Ws[1], xs[1], Ks[1], Ns[1], out=ys[1])  # eager: grows the image
+        torch.cuda.synchronize()
+        big = ys[1].clone()
+        ys[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys[0], ref_small), f"replay {r} after the buffer grew"
+        if r:
+            assert torch.equal(ys[1], big)
+    del g
+    torch.cuda.synchronize()
+    check(lib().kata_release_stream(ctypes.c_void_p(cs.cuda_stream)))
+    with torch.cuda.stream(cs):
+        ops.gemv_ptq1_wide(Ws[0], xs[0], Ks[0], Ns[0], out=ys[0])      # reallocates
+    torch.cuda.synchronize()
+    assert torch.equal(ys[0], ref_small)
