@@ -262,6 +262,19 @@ __device__ inline uint32_t trit0_word(uint32_t w) {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, o3), __builtin_bit_cast(uint32_t, e3), 0x07030501u);
 }
 
+// Digit-table entry of byte value bv (< 256): the trits of digits 1..4 as int8, byte n - 1
+// for digit n.  m_n = (bv * 3^n) mod 256 for two digits at a time in 16-bit lanes (bv * 81
+// < 2^16); 3 m_n - 256 holds the trit (digit - 1) in its high byte.
+__device__ inline uint32_t trit_entry(uint32_t bv) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 b = (u16x2){(unsigned short)bv, (unsigned short)bv};
+    const u16x2 m12 = (b * (u16x2){3, 9}) & (u16x2){0xff, 0xff};
+    const u16x2 m34 = (b * (u16x2){27, 81}) & (u16x2){0xff, 0xff};
+    const u16x2 h12 = m12 * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    const u16x2 h34 = m34 * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h34), __builtin_bit_cast(uint32_t, h12), 0x07050301u);
+}
+
 // Work split ("activation-stationary").  One 1024-thread workgroup (16 waves) per CU owns
 // the contiguous tile range [wt0, wt0 + Tt) (4 rows per tile) of one matrix.  Its work
 // items (c, tile) — 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered by
@@ -315,6 +328,9 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const uint8_t* __restrict__ W = P.W[0];
     float* __restrict__ y = P.y[0];
     int N = P.N[0], tpw = P.tpw[0], ldy = P.ldy[0], wg0 = 0;
+    // the activation pointer and layout are read with the matrix fields, not later inside
+    // wave 0's branch (a second argument-load round trip before its first copy)
+    asm volatile("" ::"s"(x), "s"(x_dtype), "s"(x_layout), "s"(K), "s"(nq));
     if constexpr (MULTI) {
         const uint8_t* Wv[kMaxMats] = {P.W[0], P.W[1], P.W[2], P.W[3]};
         float* yv[kMaxMats] = {P.y[0], P.y[1], P.y[2], P.y[3]};
@@ -389,11 +405,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 #pragma unroll
     for (int i = 0; i < lut_bytes(LR) / 16 / 1024; i++) {
         const int o = tid + i * 1024;
-        const uint32_t bv = (uint32_t)o / (REPS / 4);
-        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
-                       m4 = (m3 * 3u) & 0xffu;
-        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
-                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
+        const uint32_t e = trit_entry((uint32_t)o / (REPS / 4));
         lut[o] = make_uint4(e, e, e, e);
     }
     // clear the A image (slots without an element and padding blocks stay zero) and the
@@ -786,11 +798,7 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
 #pragma unroll
     for (int i = 0; i < lut_bytes(kVwLR) / 16 / 512; i++) {
         const int o = tid + i * 512;
-        const uint32_t bv = (uint32_t)o / (REPS / 4);
-        const uint32_t m1 = (bv * 3u) & 0xffu, m2 = (m1 * 3u) & 0xffu, m3 = (m2 * 3u) & 0xffu,
-                       m4 = (m3 * 3u) & 0xffu;
-        const uint32_t e = ((((m1 * 3u) >> 8) - 1u) & 0xffu) | ((((m2 * 3u) >> 8) - 1u) & 0xffu) << 8 |
-                           ((((m3 * 3u) >> 8) - 1u) & 0xffu) << 16 | ((((m4 * 3u) >> 8) - 1u) & 0xffu) << 24;
+        const uint32_t e = trit_entry((uint32_t)o / (REPS / 4));
         lut[o] = make_uint4(e, e, e, e);
     }
 
