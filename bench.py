@@ -401,6 +401,29 @@ def run_q8(torch, ops, dev, time_reps, reps):
         us2 = time_reps(lambda r: ops.gemv_q8(Wqs[r % nq8], xq2, K, N, 2, out=yq2), max(20, reps // 4))
         q8[name].update({"t2_us": round(us2, 3), "t2_GBps": round(nb / (us2 * 1e-6) / 1e9, 1)})
         del Wqs, Wq
+    # the MTP block's shared-input launches (src/engine.cpp:361,369): wq + wk + wv and gate + up
+    # as one batched launch against their separate launches, one activation row
+    def q8_mat(N, K, seed):
+        rng = np.random.default_rng(seed)
+        blk = rng.integers(-127, 128, size=(N, K // 32, 34), dtype=np.int64).astype(np.int8).view(np.uint8)
+        blk[:, :, 0:2] = np.abs(rng.normal(0.0, 0.02, size=(N, K // 32))).astype(np.float16).view(np.uint8).reshape(N, K // 32, 2)
+        return torch.from_numpy(np.ascontiguousarray(blk).reshape(N, -1)).to(dev)
+    xq = torch.from_numpy(np.random.default_rng(SEED + 700).standard_normal((1, 5120)).astype(np.float16)).to(dev)
+    for name, Ns in (("wq_wk_wv", (12288, 1024, 1024)), ("gate_up", (17408, 17408))):
+        nb = sum(N * (5120 // 32) * 34 for N in Ns)
+        ncp = max(2, -(-512 * 1024 * 1024 // nb))
+        sets = [[q8_mat(N, 5120, SEED + 800 + 7 * i) for i, N in enumerate(Ns)]]
+        sets += [[w.clone() for w in sets[0]] for _ in range(ncp - 1)]
+        ys = [torch.empty((1, N), dtype=torch.float32, device=dev) for N in Ns]
+        us_b = time_reps(lambda r: ops.gemv_q8_batch(sets[r % ncp], xq, 5120, list(Ns), 1, outs=ys), max(20, reps // 4))
+
+        def separate(r):
+            for w, y, N in zip(sets[r % ncp], ys, Ns):
+                ops.gemv_q8(w, xq, 5120, N, 1, out=y)
+        us_s = time_reps(separate, max(20, reps // 4))
+        q8[name] = {"K": 5120, "N": list(Ns), "batched_us": round(us_b, 3), "batched_GBps": round(nb / (us_b * 1e-6) / 1e9, 1),
+                    "separate_us": round(us_s, 3), "separate_GBps": round(nb / (us_s * 1e-6) / 1e9, 1)}
+        del sets
     return q8
 
 

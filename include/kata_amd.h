@@ -107,6 +107,14 @@ size_t kata_gemv_ptq1_wide_noalloc_scratch_bytes(void);
 int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                    void* stream);
 
+/* The Q8_0 GEMV for 1..4 matrices that multiply one activation (same K), in one launch:
+ * y[i] [T][N[i]] for W[i] (W, y and N are HOST arrays of count device pointers / row
+ * counts); each matrix's results equal kata_gemv_q8_0's bit for bit.  No counterpart
+ * function in the reference, which issues one `gq` per matrix; this batches the calls of
+ * Engine::mtpRows that share an input: wq + wk + wv and gate + up (src/engine.cpp:361,369). */
+int kata_gemv_q8_0_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                         int x_dtype, int K, int T, void* stream);
+
 /* ---------------------------------------------------------------- prefill ------------
  * Exact fp16 prefill GEMM with the ternary decode fused into the LDS tile load:
  * C[m][n] = sum_k A[m][k] * half(trit[n][k] * d[n][k/128]), fp32 accumulation.
@@ -257,6 +265,13 @@ uint32_t kata_dispatch_i8_mask(const kata_dispatch* d);
 /* T=1 decode GEMV of the matrix at byte offset wOff (x fp32 [K], y fp32 [N]). */
 int kata_dispatch_gemv(kata_dispatch* d, uint64_t wOff, const float* x, float* y, int K, int N,
                        void* stream);
+/* The `gq` lambda of Engine::mtpRows (src/engine.cpp:351) over the dispatcher's weights, for
+ * 1..4 Q8_0 matrices at byte offsets offs[i] (HOST array) that read the same activation x
+ * ([T][K] fp32 or fp16, T in {1,2}) into outs[i] ([T][N[i]] fp32, HOST array of device
+ * pointers): one kata_gemv_q8_0_batch launch (the MTP block's wq + wk + wv and gate + up,
+ * src/engine.cpp:361,369; a single matrix for eh_proj, wo and down). */
+int kata_dispatch_gemv_q8(kata_dispatch* d, int count, const uint64_t* offs, const void* x, int x_dtype,
+                          float* const* outs, const int* N, int K, int T, void* stream);
 /* Prefill matmul of the named matrix: fp16 exact path, or the int8 path when selected
  * (then A is quantised into caller-provided A8 [M][K] / SX [K/128][ldS] work buffers;
  * they may be NULL when the matrix is on the fp16 path).  C fp32 [M][N]. */

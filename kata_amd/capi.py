@@ -39,6 +39,8 @@ SIGNATURES = {
     "kata_gemv_ptq1_max_k": (I, [I]),
     "kata_gemv_ptq1_batch": (I, [I, P, P, P, P, I, I, I, I, P]),
     "kata_gemv_q8_0": (I, [P, P, I, P, I, I, I, P]),
+    "kata_gemv_q8_0_batch": (I, [I, P, P, P, P, I, I, I, P]),
+    "kata_dispatch_gemv_q8": (I, [P, I, P, P, I, P, P, I, I, P]),
     "kata_gemm_ptq1_f16": (I, [P, I, P, P, I, I, I, I, I, P]),
     "kata_gemm_q8_0_f16": (I, [P, I, P, P, I, I, I, I, I, P]),
     "kata_quant_rows_i8": (I, [P, P, P, I, I, I, P]),

@@ -165,6 +165,24 @@ int kata_gemv_q8_0(const uint8_t* W, const void* x, int x_dtype, float* y, int K
     return check_launch(kata::launch_gemv_q8(W, x, x_dtype, y, K, N, T, (hipStream_t)stream), "gemv q8_0");
 }
 
+int kata_gemv_q8_0_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x, int x_dtype,
+                         int K, int T, void* stream) {
+    if (count < 1 || count > kata::gemv_q8_max_mats())
+        return fail(KATA_EINVAL, "count=%d must be 1..%d", count, kata::gemv_q8_max_mats());
+    if (!W || !y || !N || !x) return fail(KATA_EINVAL, "null argument");
+    if (K <= 0 || K % 32 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 32", K);
+    if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
+    for (int i = 0; i < count; i++) {
+        if (!W[i] || !y[i]) return fail(KATA_EINVAL, "null matrix or output %d", i);
+        if (N[i] <= 0) return fail(KATA_EINVAL, "N[%d]=%d must be positive", i, N[i]);
+        if (!aligned(W[i], 2)) return fail(KATA_EINVAL, "W[%d] must be 2-byte aligned", i);
+    }
+    return check_launch(kata::launch_gemv_q8_multi(count, W, y, N, x, x_dtype, K, T, (hipStream_t)stream),
+                        "gemv q8_0 batch");
+}
+
 // ------------------------------------------------------------------ prefill
 int kata_gemm_ptq1_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc, int M, int K,
                        int N, void* stream) {
@@ -457,6 +475,16 @@ uint32_t kata_dispatch_i8_mask(const kata_dispatch* d) { return d ? d->i8_mask :
 int kata_dispatch_gemv(kata_dispatch* d, uint64_t wOff, const float* x, float* y, int K, int N, void* stream) {
     if (!d) return fail(KATA_EINVAL, "null dispatcher");
     return kata_gemv_ptq1(d->wbase + wOff, x, KATA_F32, KATA_X_ROWS, y, K, N, 1, stream);
+}
+
+int kata_dispatch_gemv_q8(kata_dispatch* d, int count, const uint64_t* offs, const void* x, int x_dtype,
+                          float* const* outs, const int* N, int K, int T, void* stream) {
+    if (!d || !offs) return fail(KATA_EINVAL, "null argument");
+    if (count < 1 || count > kata::gemv_q8_max_mats())
+        return fail(KATA_EINVAL, "count=%d must be 1..%d", count, kata::gemv_q8_max_mats());
+    const uint8_t* W[4];
+    for (int i = 0; i < count; i++) W[i] = d->wbase + offs[i];
+    return kata_gemv_q8_0_batch(count, W, outs, N, x, x_dtype, K, T, stream);
 }
 
 int kata_dispatch_prefill(kata_dispatch* d, uint64_t wOff, const uint16_t* A, float* C, int M, int K, int N,

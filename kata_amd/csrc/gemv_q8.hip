@@ -17,6 +17,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <algorithm>
+
 namespace kata {
 
 namespace {
@@ -56,20 +58,55 @@ __device__ inline void load_x32(const void* x, int K, int b, float (&xv)[T][32])
     }
 }
 
-// Workgroup = 4 waves = (4 / KS) row groups x KS slices of the row's blocks.
-template <int T, bool XH, int KS, int R>
-__global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t* __restrict__ W, uint32_t w_off, uint32_t w_bytes,
-                                                 const void* __restrict__ x, float* __restrict__ y, int K, int N) {
-    constexpr int GROUPS = 4 / KS;
+constexpr int kQ8MaxMats = 4;
+
+// The 1..4 matrices of one launch (same K, same activation): matrix i is W[i] - w_off[i]
+// (its dword-aligned base; w_off[i] = W[i] & 3) with N[i] rows and w_bytes[i] bytes from that
+// base, output y[i] [T][N[i]]; workgroups [wg0[i], wg0[i+1]) serve it.
+struct Q8Mats {
+    const uint8_t* W[kQ8MaxMats];
+    float* y[kQ8MaxMats];
+    int N[kQ8MaxMats];
+    uint32_t w_off[kQ8MaxMats];
+    uint32_t w_bytes[kQ8MaxMats];
+    int lks[kQ8MaxMats];                         // log2 of the matrix's K slices per row group
+    int wg0[kQ8MaxMats + 1];
+    int count;
+};
+
+// Workgroup = 4 waves = (4 / KS) row groups x KS slices of the row's blocks (KS per matrix,
+// the same as a launch of that matrix alone, so a batch equals the single launches bit for bit).
+template <int T, bool XH, int R, bool MULTI>
+__global__ __launch_bounds__(256) void k_gemv_q8(Q8Mats P, const void* __restrict__ x, int K) {
     __shared__ float red[4][T][R];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = wave / KS, ks = wave % KS;
-    const int row0 = (blockIdx.x * GROUPS + grp) * R;
+    // this workgroup's matrix: every field is read before one is selected (no branches
+    // around dependent argument loads)
+    const uint8_t* __restrict__ W = P.W[0];
+    float* __restrict__ y = P.y[0];
+    int N = P.N[0], wg0 = 0, lks = P.lks[0];
+    uint32_t w_off = P.w_off[0], w_bytes = P.w_bytes[0];
+    if constexpr (MULTI) {
+#pragma unroll
+        for (int i = 1; i < kQ8MaxMats; i++) {
+            const bool sel = i < P.count && (int)blockIdx.x >= P.wg0[i];
+            W = sel ? P.W[i] : W;
+            y = sel ? P.y[i] : y;
+            N = sel ? P.N[i] : N;
+            w_off = sel ? P.w_off[i] : w_off;
+            w_bytes = sel ? P.w_bytes[i] : w_bytes;
+            lks = sel ? P.lks[i] : lks;
+            wg0 = sel ? P.wg0[i] : wg0;
+        }
+    }
+    const int KS = 1 << lks, GROUPS = 4 >> lks;
+    const int grp = wave >> lks, ks = wave & (KS - 1);
+    const int row0 = (((int)blockIdx.x - wg0) * GROUPS + grp) * R;
     const int nb = K / kQ8Group;
     const int b0 = (ks * nb) / KS, b1 = ((ks + 1) * nb) / KS;
     const uint32_t row_bytes = (uint32_t)nb * kQ8BlockBytes;
     // W as a raw buffer from its dword-aligned base (w_off = W & 3); exact bounds
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(W - w_off), 0, (int)w_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)w_bytes, 0x00020000);
 
     float acc[T][R];
 #pragma unroll
@@ -194,24 +231,15 @@ __global__ __launch_bounds__(256) void k_gemv_q8(const uint8_t* __restrict__ W, 
         const int t = lane / R, r = lane % R;
         float v = 0.0f;
 #pragma unroll
-        for (int k2 = 0; k2 < KS; k2++) v += red[wave + k2][t][r];
+        for (int k2 = 0; k2 < 4; k2++)
+            if (k2 < KS) v += red[wave + k2][t][r];
         if (row0 + r < N) y[(size_t)t * N + row0 + r] = v;
     }
 }
 
-template <int T, bool XH, int KS, int R>
-void launch_q8_k(const uint8_t* W, uint32_t w_off, uint32_t w_bytes, const void* x, float* y, int K, int N,
-                 hipStream_t s) {
-    const int groups = (N + R - 1) / R;
-    const int wgs = (groups + 4 / KS - 1) / (4 / KS);
-    hipLaunchKernelGGL((k_gemv_q8<T, XH, KS, R>), dim3(wgs), dim3(256), 0, s, W, w_off, w_bytes, x, y, K, N);
-}
-
 template <int T, bool XH>
-hipError_t launch_q8_t(const uint8_t* W, const void* x, float* y, int K, int N, hipStream_t s) {
+hipError_t launch_q8_t(Q8Mats& P, const void* x, int K, hipStream_t s) {
     const int nb = K / kQ8Group;
-    const uint32_t w_off = (uint32_t)((uintptr_t)W & 3);
-    const uint32_t w_bytes = w_off + (uint32_t)N * (uint32_t)nb * kQ8BlockBytes;
     // one fp16 row (v_dot2 form, little VALU per byte): 2 rows per wave, twice the waves of
     // 4 (17408 x 5120: 26.1 -> 20.9 us); two rows (fp32 FMAs per quant and token) keep 4 rows
     // per wave to reuse each block's activations (2 rows per wave: 28.5 -> 32.2 us).  Rows
@@ -220,19 +248,46 @@ hipError_t launch_q8_t(const uint8_t* W, const void* x, float* y, int K, int N, 
     // the one-slice grid would be small (5120 x 1024: 6.7 -> 3.7 us); at T = 2 rows of >= 128
     // blocks over 4.
     constexpr int R = T == 1 ? 2 : 4;
-    if (T == 1 && nb >= 256) launch_q8_k<T, XH, 2, R>(W, w_off, w_bytes, x, y, K, N, s);
-    else if (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) launch_q8_k<T, XH, 4, R>(W, w_off, w_bytes, x, y, K, N, s);
-    else launch_q8_k<T, XH, 1, R>(W, w_off, w_bytes, x, y, K, N, s);
+    P.wg0[0] = 0;
+    for (int i = 0; i < P.count; i++) {
+        const int N = P.N[i];
+        P.lks[i] = (T == 1 && nb >= 256) ? 1 : (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) ? 2 : 0;
+        const int rpw = R * (4 >> P.lks[i]);     // rows per workgroup
+        P.wg0[i + 1] = P.wg0[i] + (N + rpw - 1) / rpw;
+    }
+    for (int i = P.count; i < kQ8MaxMats; i++) P.wg0[i + 1] = P.wg0[P.count];
+    if (P.count > 1)
+        hipLaunchKernelGGL((k_gemv_q8<T, XH, R, true>), dim3(P.wg0[P.count]), dim3(256), 0, s, P, x, K);
+    else
+        hipLaunchKernelGGL((k_gemv_q8<T, XH, R, false>), dim3(P.wg0[P.count]), dim3(256), 0, s, P, x, K);
     return hipGetLastError();
 }
 
 }  // namespace
 
+int gemv_q8_max_mats() { return kQ8MaxMats; }
+
+hipError_t launch_gemv_q8_multi(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                int x_dtype, int K, int T, hipStream_t s) {
+    if (count < 1 || count > kQ8MaxMats) return hipErrorInvalidValue;
+    const size_t nb = (size_t)(K / kQ8Group);
+    Q8Mats P{};
+    P.count = count;
+    for (int i = 0; i < count; i++) {
+        if ((size_t)N[i] * nb * kQ8BlockBytes + 4 > 0x7fffffffu) return hipErrorInvalidValue;
+        P.w_off[i] = (uint32_t)((uintptr_t)W[i] & 3);
+        P.W[i] = W[i] - P.w_off[i];
+        P.y[i] = y[i];
+        P.N[i] = N[i];
+        P.w_bytes[i] = P.w_off[i] + (uint32_t)((size_t)N[i] * nb * kQ8BlockBytes);
+    }
+    if (T == 1) return x_dtype == 1 ? launch_q8_t<1, true>(P, x, K, s) : launch_q8_t<1, false>(P, x, K, s);
+    return x_dtype == 1 ? launch_q8_t<2, true>(P, x, K, s) : launch_q8_t<2, false>(P, x, K, s);
+}
+
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                           hipStream_t s) {
-    if ((size_t)N * (size_t)(K / kQ8Group) * kQ8BlockBytes + 4 > 0x7fffffffu) return hipErrorInvalidValue;
-    if (T == 1) return x_dtype == 1 ? launch_q8_t<1, true>(W, x, y, K, N, s) : launch_q8_t<1, false>(W, x, y, K, N, s);
-    return x_dtype == 1 ? launch_q8_t<2, true>(W, x, y, K, N, s) : launch_q8_t<2, false>(W, x, y, K, N, s);
+    return launch_gemv_q8_multi(1, &W, &y, &N, x, x_dtype, K, T, s);
 }
 
 }  // namespace kata

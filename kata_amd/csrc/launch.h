@@ -34,9 +34,12 @@ hipError_t launch_gemv_wide_batch(int count, const uint8_t* const* W, float* con
                                   int x_dtype, int K, int T, hipStream_t s);
 size_t gemv_wide_noalloc_scratch_bytes();
 
-// ---- Q8_0 GEMV (gemv_q8.hip)
+// ---- Q8_0 GEMV (gemv_q8.hip); the batch form: 1..gemv_q8_max_mats() matrices sharing x
 hipError_t launch_gemv_q8(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                           hipStream_t s);
+hipError_t launch_gemv_q8_multi(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
+                                int x_dtype, int K, int T, hipStream_t s);
+int gemv_q8_max_mats();
 
 // ---- prefill (gemm_f16.hip, gemm_i8.hip, expand.hip)
 hipError_t launch_gemm_f16(const uint16_t* A, int lda, const uint8_t* W, void* C, int c_dtype, int ldc,

@@ -62,6 +62,16 @@ class Dispatch:
     def gemv(self, wOff: int, x: torch.Tensor, y: torch.Tensor, K: int, N: int) -> None:
         check(lib().kata_dispatch_gemv(self._h, wOff, _ptr(x), _ptr(y), K, N, _stream(self.wbuf)))
 
+    def gemv_q8(self, offs, x: torch.Tensor, outs, K: int, Ns) -> None:
+        """The MTP block's `gq` (src/engine.cpp:351) for 1..4 Q8_0 matrices reading x [T][K]."""
+        n = len(offs)
+        T = x.shape[0]
+        oa = (ctypes.c_uint64 * n)(*offs)
+        ya = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        Na = (ctypes.c_int * n)(*Ns)
+        check(lib().kata_dispatch_gemv_q8(self._h, n, oa, _ptr(x), 1 if x.dtype == torch.float16 else 0, ya, Na, K, T,
+                                          _stream(self.wbuf)))
+
     def prefill(self, wOff: int, A: torch.Tensor, C: torch.Tensor, K: int, N: int, name: str,
                 A8: torch.Tensor | None = None, SX: torch.Tensor | None = None) -> None:
         M = A.shape[0]

@@ -134,6 +134,26 @@ def gemv_q8(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1,
     return y
 
 
+def gemv_q8_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, outs=None):
+    """Q8_0 GEMVs of up to 4 matrices sharing the activation x [T][K], one launch: returns [y_i]."""
+    if len(Ws) != len(Ns) or (outs is not None and len(outs) != len(Ns)):
+        raise ValueError("Ws, Ns (and outs) must have the same length")
+    if K <= 0 or K % Q8_GROUP:
+        raise ValueError(f"K={K} must be a positive multiple of {Q8_GROUP}")
+    for i, (W, N) in enumerate(zip(Ws, Ns)):
+        _need_bytes(f"Ws[{i}]", W, N * (K // Q8_GROUP) * Q8_BLOCK_BYTES)
+        _need_bytes(f"outs[{i}]", outs[i] if outs is not None else None, T * N * 4)
+    _need_bytes("x", x, T * K * x.element_size())
+    _need_gpu(x, *Ws)
+    n = len(Ws)
+    ys = outs if outs is not None else [torch.empty((T, N), dtype=torch.float32, device=x.device) for N in Ns]
+    Wa = (ctypes.c_void_p * n)(*[W.data_ptr() for W in Ws])
+    ya = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    Na = (ctypes.c_int * n)(*Ns)
+    check(lib().kata_gemv_q8_0_batch(n, Wa, ya, Na, _ptr(x), _xdtype(x), K, T, _stream(x)))
+    return ys
+
+
 # ----------------------------------------------------------------------------- prefill
 def gemm_ptq1_f16(A: torch.Tensor, W: torch.Tensor, K: int, N: int, out_dtype=torch.float32,
                   out: torch.Tensor | None = None) -> torch.Tensor:

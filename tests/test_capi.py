@@ -232,6 +232,30 @@ def test_gemv_wide_batch_rejects():
     assert call(2, W2, arr(ctypes.c_void_p, [FAKE.value, None]), N2, p, 1, 1024, 4, None) == KATA_EINVAL
 
 
+def test_gemv_q8_batch_rejects():
+    lib = L.lib()
+    p = FAKE
+
+    def arr(ctype, vals):
+        return (ctype * len(vals))(*vals)
+
+    W2 = arr(ctypes.c_void_p, [FAKE.value, FAKE.value])
+    y2 = arr(ctypes.c_void_p, [FAKE.value, FAKE.value])
+    N2 = arr(ctypes.c_int, [16, 32])
+    call = lib.kata_gemv_q8_0_batch
+    assert call(0, W2, y2, N2, p, 1, 1024, 1, None) == KATA_EINVAL            # count
+    assert call(5, W2, y2, N2, p, 1, 1024, 1, None) == KATA_EINVAL
+    assert call(2, W2, y2, N2, p, 1, 1024, 3, None) == KATA_EINVAL            # T
+    assert call(2, W2, y2, N2, p, 1, 1000, 1, None) == KATA_EINVAL            # K % 32
+    assert call(2, W2, y2, N2, p, 7, 1024, 1, None) == KATA_EINVAL            # x dtype
+    assert call(2, W2, y2, N2, ctypes.c_void_p(0x10008), 1, 1024, 1, None) == KATA_EINVAL
+    assert call(2, None, y2, N2, p, 1, 1024, 1, None) == KATA_EINVAL
+    assert call(2, W2, y2, arr(ctypes.c_int, [16, 0]), p, 1, 1024, 1, None) == KATA_EINVAL
+    assert call(2, arr(ctypes.c_void_p, [FAKE.value, 0x10001]), y2, N2, p, 1, 1024, 1, None) == KATA_EINVAL
+    assert call(2, W2, arr(ctypes.c_void_p, [FAKE.value, None]), N2, p, 1, 1024, 1, None) == KATA_EINVAL
+    assert lib.kata_dispatch_gemv_q8(None, 1, arr(ctypes.c_uint64, [0]), p, 1, y2, N2, 1024, 1, None) == KATA_EINVAL
+
+
 def test_fwht_rejects_aliasing():
     """An output overlapping an input is rejected before any launch (workgroups re-read their
     row while others write theirs); no GPU is needed for the argument checks."""
