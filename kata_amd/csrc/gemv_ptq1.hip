@@ -38,8 +38,9 @@ namespace kata {
 namespace {
 
 constexpr float kQMax = 32639.0f;   // |q| <= 32639 keeps hi = (q+128)>>8 inside int8
-constexpr int kMfmaPerBlock = 3;
-constexpr int kAImageBytes = kMfmaPerBlock * 4 * 16;   // per block and A row (token, limb)
+constexpr int kMfmaPerBlock = 3;   // the wide verification GEMV's operand layout
+constexpr int kDenseMfma = 2;      // the decode GEMV's dense layout: 32 trits per lane group
+constexpr int kAImageBytes = kDenseMfma * 4 * 16;   // per block and A row (token, limb)
 constexpr int kWaves = 16;
 constexpr int kChunkMax = 3;   // 8-element activation chunks per thread: K <= 3 * 8 * 1024
 constexpr int kMaxMats = 4;    // matrices sharing one activation in one launch
@@ -82,8 +83,39 @@ __host__ __device__ constexpr int gemv_elem_img_off(int e, int kq, int T) {
     return (kind >> 2) * (4 * 2 * T * 16) + g * (2 * T * 16) + (kind & 3) * 4 + kb;
 }
 
+// The decode GEMV's dense layout: lane group g of a B column (one row, one block) holds the
+// 32 trits of qs bytes 6g .. 6g + 5 (all five digits) and two digits of qh byte 24 + (g >> 1)
+// (digits 2(g & 1) and 2(g & 1) + 1), so two MFMAs cover the block's 128 trits with no empty
+// slot.  With c0..c5 the lane's six qs bytes the B dwords are
+//   m=0: L(c0) L(c1) L(c2) L(c3)      m=1: L(c4) L(c5) Z(c0..c3) {Z(c4), Z(c5), Q(a), Q(a+1)}
+// (L = digits 1..4, byte n - 1 for digit n; Z = digit 0; Q = the qh digits).  The lane reads
+// the 8 bytes at 4-byte aligned gemv_dense_byte0(g) (c0 at byte offset 2 (g & 1)) and the
+// dword at block byte 24 (qh and the scale).  Offset of element e in the block's A image
+// [m 2][g 4][i 2T][16 B]:
+__host__ __device__ constexpr int gemv_dense_byte0(int g) { return g == 0 ? 0 : g == 1 ? 4 : g == 2 ? 12 : 16; }
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+__host__ __device__ constexpr int gemv_dense_img_off(int e, int T) {
+    int p = 0, n = 0;
+    ptq1_elem_src(e, p, n);
+    int g = 0, m = 1, slot = 0;
+    if (p < 24) {
+        g = p / 6;
+        const int j = p - 6 * g;
+        if (n > 0) {
+            m = j < 4 ? 0 : 1;
+            slot = 4 * (j & 3) + n - 1;
+        } else {
+            slot = 8 + j;
+        }
+    } else {
+        g = 2 * (p - 24) + (n >> 1);
+        slot = 14 + (n & 1);
+    }
+    return m * (4 * 2 * T * 16) + g * (2 * T * 16) + slot;
+}
+
 // Image offsets of the 8 elements a quantising thread owns: thread index & 63 =
-// 16*kq + sub, elements 8*sub .. 8*sub + 7 of a block with quarter kq; [T - 1][idx][e].
+// 16*kq + sub, elements 8*sub .. 8*sub + 7 of a block; [T - 1][idx][e].
 struct alignas(16) ImgOffTable {
     uint16_t v[2][64][8];
 };
@@ -91,7 +123,7 @@ constexpr ImgOffTable make_img_off_table() {
     ImgOffTable t{};
     for (int T = 1; T <= 2; T++)
         for (int idx = 0; idx < 64; idx++)
-            for (int e = 0; e < 8; e++) t.v[T - 1][idx][e] = (uint16_t)gemv_elem_img_off(8 * (idx & 15) + e, idx >> 4, T);
+            for (int e = 0; e < 8; e++) t.v[T - 1][idx][e] = (uint16_t)gemv_dense_img_off(8 * (idx & 15) + e, T);
     return t;
 }
 __constant__ ImgOffTable kImgOff = make_img_off_table();
@@ -107,6 +139,15 @@ __device__ inline uint32_t lut_addr(uint32_t w, int q, uint32_t laneoff) {
     return (((w >> (8 * q)) & 0xffu) << (LR + 2)) | laneoff;
 }
 __host__ __device__ constexpr int lut_bytes(int LR) { return 256 * (4 << LR); }
+// The same address for byte q of w where q is a per-lane value: sel = lut_sel<LR>(q)
+// (the v_perm selector for LR = 6), computed once per lane.
+template <int LR>
+__host__ __device__ constexpr uint32_t lut_sel(uint32_t q) { return 0x0c0c0400u | ((4u + q) << 8); }
+template <int LR>
+__device__ inline uint32_t lut_addr_sel(uint32_t w, uint32_t sel, uint32_t q, uint32_t laneoff) {
+    if (LR == 6) return __builtin_amdgcn_perm(w, laneoff, sel);
+    return (((w >> (8 * q)) & 0xffu) << (LR + 2)) | laneoff;
+}
 
 typedef __attribute__((address_space(3))) const uint8_t lds_u8;
 // 32-bit load at byte offset addr of an LDS array; for the digit table, the kernel's first
@@ -310,7 +351,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 #pragma clang fp contract(off)
     static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by item parity");
     constexpr int ASTRIDE = 4 * 2 * T * 16;      // A image bytes per (virtual block, MFMA)
-    constexpr int BLK = kMfmaPerBlock * ASTRIDE;  // A image bytes per virtual block
+    constexpr int BLK = kDenseMfma * ASTRIDE;     // A image bytes per virtual block
     constexpr int REPS = 1 << LR;
     constexpr int QPAD = gemv_qpad(T);
     // trit table first: the kernel's static LDS starts at address 0
@@ -414,14 +455,15 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     for (int o = nb * T + tid; o < nbv * T; o += 1024) ((int2*)Ss)[o] = make_int2(0, 0);
 
     // (1c) weight ring.  Raw buffer loads: per-lane offset (row r of the tile, block kq of
-    // the step, the lane group's segment) plus a wave-uniform item offset; bytes past the
-    // matrix read as 0 (rows >= N; with PAD also the padding blocks of the last row).
-    // Loads past the run's end use an offset beyond the buffer: zeros, no memory access.
+    // the step, the lane group's 8 bytes, and the block's qh / scale dword) plus a
+    // wave-uniform item offset; bytes past the matrix read as 0 (rows >= N; with PAD also the
+    // padding blocks of the last row).  Loads past the run's end use an offset beyond the
+    // buffer: zeros, no memory access.
     const uint32_t row_bytes = (uint32_t)nb * kBlockBytes;
     const uint32_t tstep = 4 * row_bytes;        // next tile
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
-    const uint32_t voff = (uint32_t)r * row_bytes + (uint32_t)kq * kBlockBytes + (uint32_t)gemv_seg_byte0((g - kq) & 3);
+    const uint32_t voff = (uint32_t)r * row_bytes + (uint32_t)kq * kBlockBytes + (uint32_t)gemv_dense_byte0(g);
     // item s = (c/2, tile, c%2): pair index s / (2 Tt), tile (s % (2 Tt)) / 2, block step
     // parity s % 2; runs start at even s, so the ring slot's parity is the item's
     int lt = strided ? sh : (s0 % (2 * Tt)) >> 1;   // load cursor: tile, item offset, items left
@@ -431,10 +473,13 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     const uint32_t cstep = 4 * kBlockBytes;      // even c -> c + 1, same tile
     const uint32_t tnext = (strided ? G : 1) * tstep - cstep;    // odd c -> c - 1, next tile
     const uint32_t cwrap = cstep - (uint32_t)(Tt - 1) * tstep;   // odd c, last tile -> next pair
-    uint32_t wl[D], wh[D];
+    // 12 bytes per lane: lane group 3's third dword is the block's bytes 24..27 (qh, scale),
+    // which the other lane groups of the column take from it by a cross-lane permute
+    uint32_t wl[D], wh[D], wq[D];
     auto load_next = [&](int slot) {
         const uint32_t so = lrem > 0 ? lso : 0x80000000u;
-        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrsrc, (int)voff, (int)so, 0));
+        const u32x3 w = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(wrsrc, (int)voff, (int)so, 0));
+        wq[slot] = w.z;
         wl[slot] = w.x;
         wh[slot] = w.y;
         if (slot & 1) {
@@ -529,39 +574,53 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
                          : Js + lane * 4;
     const uint32_t pinc = diag * (D / 2) * pstep;
     float vprev[T];
-    v4i A[2][kMfmaPerBlock];                     // block steps 2 cp and 2 cp + 1
+    v4i A[2][kDenseMfma];                        // block steps 2 cp and 2 cp + 1
     float sc[2][T];
     auto load_a = [&](int cp) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int c = 2 * cp + h;
 #pragma unroll
-            for (int m = 0; m < kMfmaPerBlock; m++) A[h][m] = *(const v4i*)(xa + c * BLK + m * ASTRIDE);
+            for (int m = 0; m < kDenseMfma; m++) A[h][m] = *(const v4i*)(xa + c * BLK + m * ASTRIDE);
 #pragma unroll
             for (int t = 0; t < T; t++) sc[h][t] = xs[c * 8 * T + 2 * t];
         }
     };
-    auto decode = [&](uint32_t w0, uint32_t w1, v4i* B) {
-        B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 1, laneoff)),
-                   (int)lds_u32(lb, lut_addr<LR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w0, 3, laneoff))};
-        B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<LR>(w1, 0, laneoff)),
-                   (int)lds_u32(lb, lut_addr<LR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<LR>(w1, 2, laneoff))};
-        B[2][0] = (int)lds_u32(lb, lut_addr<LR>(w1, 3, laneoff));   // B[2][2..3] stay zero
-        B[2][1] = (int)trit0_word(w1);
+    // Dense decode (the layout at gemv_dense_img_off).  Per-lane constants: the byte shift of
+    // c0 in the 8 loaded bytes (2 (g & 1)), the perm selectors that take c4, c5 and the qh
+    // byte, and the multipliers 3^a, 3^(a+1) of the lane's two qh digits (a = 2 (g & 1)).
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t csh = 2u * (uint32_t)(g & 1);
+    const uint32_t sel_c4 = lut_sel<LR>(csh), sel_c5 = lut_sel<LR>(csh + 1);
+    const uint32_t sel_z45 = 0x0c000c00u | ((csh + 1) << 16) | csh;      // (c4, 0, c5, 0)
+    const uint32_t qb = (uint32_t)(g >> 1);
+    const uint32_t sel_q = 0x0c000c00u | (qb << 16) | qb;                // (qh, 0, qh, 0)
+    const u16x2 qmul = (g & 1) ? (u16x2){9, 27} : (u16x2){1, 3};
+    const int qsrc = (lane | 48) << 2;
+    auto decode = [&](uint32_t w0, uint32_t w1, uint32_t& wqv, v4i* B) {
+        wqv = (uint32_t)__builtin_amdgcn_ds_bpermute(qsrc, (int)wqv);   // block bytes 24..27
+        const uint32_t c03 = __builtin_amdgcn_alignbyte(w1, w0, csh);     // c0..c3
+        B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(c03, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(c03, 1, laneoff)),
+                   (int)lds_u32(lb, lut_addr<LR>(c03, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(c03, 3, laneoff))};
+        const u16x2 z45 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w1, sel_z45)) * (u16x2){3, 3} +
+                          (u16x2){0xff00, 0xff00};
+        const u16x2 mq = (__builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, wqv, sel_q)) * qmul) & (u16x2){0xff, 0xff};
+        const u16x2 hq = mq * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+        B[1] = v4i{(int)lds_u32(lb, lut_addr_sel<LR>(w1, sel_c4, csh, laneoff)),
+                   (int)lds_u32(lb, lut_addr_sel<LR>(w1, sel_c5, csh + 1, laneoff)), (int)trit0_word(c03),
+                   (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hq), __builtin_bit_cast(uint32_t, z45), 0x07050301u)};
     };
     int ct = strided ? 0 : (s0 % (2 * Tt)) >> 1, cp = strided ? sp : s0 / (2 * Tt);   // compute cursor: tile, pair
-    v4i B0[kMfmaPerBlock], B1[kMfmaPerBlock];
-    B0[2] = v4i{0, 0, 0, 0};
-    B1[2] = v4i{0, 0, 0, 0};
+    v4i B0[kDenseMfma], B1[kDenseMfma];
     // item in ring slot u; `next`: item + 1 is in the run (its operands are read here)
     auto body = [&](auto uc, bool next) {
         constexpr int u = decltype(uc)::value;
-        if (next) decode(wl[(u + 1) % D], wh[(u + 1) % D], (u & 1) ? B0 : B1);
+        if (next) decode(wl[(u + 1) % D], wh[(u + 1) % D], wq[(u + 1) % D], (u & 1) ? B0 : B1);
         const v4i* B = (u & 1) ? B1 : B0;
         v4i Dm = {0, 0, 0, 0};
 #pragma unroll
-        for (int m = 0; m < kMfmaPerBlock; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
-        float d = half_bits_to_float(wh[u] >> 16);
+        for (int m = 0; m < kDenseMfma; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
+        float d = half_bits_to_float(wq[u] >> 16);
         if (PAD && 4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
         float* dst = (float*)(pcur + (u >> 1) * pstep);
 #pragma unroll
@@ -582,7 +641,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     };
     if (n > 0) {
         load_a(cp);
-        decode(wl[0], wh[0], B0);
+        decode(wl[0], wh[0], wq[0], B0);
     }
     int j = 0;
     for (; j + D < n; j += D) {                  // full passes: every item has a successor
