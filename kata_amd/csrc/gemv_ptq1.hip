@@ -837,23 +837,41 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
     const int xn = lane & 15, g = lane >> 4;
     const int nb = K >> 7;
     const size_t row_bytes = (size_t)nb * kBlockBytes;
-    const int tw0 = (int)(((long long)blockIdx.x * total_tiles) / gridDim.x);
-    const int Tt = (int)(((long long)(blockIdx.x + 1) * total_tiles) / gridDim.x) - tw0;
+    // balanced split of the tiles: the first total % grid workgroups take one tile more (32-bit
+    // arithmetic; a 64-bit division here was a long software sequence at kernel start)
+    const int tq = total_tiles / (int)gridDim.x, tr = total_tiles - tq * (int)gridDim.x;
+    const int bx = (int)blockIdx.x;
+    const int tw0 = bx * tq + min(bx, tr);
+    const int Tt = tq + (bx < tr ? 1 : 0);
 
     // per tile slot: this lane's row (clamped to the matrix: rows past it read its last row,
     // whose results are not stored) at its segment of block 0
+    // (every matrix field is read once, up front, and selected by value: indexing the
+    // kernel arguments with a tile's matrix index made a chain of dependent argument loads)
+    const uint8_t* Wv[kMaxMats] = {P.W[0], P.W[1], P.W[2], P.W[3]};
+    int Nv[kMaxMats] = {P.N[0], P.N[1], P.N[2], P.N[3]};
+    int t0v[kMaxMats] = {P.t0[0], P.t0[1], P.t0[2], P.t0[3]};
+    const int cnt = P.count;
+    asm volatile("" ::"s"(Wv[0]), "s"(Wv[1]), "s"(Wv[2]), "s"(Wv[3]), "s"(Nv[0]), "s"(Nv[1]), "s"(Nv[2]), "s"(Nv[3]));
+    asm volatile("" ::"s"(t0v[1]), "s"(t0v[2]), "s"(t0v[3]), "s"(cnt));
     const uint8_t* wp[kVwTMax];
 #pragma unroll
     for (int t = 0; t < kVwTMax; t++) {
         const int gt = tw0 + min(t, Tt - 1);
-        int mi = 0;
+        const uint8_t* Wm = Wv[0];
+        int Nm = Nv[0], t0m = t0v[0];
 #pragma unroll
-        for (int i = 1; i < kMaxMats; i++) mi = (i < P.count && gt >= P.t0[i]) ? i : mi;
-        const int row = min((gt - P.t0[mi]) * 16 + xn, P.N[mi] - 1);
-        wp[t] = P.W[mi] + (size_t)row * row_bytes + gemv_seg_byte0(g);
+        for (int i = 1; i < kMaxMats; i++) {
+            const bool sel = i < cnt && gt >= t0v[i];
+            Wm = sel ? Wv[i] : Wm;
+            Nm = sel ? Nv[i] : Nm;
+            t0m = sel ? t0v[i] : t0m;
+        }
+        const int row = min((gt - t0m) * 16 + xn, Nm - 1);
+        wp[t] = Wm + (size_t)row * row_bytes + gemv_seg_byte0(g);
     }
 
-    // trit table (visible after the first chunk's barrier)
+    // trit table (visible after the LDS-only barrier in the first chunk)
 #pragma unroll
     for (int i = 0; i < lut_bytes(kVwLR) / 16 / 512; i++) {
         const int o = tid + i * 512;
@@ -900,6 +918,12 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
                     wl[t][bb] = w.x;
                     wh[t][bb] = w.y;
                 }
+            if (kb0 == 0) {                      // every wave runs the same chunks: uniform
+                // the trit table (built before the loads) is visible to every wave after
+                // this LDS-only barrier
+                __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+                __builtin_amdgcn_s_barrier();
+            }
             static_for<TT>([&](auto tc) {
                 constexpr int t = decltype(tc)::value;
 #pragma unroll
@@ -957,18 +981,26 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
         }
     }
     if (wave == 0) {
+        float* yv[kMaxMats] = {P.y[0], P.y[1], P.y[2], P.y[3]};
+        const int ldv[kMaxMats] = {P.ldy[0], P.ldy[1], P.ldy[2], P.ldy[3]};
 #pragma unroll
         for (int t = 0; t < kVwTMax; t++) {
             if (t < Tt) {
                 const int gt = tw0 + t;
-                int mi = 0;
+                float* yy = yv[0];
+                int Nm = Nv[0], t0m = t0v[0], ldm = ldv[0];
 #pragma unroll
-                for (int i = 1; i < kMaxMats; i++) mi = (i < P.count && gt >= P.t0[i]) ? i : mi;
-                const int row = (gt - P.t0[mi]) * 16 + xn;
-                if (row < P.N[mi]) {
-                    float* yy = P.y[mi];
-                    if (2 * g < T) yy[(size_t)(2 * g) * P.ldy[mi] + row] = acc[t][0];
-                    if (2 * g + 1 < T) yy[(size_t)(2 * g + 1) * P.ldy[mi] + row] = acc[t][1];
+                for (int i = 1; i < kMaxMats; i++) {
+                    const bool sel = i < cnt && gt >= t0v[i];
+                    yy = sel ? yv[i] : yy;
+                    Nm = sel ? Nv[i] : Nm;
+                    t0m = sel ? t0v[i] : t0m;
+                    ldm = sel ? ldv[i] : ldm;
+                }
+                const int row = (gt - t0m) * 16 + xn;
+                if (row < Nm) {
+                    if (2 * g < T) yy[(size_t)(2 * g) * ldm + row] = acc[t][0];
+                    if (2 * g + 1 < T) yy[(size_t)(2 * g + 1) * ldm + row] = acc[t][1];
                 }
             }
         }
