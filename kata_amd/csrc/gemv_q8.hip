@@ -59,6 +59,8 @@ __device__ inline void load_x32(const void* x, int K, int b, float (&xv)[T][32])
 }
 
 constexpr int kQ8MaxMats = 4;
+constexpr int kQ8XlMax = 96 * 1024;   // largest activation copy in LDS (T = 2)
+constexpr int kQ8XlRows = 2;          // rows per wave with the LDS copy
 
 // The 1..4 matrices of one launch (same K, same activation): matrix i is W[i] - w_off[i]
 // (its dword-aligned base; w_off[i] = W[i] & 3) with N[i] rows and w_bytes[i] bytes from that
@@ -76,9 +78,19 @@ struct Q8Mats {
 
 // Workgroup = 4 waves = (4 / KS) row groups x KS slices of the row's blocks (KS per matrix,
 // the same as a launch of that matrix alone, so a batch equals the single launches bit for bit).
-template <int T, bool XH, int R, bool MULTI>
-__global__ __launch_bounds__(256) void k_gemv_q8(Q8Mats P, const void* __restrict__ x, int K) {
+// XL: the activation rows are copied into LDS once per workgroup and every wave reads its
+// blocks' activations from there (one K slice: the workgroup's 4 waves are 4 row groups that
+// share them), instead of each row group reading them from L2.
+template <int T, bool XH, int R, bool MULTI, bool XL>
+__global__ __launch_bounds__(256) void k_gemv_q8(Q8Mats P, const void* __restrict__ xg, int K) {
     __shared__ float red[4][T][R];
+    extern __shared__ __align__(16) uint8_t xlds[];
+    const void* __restrict__ x = XL ? (const void*)xlds : xg;
+    if constexpr (XL) {
+        const int n16 = T * K * (XH ? 2 : 4) / 16;
+        for (int i = threadIdx.x; i < n16; i += 256) ((uint4*)xlds)[i] = ((const uint4*)xg)[i];
+        __syncthreads();
+    }
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // this workgroup's matrix: every field is read before one is selected (no branches
     // around dependent argument loads)
@@ -237,30 +249,56 @@ __global__ __launch_bounds__(256) void k_gemv_q8(Q8Mats P, const void* __restric
     }
 }
 
-template <int T, bool XH>
-hipError_t launch_q8_t(Q8Mats& P, const void* x, int K, hipStream_t s) {
+template <int T, bool XH, int R>
+hipError_t launch_q8_r(Q8Mats& P, const void* x, int K, bool xl, hipStream_t s) {
     const int nb = K / kQ8Group;
-    // one fp16 row (v_dot2 form, little VALU per byte): 2 rows per wave, twice the waves of
-    // 4 (17408 x 5120: 26.1 -> 20.9 us); two rows (fp32 FMAs per quant and token) keep 4 rows
-    // per wave to reuse each block's activations (2 rows per wave: 28.5 -> 32.2 us).  Rows
-    // are split over K slices: at T = 1 rows of >= 256 blocks over 2 waves (5120 x 17408:
-    // 22.1 us with 4 slices, 22.9 with 1, 20.9 with 2) and rows of >= 128 blocks over 4 when
-    // the one-slice grid would be small (5120 x 1024: 6.7 -> 3.7 us); at T = 2 rows of >= 128
-    // blocks over 4.
-    constexpr int R = T == 1 ? 2 : 4;
+    const int xbytes = T * K * (XH ? 2 : 4);
     P.wg0[0] = 0;
     for (int i = 0; i < P.count; i++) {
         const int N = P.N[i];
-        P.lks[i] = (T == 1 && nb >= 256) ? 1 : (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) ? 2 : 0;
+        P.lks[i] = xl ? 0 : (T == 1 && nb >= 256) ? 1 : (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) ? 2 : 0;
         const int rpw = R * (4 >> P.lks[i]);     // rows per workgroup
         P.wg0[i + 1] = P.wg0[i] + (N + rpw - 1) / rpw;
     }
     for (int i = P.count; i < kQ8MaxMats; i++) P.wg0[i + 1] = P.wg0[P.count];
-    if (P.count > 1)
-        hipLaunchKernelGGL((k_gemv_q8<T, XH, R, true>), dim3(P.wg0[P.count]), dim3(256), 0, s, P, x, K);
-    else
-        hipLaunchKernelGGL((k_gemv_q8<T, XH, R, false>), dim3(P.wg0[P.count]), dim3(256), 0, s, P, x, K);
+    if (xl) {
+        // the dynamic-LDS limit of both instantiations, raised once per process
+        static const hipError_t attr = [] {
+            hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q8<T, XH, R, true, true>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kQ8XlMax);
+            if (e == hipSuccess)
+                e = hipFuncSetAttribute((const void*)k_gemv_q8<T, XH, R, false, true>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, kQ8XlMax);
+            return e;
+        }();
+        if (attr != hipSuccess) return attr;
+        if (P.count > 1)
+            hipLaunchKernelGGL((k_gemv_q8<T, XH, R, true, true>), dim3(P.wg0[P.count]), dim3(256), xbytes, s, P, x, K);
+        else
+            hipLaunchKernelGGL((k_gemv_q8<T, XH, R, false, true>), dim3(P.wg0[P.count]), dim3(256), xbytes, s, P, x, K);
+    } else if (P.count > 1) {
+        hipLaunchKernelGGL((k_gemv_q8<T, XH, R, true, false>), dim3(P.wg0[P.count]), dim3(256), 0, s, P, x, K);
+    } else {
+        hipLaunchKernelGGL((k_gemv_q8<T, XH, R, false, false>), dim3(P.wg0[P.count]), dim3(256), 0, s, P, x, K);
+    }
     return hipGetLastError();
+}
+
+// One fp16 row (v_dot2 form, little VALU per byte): 2 rows per wave, twice the waves of 4
+// (17408 x 5120: 26.1 -> 20.9 us).  Two rows (fp32 FMAs per quant and token): rows of fewer
+// than 256 blocks with the activations shared through LDS (XL) and 2 rows per wave
+// (17408 x 5120: 29.8 -> 24.0 us; XL at 4 rows per wave 27.2, at 8 37.9); longer rows read
+// them per row group and keep 4 rows per wave to reuse each block's activations (5120 x 17408:
+// XL 36.3 us, too few workgroups for one K slice each).  Rows are split over K slices: at
+// T = 1 rows of >= 256 blocks over 2 waves (5120 x 17408: 22.1 us with 4 slices, 22.9 with 1,
+// 20.9 with 2) and rows of >= 128 blocks over 4 when the one-slice grid would be small
+// (5120 x 1024: 6.7 -> 3.7 us); at T = 2 (without XL) rows of >= 128 blocks over 4.
+template <int T, bool XH>
+hipError_t launch_q8_t(Q8Mats& P, const void* x, int K, hipStream_t s) {
+    const int nb = K / kQ8Group;
+    const bool xl = T == 2 && T * K * (XH ? 2 : 4) <= kQ8XlMax && nb < 256;
+    if (xl) return launch_q8_r<T, XH, kQ8XlRows>(P, x, K, true, s);
+    return launch_q8_r<T, XH, T == 1 ? 2 : 4>(P, x, K, false, s);
 }
 
 }  // namespace
