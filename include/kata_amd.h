@@ -93,7 +93,7 @@ int kata_gemv_ptq1_wide_batch(int count, const uint8_t* const* W, float* const* 
  * for bit); the activation image goes to a fixed per-device array of
  * kata_gemv_ptq1_wide_noalloc_scratch_bytes() bytes (4 MiB) held by each device the library
  * runs on until the process ends, instead of the stream's buffer.  Rejects (KATA_EINVAL) a K
- * whose image would not fit it (K beyond 172 928: 3104 bytes per 128 weights of a row).
+ * whose image would not fit it (K beyond 258 048: 2080 bytes per 128 weights of a row).
  * Calls that overlap in time on one device share the array and race. */
 int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                                 void* stream);

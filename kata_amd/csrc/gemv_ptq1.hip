@@ -38,8 +38,7 @@ namespace kata {
 namespace {
 
 constexpr float kQMax = 32639.0f;   // |q| <= 32639 keeps hi = (q+128)>>8 inside int8
-constexpr int kMfmaPerBlock = 3;   // the wide verification GEMV's operand layout
-constexpr int kDenseMfma = 2;      // the decode GEMV's dense layout: 32 trits per lane group
+constexpr int kDenseMfma = 2;      // MFMAs per block: the dense layout, 32 trits per lane group
 constexpr int kAImageBytes = kDenseMfma * 4 * 16;   // per block and A row (token, limb)
 constexpr int kWaves = 16;
 constexpr int kChunkMax = 3;   // 8-element activation chunks per thread: K <= 3 * 8 * 1024
@@ -58,32 +57,7 @@ struct GemvMats {
     int count;
 };
 
-// A block is read as four 8-byte segments starting at bytes 20, 0, 8, 16 (segment 3 uses
-// only bytes 16..19; bytes 20..23 belong to segment 0).  Segment 0 carries the scale.
-// Lane group g working on block 4c + kq reads segment (g - kq) & 3, so the lanes whose
-// result rows hold that block (g == kq) are the ones holding the scale.
-__host__ __device__ constexpr int gemv_seg_byte0(int seg) { return seg == 0 ? 20 : seg == 1 ? 0 : seg == 2 ? 8 : 16; }
-
-// Offset of element e of a block with quarter kq (block index & 3) inside the block's A
-// image [m 3][g 4][i 2T][16 B] (row i = 0: token 0's high limb).  Element e sits at byte
-// p, digit n (ptq1_elem_src); byte p is in segment seg at d = p - gemv_seg_byte0(seg), and
-// lane group g = (seg + kq) & 3 reads that segment.  With b0..b7 the lane's 8 bytes
-// (w0 = b0..b3, w1 = b4..b7) the B dwords are
-//   m=0: L(b0) L(b1) L(b2) L(b3)     m=1: Z(w0) L(b4) L(b5) L(b6)     m=2: L(b7) Z(w1) 0 0
-// where L(b) = digits 1..4 of byte b (byte kb holds digit kb + 1) and Z(w) = digit 0 of
-// the dword's bytes (byte kb for byte kb).  Image bytes that carry no element (the scale
-// bytes, qh digit 4, bytes 20..23 as read by segment 3) hold a zero activation.
-__host__ __device__ constexpr int gemv_elem_img_off(int e, int kq, int T) {
-    int p = 0, n = 0;
-    ptq1_elem_src(e, p, n);
-    const int seg = p < 8 ? 1 : p < 16 ? 2 : p < 20 ? 3 : 0;
-    const int d = p - gemv_seg_byte0(seg), g = (seg + kq) & 3;
-    const int kind = n > 0 ? (d < 4 ? d : d + 1) : (d < 4 ? 4 : 9);
-    const int kb = n > 0 ? n - 1 : d & 3;
-    return (kind >> 2) * (4 * 2 * T * 16) + g * (2 * T * 16) + (kind & 3) * 4 + kb;
-}
-
-// The decode GEMV's dense layout: lane group g of a B column (one row, one block) holds the
+// The dense operand layout (both GEMVs): lane group g of a B column (one row, one block) holds the
 // 32 trits of qs bytes 6g .. 6g + 5 (all five digits) and two digits of qh byte 24 + (g >> 1)
 // (digits 2(g & 1) and 2(g & 1) + 1), so two MFMAs cover the block's 128 trits with no empty
 // slot.  With c0..c5 the lane's six qs bytes the B dwords are
@@ -316,6 +290,43 @@ __device__ inline uint32_t trit_entry(uint32_t bv) {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h34), __builtin_bit_cast(uint32_t, h12), 0x07050301u);
 }
 
+// Dense decode (the layout at gemv_dense_img_off) of one lane's share of a block: w0, w1 the 8
+// bytes at gemv_dense_byte0(g), wq the block's bytes 24..27 (qh, scale).  Per-lane constants
+// (DenseLane): the byte shift of c0 in the 8 bytes (2 (g & 1)), the perm selectors that take
+// c4, c5 and the qh byte, and the multipliers 3^a, 3^(a+1) of the lane's two qh digits
+// (a = 2 (g & 1)).  B[0], B[1] are the B operands of the block's two MFMAs.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+struct DenseLane {
+    uint32_t csh, sel_c4, sel_c5, sel_z45, sel_q;
+    u16x2 qmul;
+};
+template <int LR>
+__device__ inline DenseLane dense_lane(int g) {
+    DenseLane L;
+    L.csh = 2u * (uint32_t)(g & 1);
+    L.sel_c4 = lut_sel<LR>(L.csh);
+    L.sel_c5 = lut_sel<LR>(L.csh + 1);
+    L.sel_z45 = 0x0c000c00u | ((L.csh + 1) << 16) | L.csh;               // (c4, 0, c5, 0)
+    const uint32_t qb = (uint32_t)(g >> 1);
+    L.sel_q = 0x0c000c00u | (qb << 16) | qb;                             // (qh, 0, qh, 0)
+    L.qmul = (g & 1) ? (u16x2){9, 27} : (u16x2){1, 3};
+    return L;
+}
+template <int LR>
+__device__ inline void dense_decode(uint32_t w0, uint32_t w1, uint32_t wq, lds_u8* lb, uint32_t laneoff,
+                                    const DenseLane& L, v4i* B) {
+    const uint32_t c03 = __builtin_amdgcn_alignbyte(w1, w0, L.csh);       // c0..c3
+    B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(c03, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(c03, 1, laneoff)),
+               (int)lds_u32(lb, lut_addr<LR>(c03, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(c03, 3, laneoff))};
+    const u16x2 z45 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w1, L.sel_z45)) * (u16x2){3, 3} +
+                      (u16x2){0xff00, 0xff00};
+    const u16x2 mq = (__builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, wq, L.sel_q)) * L.qmul) & (u16x2){0xff, 0xff};
+    const u16x2 hq = mq * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    B[1] = v4i{(int)lds_u32(lb, lut_addr_sel<LR>(w1, L.sel_c4, L.csh, laneoff)),
+               (int)lds_u32(lb, lut_addr_sel<LR>(w1, L.sel_c5, L.csh + 1, laneoff)), (int)trit0_word(c03),
+               (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hq), __builtin_bit_cast(uint32_t, z45), 0x07050301u)};
+}
+
 // Work split ("activation-stationary").  One 1024-thread workgroup (16 waves) per CU owns
 // the contiguous tile range [wt0, wt0 + Tt) (4 rows per tile) of one matrix.  Its work
 // items (c, tile) — 4 consecutive blocks 4c..4c+3 of the tile's 4 rows — are numbered by
@@ -502,7 +513,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // (2) quantise: per block and token s = amax / 32639, q = rint(x * (32639 / amax))
     // (0 if amax = 0; |q| <= 32639, so hi = (q + 128) >> 8 fits int8), and (3) scatter the
     // limbs hi and lo = q - 256 hi (the low byte of q): element 8*(j & 15) + e of block
-    // j >> 4 goes to image offset gemv_elem_img_off(8*(j & 15) + e, (j >> 4) & 3, T) +
+    // j >> 4 goes to image offset gemv_dense_img_off(8*(j & 15) + e, T) +
     // 16*(2t + limb) of that block
     {
         const uint4 offw = *(const uint4*)(Os + (tid & 63) * 16);
@@ -586,29 +597,11 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
             for (int t = 0; t < T; t++) sc[h][t] = xs[c * 8 * T + 2 * t];
         }
     };
-    // Dense decode (the layout at gemv_dense_img_off).  Per-lane constants: the byte shift of
-    // c0 in the 8 loaded bytes (2 (g & 1)), the perm selectors that take c4, c5 and the qh
-    // byte, and the multipliers 3^a, 3^(a+1) of the lane's two qh digits (a = 2 (g & 1)).
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    const uint32_t csh = 2u * (uint32_t)(g & 1);
-    const uint32_t sel_c4 = lut_sel<LR>(csh), sel_c5 = lut_sel<LR>(csh + 1);
-    const uint32_t sel_z45 = 0x0c000c00u | ((csh + 1) << 16) | csh;      // (c4, 0, c5, 0)
-    const uint32_t qb = (uint32_t)(g >> 1);
-    const uint32_t sel_q = 0x0c000c00u | (qb << 16) | qb;                // (qh, 0, qh, 0)
-    const u16x2 qmul = (g & 1) ? (u16x2){9, 27} : (u16x2){1, 3};
+    const DenseLane dl = dense_lane<LR>(g);
     const int qsrc = (lane | 48) << 2;
     auto decode = [&](uint32_t w0, uint32_t w1, uint32_t& wqv, v4i* B) {
-        wqv = (uint32_t)__builtin_amdgcn_ds_bpermute(qsrc, (int)wqv);   // block bytes 24..27
-        const uint32_t c03 = __builtin_amdgcn_alignbyte(w1, w0, csh);     // c0..c3
-        B[0] = v4i{(int)lds_u32(lb, lut_addr<LR>(c03, 0, laneoff)), (int)lds_u32(lb, lut_addr<LR>(c03, 1, laneoff)),
-                   (int)lds_u32(lb, lut_addr<LR>(c03, 2, laneoff)), (int)lds_u32(lb, lut_addr<LR>(c03, 3, laneoff))};
-        const u16x2 z45 = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w1, sel_z45)) * (u16x2){3, 3} +
-                          (u16x2){0xff00, 0xff00};
-        const u16x2 mq = (__builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, wqv, sel_q)) * qmul) & (u16x2){0xff, 0xff};
-        const u16x2 hq = mq * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
-        B[1] = v4i{(int)lds_u32(lb, lut_addr_sel<LR>(w1, sel_c4, csh, laneoff)),
-                   (int)lds_u32(lb, lut_addr_sel<LR>(w1, sel_c5, csh + 1, laneoff)), (int)trit0_word(c03),
-                   (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hq), __builtin_bit_cast(uint32_t, z45), 0x07050301u)};
+        wqv = (uint32_t)__builtin_amdgcn_ds_bpermute(qsrc, (int)wqv);   // block bytes 24..27, from lane group 3
+        dense_decode<LR>(w0, w1, wqv, lb, laneoff, dl, B);
     };
     int ct = strided ? 0 : (s0 % (2 * Tt)) >> 1, cp = strided ? sp : s0 / (2 * Tt);   // compute cursor: tile, pair
     v4i B0[kDenseMfma], B1[kDenseMfma];
@@ -682,7 +675,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 // the LDS banks (a store instruction of the unpadded layout needs ~15 passes, this one
 // ~1.25).  kWideOff[e]: offset of element e's high limb for token 0 in that layout.
 constexpr int kWideG = 272, kWideM = 4 * kWideG;
-constexpr int kWideBlkBytes = 3 * kWideM;
+constexpr int kWideBlkBytes = kDenseMfma * kWideM;
 
 struct alignas(16) WideOffTable {
     uint16_t v[128];
@@ -690,7 +683,7 @@ struct alignas(16) WideOffTable {
 constexpr WideOffTable make_wide_off_table() {
     WideOffTable t{};
     for (int e = 0; e < 128; e++) {
-        const int o = gemv_elem_img_off(e, 0, 8);   // [mfma][g][row 16][16 B], unpadded
+        const int o = gemv_dense_img_off(e, 8);     // [mfma][g][row 16][16 B], unpadded
         t.v[e] = (uint16_t)((o >> 10) * kWideM + ((o >> 8) & 3) * kWideG + (o & 15));
     }
     return t;
@@ -721,7 +714,7 @@ constexpr int kVwCBMax = 40;                     // blocks per K chunk (the wave
 constexpr int kVwWaves = 8;
 constexpr int kVwBB = kVwCBMax / kVwWaves;       // blocks of a wave per chunk
 constexpr int kVwLR = 6;                         // 64 trit-table replicas (conflict-free lookups)
-constexpr int kVwImgBlk = 3 * 4 * 16 * 16;       // image bytes per block (3072)
+constexpr int kVwImgBlk = kDenseMfma * 4 * 16 * 16;   // image bytes per block (2048)
 constexpr int kVwPrepBlocks = 1;                 // blocks per prep workgroup (one: the shortest chain)
 constexpr int kVwPrepThreads = kVwPrepBlocks >= 2 ? 256 : 128;   // 8 tokens x 16 chunks per block
 static_assert(8 * kVwPrepBlocks * 16 % kVwPrepThreads == 0, "whole quantisation tasks per prep thread");
@@ -820,8 +813,8 @@ __global__ __launch_bounds__(kVwPrepThreads) void k_gemv_vw_prep(const void* __r
     }
     __syncthreads();
     // unpadded copy out: 16-byte row r of lane group g of MFMA m of block b
-    for (int o = tid; o < cb * 3 * 4 * 16; o += kVwPrepThreads) {
-        const int r = o & 15, g = (o >> 4) & 3, mb = o >> 6, m = mb % 3, b = mb / 3;
+    for (int o = tid; o < cb * kDenseMfma * 4 * 16; o += kVwPrepThreads) {
+        const int r = o & 15, g = (o >> 4) & 3, mb = o >> 6, m = mb % kDenseMfma, b = mb / kDenseMfma;
         *(uint4*)(img + (size_t)blk0 * kVwImgBlk + o * 16) =
             *(const uint4*)(im + b * kWideBlkBytes + m * kWideM + g * kWideG + r * 16);
     }
@@ -868,7 +861,7 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
             t0m = sel ? t0v[i] : t0m;
         }
         const int row = min((gt - t0m) * 16 + xn, Nm - 1);
-        wp[t] = Wm + (size_t)row * row_bytes + gemv_seg_byte0(g);
+        wp[t] = Wm + (size_t)row * row_bytes + gemv_dense_byte0(g);
     }
 
     // trit table (visible after the LDS-only barrier in the first chunk)
@@ -881,6 +874,8 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
 
     const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
     lds_u8* lb = (lds_u8*)lut;
+    const DenseLane dl = dense_lane<kVwLR>(g);
+    const int qsrc = (lane | 48) << 2;
     const uint8_t* xa = ximg + g * 256 + xn * 16;
     float acc[kVwTMax][2];
 #pragma unroll
@@ -891,13 +886,13 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
         const int bw0 = (wave * cb) / kVwWaves, nbw = ((wave + 1) * cb) / kVwWaves - bw0;
         // (1) the A operands and scales of the wave's blocks, straight from the image (in L2:
         // every workgroup reads it) into registers, issued before the weight loads
-        v4i A[kVwBB][kMfmaPerBlock];
+        v4i A[kVwBB][kDenseMfma];
         float2 sc[kVwBB];
 #pragma unroll
         for (int bb = 0; bb < kVwBB; bb++) {
             const int b = kb0 + min(bw0 + bb, cb - 1);
 #pragma unroll
-            for (int m = 0; m < kMfmaPerBlock; m++) A[bb][m] = *(const v4i*)(xa + (size_t)b * kVwImgBlk + m * 1024);
+            for (int m = 0; m < kDenseMfma; m++) A[bb][m] = *(const v4i*)(xa + (size_t)b * kVwImgBlk + m * 1024);
             sc[bb] = xscl[(size_t)b * 4 + g];
         }
         // (3) every weight load of the wave's blocks for all TT tiles first (76 KB per CU for
@@ -907,16 +902,18 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
         // chunk) load a valid dummy address.
         auto run = [&](auto ttc) {
             constexpr int TT = decltype(ttc)::value;
-            uint32_t wl[TT][kVwBB], wh[TT][kVwBB];
+            // 12 bytes per lane and block: the lane's 8 and (lane group 3) the qh / scale dword
+            uint32_t wl[TT][kVwBB], wh[TT][kVwBB], wq[TT][kVwBB];
 #pragma unroll
             for (int t = 0; t < TT; t++)
 #pragma unroll
                 for (int bb = 0; bb < kVwBB; bb++) {
                     const uint8_t* a = bb < nbw ? wp[t] + (size_t)(kb0 + bw0 + bb) * kBlockBytes : ximg;
-                    uint2 w;
-                    __builtin_memcpy(&w, a, 8);
+                    uint3 w;
+                    __builtin_memcpy(&w, a, 12);
                     wl[t][bb] = w.x;
                     wh[t][bb] = w.y;
+                    wq[t][bb] = w.z;
                 }
             if (kb0 == 0) {                      // every wave runs the same chunks: uniform
                 // the trit table (built before the loads) is visible to every wave after
@@ -929,19 +926,14 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
 #pragma unroll
                 for (int bb = 0; bb < kVwBB; bb++) {
                     if (bb < nbw) {
-                        const uint32_t w0 = wl[t][bb], w1 = wh[t][bb];
-                        v4i B[kMfmaPerBlock];
-                        B[0] = v4i{(int)lds_u32(lb, lut_addr<kVwLR>(w0, 0, laneoff)), (int)lds_u32(lb, lut_addr<kVwLR>(w0, 1, laneoff)),
-                                   (int)lds_u32(lb, lut_addr<kVwLR>(w0, 2, laneoff)), (int)lds_u32(lb, lut_addr<kVwLR>(w0, 3, laneoff))};
-                        B[1] = v4i{(int)trit0_word(w0), (int)lds_u32(lb, lut_addr<kVwLR>(w1, 0, laneoff)),
-                                   (int)lds_u32(lb, lut_addr<kVwLR>(w1, 1, laneoff)), (int)lds_u32(lb, lut_addr<kVwLR>(w1, 2, laneoff))};
-                        B[2] = v4i{(int)lds_u32(lb, lut_addr<kVwLR>(w1, 3, laneoff)), (int)trit0_word(w1), 0, 0};
+                        // the row's qh / scale dword, read by lane group 3
+                        const uint32_t wqc = (uint32_t)__builtin_amdgcn_ds_bpermute(qsrc, (int)wq[t][bb]);
+                        v4i B[kDenseMfma];
+                        dense_decode<kVwLR>(wl[t][bb], wh[t][bb], wqc, lb, laneoff, dl, B);
                         v4i D = {0, 0, 0, 0};
 #pragma unroll
-                        for (int m = 0; m < kMfmaPerBlock; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[bb][m], B[m], D, 0, 0, 0);
-                        // the row's scale sits in bytes 26..27, read by lane group 0
-                        const uint32_t dbits = (uint32_t)__builtin_amdgcn_ds_bpermute(xn * 4, (int)w1) >> 16;
-                        const float d = half_bits_to_float(dbits);
+                        for (int m = 0; m < kDenseMfma; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[bb][m], B[m], D, 0, 0, 0);
+                        const float d = half_bits_to_float(wqc >> 16);
                         acc[t][0] += (float)(D[0] * 256 + D[1]) * (d * sc[bb].x);
                         acc[t][1] += (float)(D[2] * 256 + D[3]) * (d * sc[bb].y);
                     }
