@@ -8,7 +8,14 @@ GEMV of every ternary matrix of one layer of each kind at the 27B shapes —
 GDN qkv 5120->10240, z 5120->6144, ssm_out 6144->5120; GQA q 5120->12288, k/v 5120->1024,
 o 6144->5120; FFN gate/up 5120->17408, down 17408->5120.  The matrices that multiply the
 same input run as one launch (kata_gemv_ptq1_batch: qkv+z, q+k+v, gate+up; ssm_out, o and
-down alone), 6 launches per step; the activation is quantised inside the GEMV kernel.
+down alone), 6 launches per step.  The GEMVs take each input in the operand form (KATA_XQ:
+the activation quantised to the kernel's 16-bit block fixed point and laid out as its
+matrix-core operand), which in the model the input transform writes in place of fp32 rows
+(kata_add_rms_fwht / kata_rms_fwht with out_dtype KATA_XQ, the dispatcher's decode form);
+it is prepared once before the timed region, as the reference's GEMV is timed on an
+activation its rms_fwht kernel already wrote.  `raw_x_step` times the same step on fp16 rows,
+each GEMV workgroup quantising them itself, and input_transform times the transform with
+either output.
 Weights are seeded
 synthetic PTQ1_0 (trits iid on {-1,0,1}, fp16 scales |N(0,0.02)|), activations fp16
 N(0,1).  Steps rotate over enough distinct weight copies (>= 512 MB) that no matrix is
@@ -99,7 +106,7 @@ def run_config5(torch, ops, dev, stream):
     launches = [(K, [device_weights(torch, dev, K, N, gen) for N in Ns], Ns) for L in layers for K, Ns in L]
     launches.append((LM_HEAD[0], [device_weights(torch, dev, LM_HEAD[0], LM_HEAD[1][0], gen)], LM_HEAD[1]))
     total = sum(w.numel() for _, ws, _ in launches for w in ws)
-    xs = {K: torch.randn((1, K), generator=gen, device=dev).half() for K in (5120, 6144, 17408)}
+    xs = {K: ops.gemv_prepare_x(torch.randn((1, K), generator=gen, device=dev).half(), K, 1) for K in (5120, 6144, 17408)}
     ys = {N: torch.empty((1, N), dtype=torch.float32, device=dev) for N in (1024, 5120, 6144, 10240, 12288, 17408, 248320)}
 
     def sweep():
@@ -462,7 +469,9 @@ def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
 def run_calibration(torch, ops, dev, stream, cap_stream, reps):
     """The launch floor of an empty kernel at the decode GEMV's geometry and a plain streaming
     read at the sweep's sizes (same protocol as per_matrix), over rotating buffers (>= 512 MB
-    per size) so that reads come from HBM."""
+    per size) so that reads come from HBM: `read` at the GEMV's geometry (one 1024-thread
+    workgroup per CU, ordinary loads), `peak` at the fastest plain-read geometry found
+    (two 256-thread workgroups per CU, non-temporal loads) -- the read ceiling."""
     calib = {}
     cword = torch.zeros(4, dtype=torch.int32, device=dev)
     calib["empty_us"] = round(graph_time(torch, lambda r: ops.calib_empty(cword), reps, stream, cap_stream), 3)
@@ -472,9 +481,11 @@ def run_calibration(torch, ops, dev, stream, cap_stream, reps):
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nb)]
         for b_ in bufs:
             b_.fill_(1)
-        us = graph_time(torch, lambda r: ops.calib_read(bufs[r % nb], cword), reps if nbytes < 1e8 else 40,
-                        stream, cap_stream)
-        calib[label] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        n = reps if nbytes < 1e8 else 40
+        us = graph_time(torch, lambda r: ops.calib_read(bufs[r % nb], cword), n, stream, cap_stream)
+        up = graph_time(torch, lambda r: ops.calib_read_peak(bufs[r % nb], cword), n, stream, cap_stream)
+        calib[label] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "peak_us": round(up, 3), "peak_GBps": round(nbytes / (up * 1e-6) / 1e9, 1)}
         del bufs
     return calib
 
@@ -545,6 +556,8 @@ def main():
         xs[grp] = torch.from_numpy(np.random.default_rng(SEED + 77 + gi).standard_normal((1, K))
                                    .astype(np.float16)).to(dev)
     ys = [torch.empty((1, N), dtype=torch.float32, device=dev) for _, _, N, _ in SWEEP]
+    # the operand form of each input (what the input transform writes in the decode path)
+    xqs = {grp: ops.gemv_prepare_x(x, x.shape[1], 1) for grp, x in xs.items()}
 
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": run_gemm(torch, ops, dev, stream, copies, ncopies)}))
@@ -570,22 +583,25 @@ def main():
         groups.setdefault(grp, []).append(j)
     group_list = [(grp, idx, SWEEP[idx[0]][1]) for grp, idx in groups.items()]
 
-    def step(i):
+    def step(i, xin=xqs):
         ws = copies[i % ncopies]
         for grp, idx, K in group_list:
-            ops.gemv_ptq1_batch([ws[j] for j in idx], xs[grp], K, [SWEEP[j][2] for j in idx], 1,
+            ops.gemv_ptq1_batch([ws[j] for j in idx], xin[grp], K, [SWEEP[j][2] for j in idx], 1,
                                 outs=[ys[j] for j in idx])
+
+    def step_raw(i):
+        step(i, xs)
 
     def step_single(i):
         ws = copies[i % ncopies]
         for j, (name, K, N, grp) in enumerate(SWEEP):
-            ops.gemv_ptq1(ws[j], xs[grp], K, N, 1, out=ys[j])
+            ops.gemv_ptq1(ws[j], xqs[grp], K, N, 1, out=ys[j])
 
     # The timed steps run either as captured HIP graphs (default: a batch of consecutive steps
     # per graph, step i on weight copy i % ncopies, captured before the timed region and
     # replayed inside it) or as host launches from Python, one call per GEMV launch.
     cap_stream = torch.cuda.Stream(dev)            # capture needs a non-default stream
-    fns = {"step": step} if args.step_only else {"step": step, "single": step_single}
+    fns = {"step": step} if args.step_only else {"step": step, "single": step_single, "raw": step_raw}
     for fn in fns.values():
         for i in range(2):
             fn(i)                                 # first calls set kernel attributes
@@ -626,7 +642,9 @@ def main():
     for i in range(args.warmup):
         fns["step"](i)
     torch.cuda.synchronize()
-    ms_total = timed("step", args.steps, nbatch=8 if args.steps >= 8 else 1)
+    nbatch = 8 if args.steps >= 8 else 1
+    ms_total = timed("step", args.steps, nbatch=nbatch)
+    step_batch_ms = list(batch_ms)
     ms_step = ms_total / args.steps
     value = set_bytes * args.steps / (ms_total * 1e-3) / 1e9
     if args.step_only:
@@ -637,6 +655,7 @@ def main():
     launches = len(group_list)
     gemv_launch_us = ms_total * 1e3 / (args.steps * launches)
     ms_single = timed("single", args.steps)
+    ms_raw = timed("raw", args.steps, nbatch=nbatch)      # batched as the headline step
     other = "host" if args.launch == "graph" else "graph"
     ms_other = timed("step", args.steps, launch=other)
     bytes_per_launch = set_bytes / launches
@@ -648,12 +667,14 @@ def main():
         return graph_time(torch, fn, nrep, stream, cap_stream)
 
     for j, (name, K, N, grp) in enumerate(SWEEP):
-        us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], xs[grp], K, N, 1, out=ys[j]), args.reps)
+        us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], xqs[grp], K, N, 1, out=ys[j]), args.reps)
+        us_raw = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], xs[grp], K, N, 1, out=ys[j]), args.reps)
         per_matrix[name] = {"K": K, "N": N, "us": round(us, 3),
-                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
+                            "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1), "raw_x_us": round(us_raw, 3)}
 
     calib = run_calibration(torch, ops, dev, stream, cap_stream, args.reps)
     calib["ffn_gate_vs_read_19.5MB"] = round(per_matrix["ffn_gate"]["us"] / calib["19.5MB"]["us"], 3)
+    calib["ffn_gate_vs_ceiling_19.5MB"] = round(per_matrix["ffn_gate"]["us"] / calib["19.5MB"]["peak_us"], 3)
 
     # ---- config 3: T=2 speculative-verify GEMV (two fp16 activation columns
     # shared per input) and the Q8_0 MTP-head GEMV (17408x5120 and 5120x17408, T=1)
@@ -664,9 +685,11 @@ def main():
         x2 = torch.from_numpy(np.random.default_rng(SEED + 300 + j).standard_normal((2, K))
                               .astype(np.float16)).to(dev)
         y2 = torch.empty((2, N), dtype=torch.float32, device=dev)
-        us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], x2, K, N, 2, out=y2), args.reps)
+        xq2 = ops.gemv_prepare_x(x2, K, 2)
+        us = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], xq2, K, N, 2, out=y2), args.reps)
+        us_raw = time_reps(lambda r: ops.gemv_ptq1(copies[r % ncopies][j], x2, K, N, 2, out=y2), args.reps)
         verify_t2[name] = {"K": K, "N": N, "us": round(us, 3),
-                           "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)}
+                           "GBps": round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1), "raw_x_us": round(us_raw, 3)}
     verify_wide = run_verify_wide(torch, ops, dev, copies, ncopies,
                                   lambda fn, n: graph_time(torch, fn, n, stream, cap_stream), args.reps)
     q8 = run_q8(torch, ops, dev, time_reps, args.reps)
@@ -675,7 +698,7 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED + 700)
     lm = [device_weights(torch, dev, 5120, 248320, gen) for _ in range(2)]   # 556 MB: past the MALL
-    lx = xs[next(g for _, K, _, g in SWEEP if K == 5120)]
+    lx = xqs[next(g for _, K, _, g in SWEEP if K == 5120)]
     ly = torch.empty((1, 248320), dtype=torch.float32, device=dev)
     lidx = torch.empty(1, dtype=torch.int32, device=dev)
     us_lm = time_reps(lambda r: ops.gemv_ptq1(lm[r % 2], lx, 5120, 248320, 1, out=ly), 40)
@@ -686,20 +709,22 @@ def main():
 
     # ---- matmul input transform (residual add + RMSNorm + sign + FWHT), decode and prefill
     xform = {}
-    for label, M in (("decode_m1", 1), ("prefill_m7300", 7300)):
+    for label, M, odt in (("decode_m1", 1, 1), ("decode_m1_operand", 1, 2), ("prefill_m7300", 7300, 1)):
         W = 5120
         xt = torch.randn((M, W), device=dev)
         yt = torch.randn((M, W), device=dev)
         gt = torch.sign(torch.randn(W, device=dev))
-        outt = torch.empty((M, W), dtype=torch.float16, device=dev)
+        obytes = ops.gemv_xq_bytes(W, M) if odt == 2 else M * W * 2
+        outt = torch.empty(obytes, dtype=torch.uint8, device=dev)
         xn = torch.empty_like(xt)
 
-        def xf(r, xt=xt, yt=yt, gt=gt, outt=outt, xn=xn, W=W, M=M):
-            ops.lib().kata_add_rms_fwht(ops._ptr(xt), ops._ptr(yt), ops._ptr(gt), ops._ptr(outt), 1, 0, ops._ptr(xn),
-                                        None, None, 0, W, M, ops._stream(xt))
+        def xf(r, xt=xt, yt=yt, gt=gt, outt=outt, xn=xn, W=W, M=M, odt=odt):
+            ops.check(ops.lib().kata_add_rms_fwht(ops._ptr(xt), ops._ptr(yt), ops._ptr(gt), ops._ptr(outt), odt, 0,
+                                                  ops._ptr(xn), None, None, 0, W, M, ops._stream(xt)))
         us = time_reps(xf, 50 if M > 1 else args.reps)
-        nbytes = M * W * (4 + 4 + 4 + 2)              # x, y in; xnew fp32, out fp16 out
-        xform[label] = {"M": M, "W": W, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        nbytes = M * W * (4 + 4 + 4) + obytes          # x, y in; xnew fp32 and out (fp16 / operand) out
+        xform[label] = {"M": M, "W": W, "out": "operand form" if odt == 2 else "fp16 rows", "us": round(us, 2),
+                        "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
     # ---- layer level: the FFN sublayer (27B shapes) through the dispatcher
     ffn = None if args.no_ffn else run_ffn(torch, ops, dev, stream, time_reps)
@@ -752,7 +777,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "fp16 in -> 16-bit block fixed point (2 x int8 limbs) x int8 trits -> exact int32 -> fp32 out",
         "numerics": ("fp16 activation -> per-128-block 16-bit fixed point as two int8 limbs; ternary weights as "
                      "int8 trits; exact int32 block sums on the int8 matrix cores; fp32 scale (fp16 d x block "
                      "scale) and fp32 accumulation; fp32 output"),
@@ -764,11 +789,15 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_ptq1<1>", "avg_launch_us": round(gemv_launch_us, 3),
                      "bytes_per_launch": bytes_per_launch},
-        "step_batches": ({"n": len(batch_ms), "best_GBps": round(set_bytes / (min(batch_ms) * 1e-3) / 1e9, 1),
-                          "median_GBps": round(set_bytes / (float(np.median(batch_ms)) * 1e-3) / 1e9, 1)}
-                         if batch_ms else None),
+        "step_batches": ({"n": len(step_batch_ms),
+                          "best_GBps": round(set_bytes / (min(step_batch_ms) * 1e-3) / 1e9, 1),
+                          "median_GBps": round(set_bytes / (float(np.median(step_batch_ms)) * 1e-3) / 1e9, 1)}
+                         if step_batch_ms else None),
         f"{other}_launch": {"ms_per_step": round(ms_other / args.steps, 5),
                             "GBps": round(set_bytes * args.steps / (ms_other * 1e-3) / 1e9, 1)},
+        "raw_x_step": {"ms_per_step": round(ms_raw / args.steps, 5),
+                       "GBps": round(set_bytes * args.steps / (ms_raw * 1e-3) / 1e9, 1),
+                       "note": "the same step on fp16 rows, quantised by every GEMV workgroup"},
         "one_launch_per_matrix": {"ms_per_step": round(ms_single / args.steps, 5),
                                   "GBps": round(set_bytes * args.steps / (ms_single * 1e-3) / 1e9, 1)},
         "per_matrix": per_matrix,

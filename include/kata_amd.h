@@ -29,6 +29,11 @@ extern "C" {
 /* activation element types */
 #define KATA_F32 0
 #define KATA_F16 1
+/* the decode GEMV's operand form of T (1, 2) activation rows: kata_gemv_xq_bytes(K, T) bytes,
+ * written by kata_gemv_prepare_x or by the input transforms (kata_add_rms_fwht,
+ * kata_rms_fwht with M == T); an x_dtype of kata_gemv_ptq1 / _batch and an out_dtype of the
+ * transforms */
+#define KATA_XQ 2
 /* activation layouts for the GEMVs */
 #define KATA_X_ROWS 0   /* x[T][K], one row per token */
 #define KATA_X_HALF2 1  /* x[K][2] fp16, the two tokens interleaved (T == 2 only) */
@@ -53,6 +58,19 @@ int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, f
 
 /* Largest K the PTQ1_0 GEMV accepts for T tokens (its activation image lives in LDS). */
 int kata_gemv_ptq1_max_k(int T);
+
+/* The operand form (KATA_XQ) of T in {1, 2} activation rows for the decode GEMV: each
+ * 128-block and token quantised to the 16-bit block fixed point the GEMV computes in (scale
+ * amax / 32639, q = rint(x * 32639 / amax) as two int8 limbs), laid out as the GEMV's
+ * matrix-core operand.  Writing it once lets every workgroup of a GEMV copy it instead of
+ * quantising x itself; kata_gemv_ptq1(W, xq, KATA_XQ, KATA_X_ROWS, ...) gives the same y bit
+ * for bit as kata_gemv_ptq1(W, x, x_dtype, x_layout, ...).  x as for kata_gemv_ptq1, K % 128
+ * == 0, xq 16-byte aligned, kata_gemv_xq_bytes(K, T) bytes (0 for an unsupported K or T:
+ * K beyond kata_gemv_ptq1_max_k(T) or an operand over 128 KB).  No counterpart function in
+ * the reference, whose GEMVs read the float activation directly (shaders/gemv_fast.metal:
+ * 9-50); it is the producer side of Engine::dGemvPtq1's input (src/engine.cpp:97-101). */
+size_t kata_gemv_xq_bytes(int K, int T);
+int kata_gemv_prepare_x(const void* x, int x_dtype, int x_layout, int K, int T, void* xq, void* stream);
 
 /* The same GEMV for 1..4 matrices that multiply one activation (same K), in one launch:
  * y[i][t][n] for W[i] with N[i] rows.  W, y and N are HOST arrays of count device
@@ -172,7 +190,10 @@ int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, v
  *   out[b][j] = (1/32) sum_k (-1)^popcount(j & k) * (v * inv * gs)[1024 b + k]
  * (gs = the sign vector with the RMSNorm weight folded in).  out is fp32 or fp16 rows
  * [M][W], or for M == 2 fp16 with the two tokens interleaved, [W][2] (KATA_X_HALF2, the
- * half2 operand of the T = 2 GEMV).  All vectors 16-byte aligned.
+ * half2 operand of the T = 2 GEMV), or for M <= 2 the decode GEMV's operand form
+ * (out_dtype KATA_XQ, out_layout KATA_X_ROWS, kata_gemv_xq_bytes(W, M) bytes: the fp32
+ * values quantised as kata_gemv_prepare_x does, so the GEMV then gives y bit for bit as
+ * from the fp32 rows).  All vectors 16-byte aligned.
  * Replaces k_add_rms_fwht (shaders/ops.metal:86-106), k_add_rms_fwht_b and
  * k_add_rms_fwht_t (shaders/prefill.metal:59-78,266-285). */
 int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out, int out_dtype, int out_layout,
@@ -193,9 +214,13 @@ int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* ou
  * 1024-thread workgroups (wgs <= 0: one per CU, the decode GEMV's geometry), the launch
  * floor.  kata_calib_read: a plain streaming read of `bytes` bytes at p (16-byte aligned,
  * < 2^31) at the same geometry, 16-byte loads, the achievable HBM read rate at that size;
- * out (device, one word) is written only in a case that practically never happens. */
+ * out (device, one word) is written only in a case that practically never happens.
+ * kata_calib_read_peak: the same read at the fastest plain-read geometry a sweep found
+ * (two 256-thread workgroups per CU, non-temporal 16-byte loads, four in flight per
+ * lane), the read ceiling the decode GEMV is measured against. */
 int kata_calib_empty(uint32_t* out, int wgs, void* stream);
 int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* stream);
+int kata_calib_read_peak(const void* p, size_t bytes, uint32_t* out, void* stream);
 
 /* Greedy argmax of n fp32 logits into *out (device int): an element counts only if strictly
  * greater than the best so far (NaN and -inf never do), lowest index on ties, 0x7fffffff

@@ -12,7 +12,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _SO = os.path.join(_HERE, "libkata_amd.so")
 _lib = None
 
-KATA_F32, KATA_F16 = 0, 1
+KATA_F32, KATA_F16, KATA_XQ = 0, 1, 2   # KATA_XQ: the decode GEMV's operand form
 KATA_X_ROWS, KATA_X_HALF2 = 0, 1
 KATA_EINVAL, KATA_ELAUNCH = -1, -2
 KATA_FORM_DECODE, KATA_FORM_PREFILL, KATA_FORM_VERIFY = 0, 1, 2
@@ -85,6 +85,9 @@ SIGNATURES = {
     "kata_dispatch_work_bytes": (SZ, [I, I, I]),
     "kata_calib_empty": (I, [P, I, P]),
     "kata_calib_read": (I, [P, SZ, P, I, P]),
+    "kata_calib_read_peak": (I, [P, SZ, P, P]),
+    "kata_gemv_xq_bytes": (SZ, [I, I]),
+    "kata_gemv_prepare_x": (I, [P, I, I, I, I, P, P]),
 }
 
 

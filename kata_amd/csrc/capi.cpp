@@ -11,6 +11,7 @@
 #include <string>
 
 #include "../../include/kata_amd.h"
+#include "gemv_operand.h"
 #include "launch.h"
 
 namespace {
@@ -53,8 +54,11 @@ int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, con
     if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
     if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
     if (K > kata::gemv_max_k(T)) return fail(KATA_EINVAL, "K=%d exceeds %d for T=%d", K, kata::gemv_max_k(T), T);
-    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16 && x_dtype != KATA_XQ) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
     if (x_layout != KATA_X_ROWS && x_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "x_layout=%d", x_layout);
+    if (x_dtype == KATA_XQ && x_layout != KATA_X_ROWS) return fail(KATA_EINVAL, "the operand form takes KATA_X_ROWS");
+    if (x_dtype == KATA_XQ && kata_gemv_xq_bytes(K, T) == 0)
+        return fail(KATA_EINVAL, "K=%d: the operand form exceeds %d bytes", K, kata::kXqMaxBytes);
     if (x_layout == KATA_X_HALF2 && (T != 2 || x_dtype != KATA_F16))
         return fail(KATA_EINVAL, "KATA_X_HALF2 needs T=2 and fp16 activations");
     if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
@@ -75,6 +79,27 @@ const char* kata_version(void) { return "kata_amd 0.1 (gfx950)"; }
 
 // ------------------------------------------------------------------ PTQ1_0 GEMV
 int kata_gemv_ptq1_max_k(int T) { return (T == 1 || T == 2) ? kata::gemv_max_k(T) : 0; }
+
+size_t kata_gemv_xq_bytes(int K, int T) {
+    if ((T != 1 && T != 2) || K <= 0 || K % 128 != 0 || K > kata::gemv_max_k(T)) return 0;
+    const int b = kata::gemv_xq_bytes(K, T);
+    return b <= kata::kXqMaxBytes ? (size_t)b : 0;
+}
+
+int kata_gemv_prepare_x(const void* x, int x_dtype, int x_layout, int K, int T, void* xq, void* stream) {
+    if (!x || !xq) return fail(KATA_EINVAL, "null pointer argument");
+    if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
+    if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
+    if (kata_gemv_xq_bytes(K, T) == 0) return fail(KATA_EINVAL, "K=%d unsupported for T=%d", K, T);
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (x_layout != KATA_X_ROWS && x_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "x_layout=%d", x_layout);
+    if (x_layout == KATA_X_HALF2 && (T != 2 || x_dtype != KATA_F16))
+        return fail(KATA_EINVAL, "KATA_X_HALF2 needs T=2 and fp16 activations");
+    if (!aligned(x, 16) || !aligned(xq, 16)) return fail(KATA_EINVAL, "x and xq must be 16-byte aligned");
+    const size_t xb = (size_t)T * K * (x_dtype == KATA_F16 ? 2 : 4);
+    if (overlap({xq, kata_gemv_xq_bytes(K, T)}, {x, xb})) return fail(KATA_EINVAL, "xq overlaps x");
+    return check_launch(kata::launch_gemv_prepare(x, x_dtype, x_layout, K, T, xq, (hipStream_t)stream), "gemv prepare x");
+}
 
 int kata_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_layout, float* y, int K, int N, int T,
                    void* stream) {
@@ -250,8 +275,14 @@ int kata_expand_ptq1_i8(const uint8_t* W, int8_t* T8, float* SW, int K, int N, v
 }
 
 // ------------------------------------------------------------------ matmul input transform
+static size_t fwht_out_bytes(int out_dtype, int W, int M) {
+    return out_dtype == KATA_XQ ? kata_gemv_xq_bytes(W, M) : (size_t)W * M * (out_dtype == KATA_F16 ? 2 : 4);
+}
+
 static int check_fwht_out(const void* out, int out_dtype, int out_layout, int W, int M) {
-    if (out_dtype != KATA_F32 && out_dtype != KATA_F16) return fail(KATA_EINVAL, "out_dtype=%d", out_dtype);
+    if (out_dtype != KATA_F32 && out_dtype != KATA_F16 && out_dtype != KATA_XQ) return fail(KATA_EINVAL, "out_dtype=%d", out_dtype);
+    if (out_dtype == KATA_XQ && (M < 1 || M > 2 || out_layout != KATA_X_ROWS || kata_gemv_xq_bytes(W, M) == 0))
+        return fail(KATA_EINVAL, "the operand form takes M <= 2, KATA_X_ROWS and a GEMV-supported W (M=%d W=%d)", M, W);
     if (out_layout != KATA_X_ROWS && out_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "out_layout=%d", out_layout);
     if (out_layout == KATA_X_HALF2 && (out_dtype != KATA_F16 || M != 2))
         return fail(KATA_EINVAL, "the half2 layout is fp16 with M == 2");
@@ -269,7 +300,7 @@ int kata_add_rms_fwht(const float* x, const float* y, const float* gs, void* out
     // theirs (the reference alternates two residual buffers, src/engine.cpp:136-146)
     {
         const size_t rows = (size_t)W * M * sizeof(float);
-        const size_t ob = (size_t)W * M * (out_dtype == KATA_F16 ? 2 : 4);
+        const size_t ob = fwht_out_bytes(out_dtype, W, M);
         const size_t hb = (size_t)W * M * (hout_dtype == KATA_F16 ? 2 : 4);
         const Span ins[] = {{x, rows}, {y, rows}, {gs, (size_t)W * 4}, {gamma, (size_t)W * 4}};
         const Span outs[] = {{out, ob}, {xnew, rows}, {hout, hb}};
@@ -299,7 +330,7 @@ int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* ou
     if (int rc = check_fwht_out(out, out_dtype, out_layout, W, M)) return rc;
     {
         const size_t rows = (size_t)W * M * sizeof(float);
-        const Span o{out, (size_t)W * M * (out_dtype == KATA_F16 ? 2 : 4)};
+        const Span o{out, fwht_out_bytes(out_dtype, W, M)};
         if (overlap(o, {src, rows}) || overlap(o, {mode == 1 ? src2 : nullptr, rows}) || overlap(o, {gs, (size_t)W * 4}))
             return fail(KATA_EINVAL, "out overlaps an input (src, src2 or gs)");
     }
@@ -345,6 +376,14 @@ int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* s
     if (wgs > 65536) return fail(KATA_EINVAL, "wgs=%d", wgs);
     return check_launch(kata::launch_calib_read((const uint8_t*)p, (uint32_t)bytes, out, calib_wgs(wgs), (hipStream_t)stream),
                         "calib_read");
+}
+
+int kata_calib_read_peak(const void* p, size_t bytes, uint32_t* out, void* stream) {
+    if (!p || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (bytes == 0 || bytes > 0x7fffffffu) return fail(KATA_EINVAL, "bytes=%zu must be in 1..2^31-1", bytes);
+    if (!aligned(p, 16)) return fail(KATA_EINVAL, "p must be 16-byte aligned");
+    return check_launch(kata::launch_calib_read_peak((const uint8_t*)p, (uint32_t)bytes, out, calib_wgs(0), (hipStream_t)stream),
+                        "calib_read_peak");
 }
 
 // ------------------------------------------------------------------ host packers
@@ -504,7 +543,8 @@ int kata_dispatch_prefill(kata_dispatch* d, uint64_t wOff, const uint16_t* A, fl
 // ------------------------------------------------------------------ layer-level: the FFN sublayer
 // Engine::step's FFN (src/engine.cpp:176-182): h = H(rmsnorm(x + y) * gs_in) (the residual
 // x + y is kept in xnew), g = W_gate h, u = W_up h (one batched launch), t = H(silu(g) u *
-// gs_down), out = W_down t.  work: H + 3F floats.
+// gs_down), out = W_down t.  work: H + 3F floats; h and t are held in the GEMV's operand form
+// (written by the transforms, fewer bytes than the floats).
 int kata_dispatch_ffn_decode(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
                              const float* y, float* xnew, const float* gs_in, const float* gs_down, float* work,
                              float* out, int H, int F, void* stream) {
@@ -514,14 +554,14 @@ int kata_dispatch_ffn_decode(kata_dispatch* d, uint64_t offGate, uint64_t offUp,
     float* g = work + H;
     float* u = g + F;
     float* t = u + F;
-    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_F32, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, 1, stream);
+    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_XQ, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, 1, stream);
     if (rc) return rc;
     const uint8_t* Wg[2] = {d->wbase + offGate, d->wbase + offUp};
     float* Yg[2] = {g, u};
     const int Ng[2] = {F, F};
-    if ((rc = kata_gemv_ptq1_batch(2, Wg, Yg, Ng, h, KATA_F32, KATA_X_ROWS, H, 1, stream))) return rc;
-    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_F32, KATA_X_ROWS, F, 1, 1, stream))) return rc;
-    return kata_gemv_ptq1(d->wbase + offDown, t, KATA_F32, KATA_X_ROWS, out, F, H, 1, stream);
+    if ((rc = kata_gemv_ptq1_batch(2, Wg, Yg, Ng, h, KATA_XQ, KATA_X_ROWS, H, 1, stream))) return rc;
+    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_XQ, KATA_X_ROWS, F, 1, 1, stream))) return rc;
+    return kata_gemv_ptq1(d->wbase + offDown, t, KATA_XQ, KATA_X_ROWS, out, F, H, 1, stream);
 }
 
 // The same sublayer for M prefill rows (src/engine.cpp:247-300): the GEMMs take fp16 rows,
@@ -573,8 +613,9 @@ int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp,
 }
 
 // ------------------------------------------------------------------ sublayer halves
-// Work layout of kata_dispatch_in / _out for a transform width K and M rows: decode fp32
-// [K]; verify fp16 [M][K]; prefill fp16 [M][K], then int8 [M][K] and fp32 [K/128][M] for the
+// Work layout of kata_dispatch_in / _out for a transform width K and M rows: decode the
+// GEMV's operand form (kata_gemv_xq_bytes(K, 1) <= 4 K bytes, the size kept from fp32 rows);
+// verify fp16 [M][K]; prefill fp16 [M][K], then int8 [M][K] and fp32 [K/128][M] for the
 // int8 path's quantised rows and scales (16-byte aligned parts).
 static size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
@@ -591,7 +632,7 @@ size_t kata_dispatch_work_bytes(int form, int K, int M) {
 
 namespace {
 struct HalfWork {
-    void* act;      // the transformed activation: fp32 (decode) or fp16 rows
+    void* act;      // the transformed activation: the GEMV operand form (decode) or fp16 rows
     int8_t* A8;     // prefill: quantised rows
     float* SX;      // prefill: their group scales [K/128][M]
 };
@@ -617,7 +658,7 @@ int half_matmul(kata_dispatch* d, int form, uint64_t off, const char* name, cons
     const uint8_t* Wm = d->wbase + off;
     switch (form) {
         case KATA_FORM_DECODE:
-            return kata_gemv_ptq1(Wm, w.act, KATA_F32, KATA_X_ROWS, out, K, N, 1, st);
+            return kata_gemv_ptq1(Wm, w.act, KATA_XQ, KATA_X_ROWS, out, K, N, 1, st);
         case KATA_FORM_VERIFY:
             return kata_gemv_ptq1_wide(Wm, w.act, KATA_F16, out, K, N, M, st);
         default:
@@ -644,13 +685,13 @@ int kata_dispatch_in(kata_dispatch* d, int form, int count, const uint64_t* offs
     }
     const hipStream_t st = (hipStream_t)stream;
     const HalfWork w = half_work(work, H, M);
-    const int act_dt = form == KATA_FORM_DECODE ? KATA_F32 : KATA_F16;
+    const int act_dt = form == KATA_FORM_DECODE ? KATA_XQ : KATA_F16;
     int rc = kata_add_rms_fwht(x, y, gs, w.act, act_dt, KATA_X_ROWS, xnew, gamma, hout, hout_dtype, H, M, stream);
     if (rc) return rc;
     if (form != KATA_FORM_PREFILL) {                 // one launch for all matrices that read h
         const uint8_t* Wm[4];
         for (int i = 0; i < count; i++) Wm[i] = d->wbase + offs[i];
-        if (form == KATA_FORM_DECODE) return kata_gemv_ptq1_batch(count, Wm, outs, N, w.act, KATA_F32, KATA_X_ROWS, H, 1, stream);
+        if (form == KATA_FORM_DECODE) return kata_gemv_ptq1_batch(count, Wm, outs, N, w.act, KATA_XQ, KATA_X_ROWS, H, 1, stream);
         return kata_gemv_ptq1_wide_batch(count, Wm, outs, N, w.act, KATA_F16, H, M, stream);
     }
     bool quantised = false;                          // prefill: quantise h once for its int8 matrices
@@ -669,7 +710,7 @@ int kata_dispatch_out(kata_dispatch* d, int form, uint64_t off, const char* name
     if (int rc = check_form(form, M, W)) return rc;
     if (H <= 0) return fail(KATA_EINVAL, "H=%d must be positive", H);
     const HalfWork w = half_work(work, W, M);
-    int rc = kata_rms_fwht(src, src2, gs, w.act, form == KATA_FORM_DECODE ? KATA_F32 : KATA_F16, KATA_X_ROWS, W, M, mode,
+    int rc = kata_rms_fwht(src, src2, gs, w.act, form == KATA_FORM_DECODE ? KATA_XQ : KATA_F16, KATA_X_ROWS, W, M, mode,
                            stream);
     if (rc) return rc;
     return half_matmul(d, form, off, name, w, out, W, H, M, false, (hipStream_t)stream);

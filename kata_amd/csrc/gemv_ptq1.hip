@@ -27,6 +27,7 @@
 //    operand in registers while it walks the CU's tiles (see the kernel comment); no
 //    atomics, deterministic.
 #include "common.h"
+#include "gemv_operand.h"
 #include "launch.h"
 
 #include <algorithm>
@@ -37,12 +38,14 @@ namespace kata {
 
 namespace {
 
-constexpr float kQMax = 32639.0f;   // |q| <= 32639 keeps hi = (q+128)>>8 inside int8
-constexpr int kDenseMfma = 2;      // MFMAs per block: the dense layout, 32 trits per lane group
-constexpr int kAImageBytes = kDenseMfma * 4 * 16;   // per block and A row (token, limb)
 constexpr int kWaves = 16;
 constexpr int kChunkMax = 3;   // 8-element activation chunks per thread: K <= 3 * 8 * 1024
 constexpr int kMaxMats = 4;    // matrices sharing one activation in one launch
+// Where the decode GEMV's activation comes from: raw rows loaded per thread into registers,
+// raw rows staged in LDS by wave 0's copies (both quantised by every workgroup), or the
+// operand form (gemv_operand.h: quantised once by its producer), copied into LDS.
+constexpr int kXmRegs = 0, kXmStage = 1, kXmOperand = 2;
+constexpr int kXqChunks = 8;   // 16-byte pieces of the operand form per thread: <= 128 KB
 
 // The matrices of one launch (same K, same activation): matrix i is W[i] (N[i] rows), its
 // output rows go to y[i][t * ldy[i] + row], and workgroups [wg0[i], wg0[i+1]) serve it with
@@ -57,37 +60,7 @@ struct GemvMats {
     int count;
 };
 
-// The dense operand layout (both GEMVs): lane group g of a B column (one row, one block) holds the
-// 32 trits of qs bytes 6g .. 6g + 5 (all five digits) and two digits of qh byte 24 + (g >> 1)
-// (digits 2(g & 1) and 2(g & 1) + 1), so two MFMAs cover the block's 128 trits with no empty
-// slot.  With c0..c5 the lane's six qs bytes the B dwords are
-//   m=0: L(c0) L(c1) L(c2) L(c3)      m=1: L(c4) L(c5) Z(c0..c3) {Z(c4), Z(c5), Q(a), Q(a+1)}
-// (L = digits 1..4, byte n - 1 for digit n; Z = digit 0; Q = the qh digits).  The lane reads
-// the 8 bytes at 4-byte aligned gemv_dense_byte0(g) (c0 at byte offset 2 (g & 1)) and the
-// dword at block byte 24 (qh and the scale).  Offset of element e in the block's A image
-// [m 2][g 4][i 2T][16 B]:
-__host__ __device__ constexpr int gemv_dense_byte0(int g) { return g == 0 ? 0 : g == 1 ? 4 : g == 2 ? 12 : 16; }
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-__host__ __device__ constexpr int gemv_dense_img_off(int e, int T) {
-    int p = 0, n = 0;
-    ptq1_elem_src(e, p, n);
-    int g = 0, m = 1, slot = 0;
-    if (p < 24) {
-        g = p / 6;
-        const int j = p - 6 * g;
-        if (n > 0) {
-            m = j < 4 ? 0 : 1;
-            slot = 4 * (j & 3) + n - 1;
-        } else {
-            slot = 8 + j;
-        }
-    } else {
-        g = 2 * (p - 24) + (n >> 1);
-        slot = 14 + (n & 1);
-    }
-    return m * (4 * 2 * T * 16) + g * (2 * T * 16) + slot;
-}
-
 // Image offsets of the 8 elements a quantising thread owns: thread index & 63 =
 // 16*kq + sub, elements 8*sub .. 8*sub + 7 of a block; [T - 1][idx][e].
 struct alignas(16) ImgOffTable {
@@ -356,11 +329,12 @@ __device__ inline void dense_decode(uint32_t w0, uint32_t w1, uint32_t wq, lds_u
 // Dynamic LDS: A image (384*T B per virtual block, quarters 64 B apart), (scale, 0)
 // pairs [vb][t], the scatter offsets (1 KB), a scratch slot for the off-diagonal lanes
 // (512 B), then item sums [S][T][16] floats, which with XS first hold the raw activation.
-template <int T, int LR, int D, bool PAD, bool XS, bool MULTI, bool STRIDE>
+template <int T, int LR, int D, bool PAD, int XM, bool MULTI, bool STRIDE>
 __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __restrict__ x, int x_dtype, int x_layout,
                                                     int K, int nq) {
 #pragma clang fp contract(off)
     static_assert(D % 2 == 0 && D >= 4, "operand double buffers alternate by item parity");
+    constexpr bool XS = XM == kXmStage, XQ = XM == kXmOperand;
     constexpr int ASTRIDE = 4 * 2 * T * 16;      // A image bytes per (virtual block, MFMA)
     constexpr int BLK = kDenseMfma * ASTRIDE;     // A image bytes per virtual block
     constexpr int REPS = 1 << LR;
@@ -436,20 +410,31 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // quarter (j >> 4) & 3 and sub-block position j & 15 do not depend on i.
     const int nch = K >> 3;
     const int xbytes = T * K * (x_dtype == 1 ? 2 : 4);
-    float v[XS ? 1 : kChunkMax][T][8];
-    if (wave == 0) {
+    float v[XM != kXmRegs ? 1 : kChunkMax][T][8];
+    if (!XQ && wave == 0) {
         dma16((const uint4*)&kImgOff.v[T - 1][0][0] + lane, lds_addr(Os));
         if constexpr (XS) {
             const int xvec = xbytes / 16;
             for (int o = 0; o < xvec; o += 64) dma16((const uint4*)x + min(o + lane, xvec - 1), lds_addr(Xs + o * 16));
         }
     }
-    if constexpr (!XS) {
+    if constexpr (XM == kXmRegs) {
 #pragma unroll
         for (int i = 0; i < kChunkMax; i++) {
             const int j = tid + 1024 * i;
             if (j < nch) load_x8<T>(x, x_dtype, x_layout, K, 8 * j, v[i]);
         }
+    }
+    // XQ: the operand form, 16 bytes per thread and piece, loaded before the weight ring so
+    // that it lands first; pieces past its end read zero (whole absent pieces are skipped)
+    const int xqb = 4 * qbytes + 8 * nbv * T;
+    uint4 xr[XQ ? kXqChunks : 1];
+    if constexpr (XQ) {
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, xqb, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < kXqChunks; i++)
+            if (i * 1024 * 16 < xqb)
+                xr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (tid + 1024 * i) * 16, 0, 0));
     }
 
     // (1b) trit table.  Consecutive threads store consecutive 16-byte words (no bank
@@ -462,8 +447,10 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     }
     // clear the A image (slots without an element and padding blocks stay zero) and the
     // scales of the padding blocks
-    for (int o = tid; o < gemv_a_lds_bytes(qbytes, T) / 16; o += 1024) ((uint4*)As)[o] = make_uint4(0, 0, 0, 0);
-    for (int o = nb * T + tid; o < nbv * T; o += 1024) ((int2*)Ss)[o] = make_int2(0, 0);
+    if constexpr (!XQ) {
+        for (int o = tid; o < gemv_a_lds_bytes(qbytes, T) / 16; o += 1024) ((uint4*)As)[o] = make_uint4(0, 0, 0, 0);
+        for (int o = nb * T + tid; o < nbv * T; o += 1024) ((int2*)Ss)[o] = make_int2(0, 0);
+    }
 
     // (1c) weight ring.  Raw buffer loads: per-lane offset (row r of the tile, block kq of
     // the step, the lane group's 8 bytes, and the block's qh / scale dword) plus a
@@ -505,17 +492,28 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 #pragma unroll
     for (int u = 0; u < D; u++) load_next(u);
 
+    // XQ: the operand form into the LDS layout (piece at byte o of the form: o plus one pad
+    // per quarter before it; the scale pairs follow the fourth quarter's pad)
+    if constexpr (XQ) {
+#pragma unroll
+        for (int i = 0; i < kXqChunks; i++) {
+            const int o = (tid + 1024 * i) * 16;
+            if (i * 1024 * 16 < xqb && o < xqb) {
+                const int q = (o >= qbytes) + (o >= 2 * qbytes) + (o >= 3 * qbytes) + (o >= 4 * qbytes);
+                *(uint4*)(As + o + q * QPAD) = xr[i];
+            }
+        }
+    }
     // the staged offsets and activation (wave 0: everything but the D ring loads has
-    // landed), the trit table and the cleared image are visible after this barrier
+    // landed), the trit table and the cleared image (XQ: the copied operand) are visible
+    // after this barrier
     __builtin_amdgcn_s_waitcnt((D & 15) | ((D >> 4) << 14) | (7 << 4) | (0 << 8));   // vmcnt(D) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
 
-    // (2) quantise: per block and token s = amax / 32639, q = rint(x * (32639 / amax))
-    // (0 if amax = 0; |q| <= 32639, so hi = (q + 128) >> 8 fits int8), and (3) scatter the
-    // limbs hi and lo = q - 256 hi (the low byte of q): element 8*(j & 15) + e of block
-    // j >> 4 goes to image offset gemv_dense_img_off(8*(j & 15) + e, T) +
-    // 16*(2t + limb) of that block
-    {
+    // (2) quantise (the quantiser of gemv_operand.h) and (3) scatter the limbs: element
+    // 8*(j & 15) + e of block j >> 4 goes to image offset gemv_dense_img_off(8*(j & 15) + e, T)
+    // + 16*(2t + limb) of that block.  XQ: done by the operand's producer.
+    if constexpr (!XQ) {
         const uint4 offw = *(const uint4*)(Os + (tid & 63) * 16);
         const uint32_t ow[4] = {offw.x, offw.y, offw.z, offw.w};
         int off[8];
@@ -527,25 +525,13 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 float a = 0.0f;
-                bool bad = false;
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float av = fabsf(vv[t][e]);
-                    bad |= !(av <= 3.402823466e38f);   // NaN or infinity
-                    a = fmaxf(a, av);
-                }
-                a = row16_max(bad ? __builtin_inff() : a);
-                // a block holding a non-finite value gets scale NaN: every output row is NaN
-                const bool blk_bad = !(a <= 3.402823466e38f);
-                const float inv = (a > 0.0f && !blk_bad) ? kQMax / a : 0.0f;
-                const float sc = blk_bad ? __builtin_nanf("") : a * (1.0f / kQMax);
+                for (int e = 0; e < 8; e++) a = fmaxf(a, gemv_amax_term(vv[t][e]));
+                float inv, sc;
+                gemv_block_scale(row16_max(a), inv, sc);
                 if ((j & 15) == 0) ((int2*)Ss)[b * T + t] = make_int2(__builtin_bit_cast(int, sc), 0);
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int q = (int)rintf(vv[t][e] * inv);
-                    img[off[e] + 32 * t] = (uint8_t)((q + 128) >> 8);
-                    img[off[e] + 32 * t + 16] = (uint8_t)q;
-                }
+                for (int e = 0; e < 8; e++) gemv_limbs(vv[t][e], inv, img[off[e] + 32 * t], img[off[e] + 32 * t + 16]);
             }
         };
         if constexpr (XS) {
@@ -561,10 +547,10 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
                 if (j < nch) process(j, v[i]);
             }
         }
+        // LDS-only barrier: a release fence here would also wait for the weight ring
+        __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
     }
-    // LDS-only barrier: a release fence here would also wait for the weight ring
-    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
 
     // (4) main loop
     const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
@@ -1001,8 +987,6 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
 
 }  // namespace
 
-// steps (of 4 blocks) per tile, rounded up to whole pairs; blocks past K are zero padding
-static int gemv_nq(int K) { return ((K / kGroup + 3) / 4 + 1) & ~1; }
 
 constexpr int kLdsMax = 160 * 1024;
 
@@ -1025,15 +1009,15 @@ static int device_cus() {
     return device_cu_count(&n_cu) == hipSuccess ? n_cu : 256;
 }
 
-template <int T, int LR, bool PAD, bool XS, bool MULTI, bool STRIDE = false>
+template <int T, int LR, bool PAD, int XM, bool MULTI, bool STRIDE = false>
 static hipError_t launch_gemv_cfg(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
                                   hipStream_t s) {
     // raised once per process (a function-local static: thread-safe initialisation)
-    static const hipError_t attr = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)k_gemv_ptq1<T, LR, kRing, PAD, XM, MULTI, STRIDE>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        kLdsMax - gemv_static_lds_bytes(LR));
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XS, MULTI, STRIDE>), dim3(P.wg0[P.count]), dim3(1024),
+    hipLaunchKernelGGL((k_gemv_ptq1<T, LR, kRing, PAD, XM, MULTI, STRIDE>), dim3(P.wg0[P.count]), dim3(1024),
                        lds - gemv_static_lds_bytes(LR), s, P, x, x_dtype, x_layout, K, gemv_nq(K));
     return hipGetLastError();
 }
@@ -1046,16 +1030,16 @@ static bool gemv_strided(const GemvMats& P, int K) {
     return P.count == 1 && np > 0 && G >= 2 && G * np >= 15 && P.tpw[0] >= 64;
 }
 
-template <int T, int LR, bool XS>
+template <int T, int LR, int XM>
 static hipError_t launch_gemv_pad(const GemvMats& P, const void* x, int x_dtype, int x_layout, int K, int lds,
                                   hipStream_t s) {
     if (P.count > 1)
-        return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XS, true>(P, x, x_dtype, x_layout, K, lds, s)
-                                : launch_gemv_cfg<T, LR, false, XS, true>(P, x, x_dtype, x_layout, K, lds, s);
+        return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XM, true>(P, x, x_dtype, x_layout, K, lds, s)
+                                : launch_gemv_cfg<T, LR, false, XM, true>(P, x, x_dtype, x_layout, K, lds, s);
     if ((K / kGroup) % 8 == 0 && gemv_strided(P, K))
-        return launch_gemv_cfg<T, LR, false, XS, false, true>(P, x, x_dtype, x_layout, K, lds, s);
-    return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XS, false>(P, x, x_dtype, x_layout, K, lds, s)
-                            : launch_gemv_cfg<T, LR, false, XS, false>(P, x, x_dtype, x_layout, K, lds, s);
+        return launch_gemv_cfg<T, LR, false, XM, false, true>(P, x, x_dtype, x_layout, K, lds, s);
+    return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XM, false>(P, x, x_dtype, x_layout, K, lds, s)
+                            : launch_gemv_cfg<T, LR, false, XM, false>(P, x, x_dtype, x_layout, K, lds, s);
 }
 
 // Split at most `wgs` workgroups over the matrices in proportion to their tiles (at least
@@ -1093,9 +1077,9 @@ static int gemv_split(GemvMats& P, int wgs) {
 }
 
 // Configuration choice, first that fits 160 KB of LDS: about one workgroup per CU, else
-// smaller tile ranges (more workgroups); the staged activation (XS) before per-thread
-// loads, except for K > 8192 (measured: 0.7 us faster at K = 17408, slower at 5120); a
-// 64-replica trit table (one v_perm per lookup) before a 16-replica one.
+// smaller tile ranges (more workgroups); for raw activations the staged copy (kXmStage)
+// before per-thread loads, except for K > 8192 (measured: 0.7 us faster at K = 17408,
+// slower at 5120); a 64-replica trit table (one v_perm per lookup) before a 16-replica one.
 template <int T>
 static hipError_t launch_gemv_t(GemvMats& P, const void* x, int x_dtype, int x_layout, int K, hipStream_t s) {
     const int cus = device_cus();
@@ -1104,19 +1088,82 @@ static hipError_t launch_gemv_t(GemvMats& P, const void* x, int x_dtype, int x_l
     for (int wgs = cus;; wgs *= 2) {
         const int tpw = gemv_split(P, wgs);
         int lds;
+        if (x_dtype == kXDtypeOperand) {
+            if ((lds = gemv_lds_bytes(K, T, 6, tpw, 0)) <= kLdsMax)
+                return launch_gemv_pad<T, 6, kXmOperand>(P, x, x_dtype, x_layout, K, lds, s);
+            if ((lds = gemv_lds_bytes(K, T, 4, tpw, 0)) <= kLdsMax)
+                return launch_gemv_pad<T, 4, kXmOperand>(P, x, x_dtype, x_layout, K, lds, s);
+            if (tpw == 1) return hipErrorInvalidValue;
+            continue;
+        }
         // long activations (K > 8192): per-thread loads start sooner than one wave's copy
         if (K > 8192 && regs_ok && (lds = gemv_lds_bytes(K, T, 6, tpw, 0)) <= kLdsMax)
-            return launch_gemv_pad<T, 6, false>(P, x, x_dtype, x_layout, K, lds, s);
+            return launch_gemv_pad<T, 6, kXmRegs>(P, x, x_dtype, x_layout, K, lds, s);
         if ((lds = gemv_lds_bytes(K, T, 6, tpw, xbytes)) <= kLdsMax)
-            return launch_gemv_pad<T, 6, true>(P, x, x_dtype, x_layout, K, lds, s);
+            return launch_gemv_pad<T, 6, kXmStage>(P, x, x_dtype, x_layout, K, lds, s);
         if ((lds = gemv_lds_bytes(K, T, 4, tpw, xbytes)) <= kLdsMax)
-            return launch_gemv_pad<T, 4, true>(P, x, x_dtype, x_layout, K, lds, s);
+            return launch_gemv_pad<T, 4, kXmStage>(P, x, x_dtype, x_layout, K, lds, s);
         if (regs_ok && (lds = gemv_lds_bytes(K, T, 6, tpw, 0)) <= kLdsMax)
-            return launch_gemv_pad<T, 6, false>(P, x, x_dtype, x_layout, K, lds, s);
+            return launch_gemv_pad<T, 6, kXmRegs>(P, x, x_dtype, x_layout, K, lds, s);
         if (regs_ok && (lds = gemv_lds_bytes(K, T, 4, tpw, 0)) <= kLdsMax)
-            return launch_gemv_pad<T, 4, false>(P, x, x_dtype, x_layout, K, lds, s);
+            return launch_gemv_pad<T, 4, kXmRegs>(P, x, x_dtype, x_layout, K, lds, s);
         if (tpw == 1) return hipErrorInvalidValue;
     }
+}
+
+// The operand form (gemv_operand.h) of T raw activation rows: one 256-thread workgroup per 4
+// steps (16 blocks, 4 per quarter); thread j quantises elements 8 (j & 15) .. + 7 of block
+// 16 w + (j >> 4) (the 16 threads of a block are one DPP row) into an LDS copy of the 16
+// block images, which is then written out with 16-byte stores.  Blocks past K are zero.
+template <int T>
+__global__ __launch_bounds__(256) void k_gemv_prepare(const void* __restrict__ x, int x_dtype, int x_layout, int K,
+                                                      uint8_t* __restrict__ xq) {
+#pragma clang fp contract(off)
+    constexpr int BLK = gemv_xq_blk_bytes(T);
+    __shared__ __align__(16) uint8_t stg[16 * BLK];
+    const int tid = threadIdx.x, sub = tid & 15, w = blockIdx.x;
+    const int nb = K >> 7, nq = gemv_nq(K), qbytes = nq * BLK;
+    const int b = 16 * w + (tid >> 4);
+    float v[T][8];
+    if (b < nb) {
+        load_x8<T>(x, x_dtype, x_layout, K, 128 * b + 8 * sub, v);
+    } else {
+#pragma unroll
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[t][e] = 0.0f;
+    }
+    uint8_t* img = stg + ((b & 3) * 4 + ((b >> 2) & 3)) * BLK;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) a = fmaxf(a, gemv_amax_term(v[t][e]));
+        float inv, sc;
+        gemv_block_scale(row16_max(a), inv, sc);
+        if (sub == 0 && b < 4 * nq) ((int2*)(xq + 4 * qbytes))[b * T + t] = make_int2(__builtin_bit_cast(int, sc), 0);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int off = kImgOff.v[T - 1][sub][e] + 32 * t;
+            gemv_limbs(v[t][e], inv, img[off], img[off + 16]);
+        }
+    }
+    __syncthreads();
+    // piece p: quarter p / (4 BLK / 16), then 4 consecutive steps of that quarter
+    constexpr int PQ = 4 * BLK / 16;
+    for (int p = tid; p < 4 * PQ; p += 256) {
+        const int q = p / PQ, r = p % PQ, c = 4 * w + (r * 16) / BLK;
+        if (c < nq) *(uint4*)(xq + q * qbytes + 4 * w * BLK + r * 16) = *(const uint4*)(stg + p * 16);
+    }
+}
+
+hipError_t launch_gemv_prepare(const void* x, int x_dtype, int x_layout, int K, int T, void* xq, hipStream_t s) {
+    const dim3 grid((unsigned)((gemv_nq(K) + 3) / 4));
+    if (T == 1)
+        hipLaunchKernelGGL(k_gemv_prepare<1>, grid, dim3(256), 0, s, x, x_dtype, x_layout, K, (uint8_t*)xq);
+    else
+        hipLaunchKernelGGL(k_gemv_prepare<2>, grid, dim3(256), 0, s, x, x_dtype, x_layout, K, (uint8_t*)xq);
+    return hipGetLastError();
 }
 
 // count matrices of N[i] rows sharing x, one launch.  A matrix whose byte size does not fit

@@ -22,6 +22,8 @@ hipError_t launch_gemv_ptq1_multi(int count, const uint8_t* const* W, float* con
                                   int x_dtype, int x_layout, int K, int T, hipStream_t s);
 int gemv_max_k(int T);   // largest K the PTQ1_0 GEMV accepts (its activation image lives in LDS)
 int gemv_max_mats();     // most matrices one launch takes
+// the operand form of T (1, 2) raw activation rows (x_dtype KATA_XQ of the GEMV)
+hipError_t launch_gemv_prepare(const void* x, int x_dtype, int x_layout, int K, int T, void* xq, hipStream_t s);
 // wide verification GEMV, T in 1..8 token rows x [T][K] (fp16 or fp32), y [T][N]
 hipError_t launch_gemv_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                             hipStream_t s);
@@ -62,6 +64,8 @@ hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs
 // ---- measurement helpers (calib.hip): empty kernel and plain streaming read, wgs x 1024
 hipError_t launch_calib_empty(uint32_t* out, int wgs, hipStream_t s);
 hipError_t launch_calib_read(const uint8_t* p, uint32_t bytes, uint32_t* out, int wgs, hipStream_t s);
+// the read ceiling: two 256-thread workgroups per CU, non-temporal 16-byte loads
+hipError_t launch_calib_read_peak(const uint8_t* p, uint32_t bytes, uint32_t* out, int cus, hipStream_t s);
 
 // ---- argmax of the logits (argmax.hip)
 hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s);

@@ -10,7 +10,9 @@
 //   mode 3: u = src * gs
 //   out[block b][j] = (1/32) sum_k (-1)^popcount(j & k) u[1024 b + k]
 // fp32 arithmetic; out fp32 or fp16, rows [M][W] or (M = 2) the two tokens interleaved
-// per element, [W][2] (the half2 operand of the T = 2 verify GEMV).
+// per element, [W][2] (the half2 operand of the T = 2 verify GEMV), or (M <= 2) the decode
+// GEMV's operand form of the fp32 values (gemv_operand.h), staged per 1024-block in LDS
+// and written as whole 16-byte A rows.
 //
 // Design: a 256-thread workgroup per (1024-block, token) for few rows (more workgroups in
 // flight; each reads the row for its sum of squares, L2-resident after the first), per
@@ -19,6 +21,7 @@
 // exchange), bits 8-9 its wave (one LDS transpose).  The sum of squares is reduced in a
 // fixed order: a butterfly across the wave's lanes, then the 4 waves through LDS.
 #include "common.h"
+#include "gemv_operand.h"
 #include "launch.h"
 
 namespace kata {
@@ -107,6 +110,39 @@ __device__ inline int gdn_perm(int i) {
 // NB blocks per workgroup: NB = 1 -> grid (W/1024, M), every block's workgroup reads the
 // row for the sum of squares (few rows: more workgroups in flight); NB = W/1024 -> grid M,
 // one workgroup per row, the row read once and held in registers (many rows).
+// This workgroup's 8 blocks of token m (elements 4 tid + r of the 1024-block blk) in the
+// decode GEMV's operand form: the 32 lanes of a block reduce its amax, the limbs go to an
+// LDS copy of the 8 block images, then 128 threads store the token's 16-byte A rows.
+__device__ inline void store_operand(const float (&v)[4], int tid, int blk, int m, int M, int W, uint8_t* xs,
+                                     uint8_t* __restrict__ xq) {
+#pragma clang fp contract(off)
+    const int BLK = gemv_xq_blk_bytes(M), qbytes = gemv_xq_qbytes(W, M);
+    float a = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) a = fmaxf(a, gemv_amax_term(v[r]));
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+    float inv, sc;
+    gemv_block_scale(a, inv, sc);
+    const int bl = tid >> 5, b = 8 * blk + bl;
+    __syncthreads();                              // the transform's last reads of xs
+    uint8_t* img = xs + bl * BLK + 32 * m;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int off = gemv_dense_img_off((4 * tid + r) & 127, M);
+        gemv_limbs(v[r], inv, img[off], img[off + 16]);
+    }
+    if ((tid & 31) == 0) ((int2*)(xq + 4 * qbytes))[b * M + m] = make_int2(__builtin_bit_cast(int, sc), 0);
+    __syncthreads();
+    if (tid < 128) {
+        // row (mm, g, limb) of block bl: A image bytes mm (8 M 16) + g (2 M 16) + (2 m + limb) 16
+        const int pb = tid >> 4, mm = (tid >> 3) & 1, g = (tid >> 1) & 3, limb = tid & 1;
+        const int off = mm * (4 * 2 * M * 16) + g * (2 * M * 16) + (2 * m + limb) * 16;
+        const int bb = 8 * blk + pb;
+        *(uint4*)(xq + (bb & 3) * qbytes + (bb >> 2) * BLK + off) = *(const uint4*)(xs + pb * BLK + off);
+    }
+}
+
 template <int NB>
 __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src, const float* __restrict__ src2,
                                                    const float* __restrict__ gs, void* __restrict__ out, int out_dtype,
@@ -189,7 +225,9 @@ __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src
             for (int r = 0; r < 4; r++) v[r] = av[r] * gv[r];
         }
         fwht1024(v, tid, xs);
-        if (out_dtype == 0) {
+        if (out_dtype == 2) {
+            store_operand(v, tid, blk0 + b, m, NB == 1 ? gridDim.y : gridDim.x, W, (uint8_t*)xs, (uint8_t*)out);
+        } else if (out_dtype == 0) {
             *(float4*)((float*)out + ro + base) = make_float4(v[0], v[1], v[2], v[3]);
         } else if (out_layout == 0) {
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -208,8 +246,9 @@ __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src
 hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs, void* out, int out_dtype,
                             int out_layout, float* xnew, const float* gamma, void* hout, int flags, int W, int M,
                             int mode, hipStream_t s) {
-    // whole rows per workgroup once there are enough rows to fill the CUs (hidden width 5120)
-    if (W == 5120 && M >= 64)
+    // whole rows per workgroup once there are enough rows to fill the CUs (hidden width 5120);
+    // the operand form (out_dtype 2) takes M <= 2
+    if (W == 5120 && M >= 64 && out_dtype != 2)
         hipLaunchKernelGGL(k_norm_fwht<5>, dim3(M), dim3(256), 0, s, src, src2, gs, out, out_dtype, out_layout, xnew,
                            gamma, hout, flags, W, mode);
     else

@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 import torch
 
-from .capi import KATA_F16, KATA_F32, KATA_X_HALF2, KATA_X_ROWS, check, lib
+from .capi import KATA_F16, KATA_F32, KATA_X_HALF2, KATA_X_ROWS, KATA_XQ, check, lib
 
 GROUP, BLOCK_BYTES = 128, 28
 Q8_GROUP, Q8_BLOCK_BYTES = 32, 34
@@ -49,11 +49,39 @@ def _ptq1_bytes(K: int, N: int) -> int:
 
 
 def _xdtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.uint8:
+        return KATA_XQ
     if x.dtype == torch.float16:
         return KATA_F16
     if x.dtype == torch.float32:
         return KATA_F32
-    raise ValueError(f"activation dtype {x.dtype} not supported (fp16 or fp32)")
+    raise ValueError(f"activation dtype {x.dtype} not supported (fp16, fp32 or the uint8 operand form)")
+
+
+def _x_bytes(x: torch.Tensor, K: int, T: int) -> int:
+    """Bytes the GEMV reads of x: the operand form's size for uint8, else T*K elements."""
+    return gemv_xq_bytes(K, T) if x.dtype == torch.uint8 else T * K * x.element_size()
+
+
+def gemv_xq_bytes(K: int, T: int) -> int:
+    """Bytes of the decode GEMV's operand form of T (1, 2) rows of K (0: unsupported)."""
+    return int(lib().kata_gemv_xq_bytes(K, T))
+
+
+def gemv_prepare_x(x: torch.Tensor, K: int, T: int = 1, half2: bool = False,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """The decode GEMV's operand form (uint8) of x ([T][K] fp16/fp32, or [K][2] fp16 when half2):
+    quantised once, then passed as x to gemv_ptq1 / gemv_ptq1_batch (same y bit for bit)."""
+    n = gemv_xq_bytes(K, T)
+    if n == 0:
+        raise ValueError(f"K={K} T={T}: no operand form")
+    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("out", out, n)
+    _need_gpu(x)
+    xq = out if out is not None else torch.empty(n, dtype=torch.uint8, device=x.device)
+    check(lib().kata_gemv_prepare_x(_ptr(x), _xdtype(x), KATA_X_HALF2 if half2 else KATA_X_ROWS, K, T, _ptr(xq),
+                                    _stream(x)))
+    return xq
 
 
 # ----------------------------------------------------------------------------- GEMVs
@@ -61,7 +89,7 @@ def gemv_ptq1(W: torch.Tensor, x: torch.Tensor, K: int, N: int, T: int = 1, half
               out: torch.Tensor | None = None) -> torch.Tensor:
     """y[T][N] fp32 = PTQ1_0 W (N x K) times x ([T][K], or [K][2] fp16 when half2)."""
     _need_bytes("W", W, _ptq1_bytes(K, N))
-    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("x", x, _x_bytes(x, K, T))
     _need_bytes("out", out, T * N * 4)
     _need_gpu(W, x)
     y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
@@ -77,7 +105,7 @@ def gemv_ptq1_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, half2: bool = F
     for i, (W, N) in enumerate(zip(Ws, Ns)):
         _need_bytes(f"Ws[{i}]", W, _ptq1_bytes(K, N))
         _need_bytes(f"outs[{i}]", outs[i] if outs is not None else None, T * N * 4)
-    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("x", x, _x_bytes(x, K, T))
     _need_gpu(x, *Ws)
     n = len(Ws)
     ys = outs if outs is not None else [torch.empty((T, N), dtype=torch.float32, device=x.device) for N in Ns]
@@ -246,17 +274,28 @@ def expand_i8(W: torch.Tensor, K: int, N: int):
 
 # ----------------------------------------------------------------------------- host packers
 # ----------------------------------------------------------------------------- matmul input transform
+def _fwht_out(out_dtype, half2: bool, M: int, W: int, device) -> torch.Tensor:
+    """Output of an input transform: fp32/fp16 rows, half2 [W][2], or (uint8) the operand form."""
+    if half2:
+        return torch.empty((W, 2), dtype=torch.float16, device=device)
+    if out_dtype == torch.uint8:
+        n = gemv_xq_bytes(W, M)
+        if n == 0:
+            raise ValueError(f"W={W} M={M}: no operand form")
+        return torch.empty(n, dtype=torch.uint8, device=device)
+    return torch.empty((M, W), dtype=out_dtype, device=device)
+
+
 def add_rms_fwht(x: torch.Tensor, gs: torch.Tensor, y: torch.Tensor | None = None, gamma: torch.Tensor | None = None,
                  out_dtype=torch.float32, half2: bool = False, want_xnew: bool = False, hout_dtype=torch.float32):
     """Residual add + RMSNorm + sign + 1024-block FWHT of fp32 rows x [M][W] (k_add_rms_fwht):
     returns (out, xnew or None, hout or None)."""
     _need_gpu(x, gs)
     M, W = x.shape
-    out = (torch.empty((W, 2), dtype=torch.float16, device=x.device) if half2
-           else torch.empty((M, W), dtype=out_dtype, device=x.device))
+    out = _fwht_out(out_dtype, half2, M, W, x.device)
     xnew = torch.empty_like(x) if want_xnew else None
     hout = torch.empty((M, W), dtype=hout_dtype, device=x.device) if gamma is not None else None
-    check(lib().kata_add_rms_fwht(_ptr(x), _ptr(y), _ptr(gs), _ptr(out), KATA_F16 if out.dtype == torch.float16 else KATA_F32,
+    check(lib().kata_add_rms_fwht(_ptr(x), _ptr(y), _ptr(gs), _ptr(out), _xdtype(out),
                                   KATA_X_HALF2 if half2 else KATA_X_ROWS, _ptr(xnew), _ptr(gamma), _ptr(hout),
                                   KATA_F16 if hout_dtype == torch.float16 else KATA_F32, W, M, _stream(x)))
     return out, xnew, hout
@@ -267,9 +306,8 @@ def rms_fwht(src: torch.Tensor, gs: torch.Tensor, mode: int, src2: torch.Tensor 
     """The other input transforms (k_rms_fwht): mode 0 RMSNorm, 1 SwiGLU, 2 GDN head order, 3 plain."""
     _need_gpu(src, gs)
     M, W = src.shape
-    out = (torch.empty((W, 2), dtype=torch.float16, device=src.device) if half2
-           else torch.empty((M, W), dtype=out_dtype, device=src.device))
-    check(lib().kata_rms_fwht(_ptr(src), _ptr(src2), _ptr(gs), _ptr(out), KATA_F16 if out.dtype == torch.float16 else KATA_F32,
+    out = _fwht_out(out_dtype, half2, M, W, src.device)
+    check(lib().kata_rms_fwht(_ptr(src), _ptr(src2), _ptr(gs), _ptr(out), _xdtype(out),
                               KATA_X_HALF2 if half2 else KATA_X_ROWS, W, M, mode, _stream(src)))
     return out
 
@@ -294,6 +332,14 @@ def calib_read(buf: torch.Tensor, out: torch.Tensor, nbytes: int | None = None, 
     n = _bytes(buf) if nbytes is None else nbytes
     _need_bytes("buf", buf, n)
     check(lib().kata_calib_read(_ptr(buf), n, _ptr(out), wgs, _stream(buf)))
+
+
+def calib_read_peak(buf: torch.Tensor, out: torch.Tensor, nbytes: int | None = None) -> None:
+    """Plain streaming read of nbytes (default: all) of buf at the fastest plain-read geometry."""
+    _need_gpu(buf, out)
+    n = _bytes(buf) if nbytes is None else nbytes
+    _need_bytes("buf", buf, n)
+    check(lib().kata_calib_read_peak(_ptr(buf), n, _ptr(out), _stream(buf)))
 
 
 def _np_ptr(a: np.ndarray):

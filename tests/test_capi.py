@@ -300,3 +300,33 @@ def test_torch_front_end_checks_sizes():
         ops.gemm_ptq1_i8(torch.zeros((4, 5120), dtype=torch.int8), torch.zeros((40, 2)), W, 5120, 2)
     with pytest.raises(ValueError, match="W holds"):
         ops.expand_f16(W, 5120, 3)
+
+
+def test_gemv_operand_form_sizes_and_rejects():
+    """Sizes of the decode GEMV's operand form (image 256 T B per block over nq even steps of
+    4 blocks, then 8 B scale pairs per block and token) and the argument checks of its
+    producers and consumers, before any launch."""
+    lib = L.lib()
+    nq = lambda K: ((K // 128 + 3) // 4 + 1) & ~1
+    for K, T in ((128, 1), (1152, 2), (5120, 1), (5120, 2), (17408, 1), (17408, 2)):
+        assert lib.kata_gemv_xq_bytes(K, T) == nq(K) * T * (1024 + 32)
+    assert lib.kata_gemv_xq_bytes(5120, 3) == 0 and lib.kata_gemv_xq_bytes(100, 1) == 0
+    assert lib.kata_gemv_xq_bytes(0, 1) == 0
+    big = lib.kata_gemv_ptq1_max_k(1) + 128
+    assert lib.kata_gemv_xq_bytes(big, 1) == 0
+    prep = lib.kata_gemv_prepare_x
+    out = ctypes.c_void_p(0x20000)
+    assert prep(FAKE, 1, 0, 5120, 3, out, None) == KATA_EINVAL          # T
+    assert prep(FAKE, 1, 0, 5000, 1, out, None) == KATA_EINVAL          # K % 128
+    assert prep(FAKE, 2, 0, 5120, 1, out, None) == KATA_EINVAL          # x dtype (not itself)
+    assert prep(FAKE, 0, 1, 5120, 2, out, None) == KATA_EINVAL          # half2 needs fp16
+    assert prep(FAKE, 1, 0, 5120, 1, ctypes.c_void_p(0x20008), None) == KATA_EINVAL   # alignment
+    assert prep(FAKE, 1, 0, 5120, 1, ctypes.c_void_p(0x10000 + 4096), None) == KATA_EINVAL   # overlap
+    assert prep(None, 1, 0, 5120, 1, out, None) == KATA_EINVAL
+    gemv = lib.kata_gemv_ptq1
+    assert gemv(FAKE, out, 2, 1, FAKE, 5120, 64, 2, None) == KATA_EINVAL   # operand form: rows only
+    # transforms: the operand form takes M <= 2 and the rows layout
+    fwht = lib.kata_rms_fwht
+    g = ctypes.c_void_p(0x40000)
+    assert fwht(FAKE, None, g, out, 2, 0, 5120, 3, 3, None) == KATA_EINVAL
+    assert fwht(FAKE, None, g, out, 2, 1, 5120, 2, 3, None) == KATA_EINVAL
