@@ -436,7 +436,9 @@ def run_q8(torch, ops, dev, time_reps, reps):
 
 def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
     """The wide verification GEMV (Engine::dWide) at T = 4 and 8 token rows on the FFN and
-    attention shapes (one weight read for all rows), and verifyWide's gate + up batched."""
+    attention shapes (one weight read for all rows), and verifyWide's gate + up batched: on
+    the operand form of the rows (what the dispatcher's transforms write; t{T}_us) and on fp16
+    rows, quantised by a prep launch first (t{T}_raw_us)."""
     # wide verification GEMV (Engine::dWide): T = 4 and 8 token rows, one weight read
     verify_wide = {}
     for j, (name, K, N, grp) in enumerate(SWEEP):
@@ -447,9 +449,12 @@ def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
             xw = torch.from_numpy(np.random.default_rng(SEED + 350 + j).standard_normal((T, K))
                                   .astype(np.float16)).to(dev)
             yw = torch.empty((T, N), dtype=torch.float32, device=dev)
-            us = time_reps(lambda r: ops.gemv_ptq1_wide(copies[r % ncopies][j], xw, K, N, out=yw), reps)
+            xq = ops.gemv_prepare_x(xw, K, T)
+            us = time_reps(lambda r: ops.gemv_ptq1_wide(copies[r % ncopies][j], xq, K, N, out=yw, T=T), reps)
+            us_raw = time_reps(lambda r: ops.gemv_ptq1_wide(copies[r % ncopies][j], xw, K, N, out=yw), reps)
             ent[f"t{T}_us"] = round(us, 3)
             ent[f"t{T}_GBps"] = round(packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
+            ent[f"t{T}_raw_us"] = round(us_raw, 3)
         verify_wide[name] = ent
     # verifyWide's gate + up in one batched launch (one quantisation of the token rows)
     jg, ju = [i for i, e in enumerate(SWEEP) if e[0] in ("ffn_gate", "ffn_up")]
@@ -458,9 +463,13 @@ def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
     for T in (4, 8):
         xw = torch.from_numpy(np.random.default_rng(SEED + 360).standard_normal((T, K)).astype(np.float16)).to(dev)
         ygu = [torch.empty((T, N), dtype=torch.float32, device=dev) for _ in range(2)]
-        us = time_reps(lambda r: ops.gemv_ptq1_wide_batch([copies[r % ncopies][jg], copies[r % ncopies][ju]], xw, K,
-                                                          [N, N], outs=ygu), reps)
+        xq = ops.gemv_prepare_x(xw, K, T)
+        us = time_reps(lambda r: ops.gemv_ptq1_wide_batch([copies[r % ncopies][jg], copies[r % ncopies][ju]], xq, K,
+                                                          [N, N], outs=ygu, T=T), reps)
+        us_raw = time_reps(lambda r: ops.gemv_ptq1_wide_batch([copies[r % ncopies][jg], copies[r % ncopies][ju]], xw,
+                                                              K, [N, N], outs=ygu), reps)
         ent[f"t{T}_us"] = round(us, 3)
+        ent[f"t{T}_raw_us"] = round(us_raw, 3)
         ent[f"t{T}_GBps"] = round(2 * packed_bytes(K, N) / (us * 1e-6) / 1e9, 1)
     verify_wide["ffn_gate_up_batched"] = ent
     return verify_wide

@@ -46,6 +46,7 @@ int check_launch(hipError_t e, const char* what) {
 }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
 int check_gemv_args(const void* W, const void* x, int x_dtype, int x_layout, const void* y, int K, int N,
                     int T) {
@@ -81,14 +82,16 @@ const char* kata_version(void) { return "kata_amd 0.1 (gfx950)"; }
 int kata_gemv_ptq1_max_k(int T) { return (T == 1 || T == 2) ? kata::gemv_max_k(T) : 0; }
 
 size_t kata_gemv_xq_bytes(int K, int T) {
-    if ((T != 1 && T != 2) || K <= 0 || K % 128 != 0 || K > kata::gemv_max_k(T)) return 0;
-    const int b = kata::gemv_xq_bytes(K, T);
+    if (T < 1 || T > 8 || K <= 0 || K % 128 != 0) return 0;
+    if (T > 2) return (size_t)kata::gemv_xq_bytes(K, T);           // the wide GEMV's image
+    if (K > kata::gemv_max_k(T)) return 0;
+    const long long b = kata::gemv_xq_bytes(K, T);
     return b <= kata::kXqMaxBytes ? (size_t)b : 0;
 }
 
 int kata_gemv_prepare_x(const void* x, int x_dtype, int x_layout, int K, int T, void* xq, void* stream) {
     if (!x || !xq) return fail(KATA_EINVAL, "null pointer argument");
-    if (T != 1 && T != 2) return fail(KATA_EINVAL, "T=%d must be 1 or 2", T);
+    if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
     if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
     if (kata_gemv_xq_bytes(K, T) == 0) return fail(KATA_EINVAL, "K=%d unsupported for T=%d", K, T);
     if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
@@ -121,12 +124,20 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
                         "gemv ptq1 batch");
 }
 
+// activation dtype of the wide entries: fp32 / fp16 rows, or the operand form of T rows
+static int check_wide_x(int x_dtype, int K, int T) {
+    if (x_dtype != KATA_F32 && x_dtype != KATA_F16 && x_dtype != KATA_XQ) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (x_dtype == KATA_XQ && kata_gemv_xq_bytes(K, T) == 0)
+        return fail(KATA_EINVAL, "K=%d T=%d has no operand form", K, T);
+    return KATA_OK;
+}
+
 int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T, void* stream) {
     if (!W || !x || !y) return fail(KATA_EINVAL, "null pointer argument");
     if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
     if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
     if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
-    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (int rc = check_wide_x(x_dtype, K, T)) return rc;
     if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
     if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
     // one or two tokens: the decode GEMV reads the weights once for both as well, faster
@@ -142,7 +153,7 @@ int kata_gemv_ptq1_wide_batch(int count, const uint8_t* const* W, float* const* 
     if (!W || !y || !N || !x) return fail(KATA_EINVAL, "null argument");
     if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
     if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
-    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (int rc = check_wide_x(x_dtype, K, T)) return rc;
     if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
     for (int i = 0; i < count; i++) {
         if (!W[i] || !y[i]) return fail(KATA_EINVAL, "null pointer in W[] or y[]");
@@ -162,14 +173,14 @@ int kata_gemv_ptq1_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, fl
     if (K <= 0 || K % 128 != 0) return fail(KATA_EINVAL, "K=%d must be a positive multiple of 128", K);
     if (N <= 0) return fail(KATA_EINVAL, "N=%d must be positive", N);
     if (T < 1 || T > 8) return fail(KATA_EINVAL, "T=%d must be 1..8", T);
-    if (x_dtype != KATA_F32 && x_dtype != KATA_F16) return fail(KATA_EINVAL, "x_dtype=%d", x_dtype);
+    if (int rc = check_wide_x(x_dtype, K, T)) return rc;
     if (!aligned(W, 4)) return fail(KATA_EINVAL, "W must be 4-byte aligned");
     if (!aligned(x, 16)) return fail(KATA_EINVAL, "x must be 16-byte aligned");
     // T <= 2: the decode GEMV, which uses no scratch at all
     if (T <= 2 && K <= kata::gemv_max_k(T))
         return check_launch(kata::launch_gemv_ptq1(W, x, x_dtype, KATA_X_ROWS, y, K, N, T, (hipStream_t)stream),
                             "gemv ptq1 wide no-alloc (T <= 2)");
-    if (!kata::gemv_wide_noalloc_fits(K, T))
+    if (x_dtype != KATA_XQ && !kata::gemv_wide_noalloc_fits(K, T))
         return fail(KATA_EINVAL, "K=%d needs a larger activation image than the %zu-byte no-allocation scratch", K,
                     kata::gemv_wide_noalloc_scratch_bytes());
     return check_launch(kata::launch_gemv_wide_noalloc(W, x, x_dtype, y, K, N, T, (hipStream_t)stream),
@@ -281,8 +292,8 @@ static size_t fwht_out_bytes(int out_dtype, int W, int M) {
 
 static int check_fwht_out(const void* out, int out_dtype, int out_layout, int W, int M) {
     if (out_dtype != KATA_F32 && out_dtype != KATA_F16 && out_dtype != KATA_XQ) return fail(KATA_EINVAL, "out_dtype=%d", out_dtype);
-    if (out_dtype == KATA_XQ && (M < 1 || M > 2 || out_layout != KATA_X_ROWS || kata_gemv_xq_bytes(W, M) == 0))
-        return fail(KATA_EINVAL, "the operand form takes M <= 2, KATA_X_ROWS and a GEMV-supported W (M=%d W=%d)", M, W);
+    if (out_dtype == KATA_XQ && (M < 1 || M > 8 || out_layout != KATA_X_ROWS || kata_gemv_xq_bytes(W, M) == 0))
+        return fail(KATA_EINVAL, "the operand form takes M <= 8, KATA_X_ROWS and a GEMV-supported W (M=%d W=%d)", M, W);
     if (out_layout != KATA_X_ROWS && out_layout != KATA_X_HALF2) return fail(KATA_EINVAL, "out_layout=%d", out_layout);
     if (out_layout == KATA_X_HALF2 && (out_dtype != KATA_F16 || M != 2))
         return fail(KATA_EINVAL, "the half2 layout is fp16 with M == 2");
@@ -590,41 +601,43 @@ int kata_dispatch_ffn_prefill(kata_dispatch* d, uint64_t offGate, uint64_t offUp
 }
 
 // The sublayer for T <= 8 verification tokens (Engine::verifyWide's FFN, src/engine.cpp:
-// 627-629): fp16 token rows through the wide GEMV, gate and up in one batched launch.  work: fp16 h [T][H], fp32 g, u [T][F],
-// fp16 t [T][F].
+// 627-629): the transforms write the GEMV operand form of the T token rows (h, t), gate and
+// up run as one batched launch.  work: h (kata_gemv_xq_bytes(H, T), 16-byte aligned), fp32
+// g, u [T][F], t (kata_gemv_xq_bytes(F, T)).
 int kata_dispatch_ffn_verify(kata_dispatch* d, uint64_t offGate, uint64_t offUp, uint64_t offDown, const float* x,
                              const float* y, float* xnew, const float* gs_in, const float* gs_down, void* work,
                              float* out, int H, int F, int T, void* stream) {
     if (!d || !x || !gs_in || !gs_down || !work || !out) return fail(KATA_EINVAL, "null argument");
     if (H % 1024 != 0 || F % 1024 != 0 || H <= 0 || F <= 0 || T < 1 || T > 8)
         return fail(KATA_EINVAL, "H=%d F=%d must be multiples of 1024, T=%d in 1..8", H, F, T);
-    uint16_t* h = (uint16_t*)work;
-    float* g = (float*)(h + (size_t)T * H);
+    const size_t hb = align16(kata_gemv_xq_bytes(H, T));
+    if (hb == 0 || kata_gemv_xq_bytes(F, T) == 0) return fail(KATA_EINVAL, "H=%d F=%d T=%d: no operand form", H, F, T);
+    uint8_t* h = (uint8_t*)work;
+    float* g = (float*)(h + hb);
     float* u = g + (size_t)T * F;
-    uint16_t* t = (uint16_t*)(u + (size_t)T * F);
-    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_F16, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, T, stream);
+    uint8_t* t = (uint8_t*)(u + (size_t)T * F);
+    int rc = kata_add_rms_fwht(x, y, gs_in, h, KATA_XQ, KATA_X_ROWS, xnew, nullptr, nullptr, 0, H, T, stream);
     if (rc) return rc;
     const uint8_t* Wgu[2] = {d->wbase + offGate, d->wbase + offUp};
     float* ygu[2] = {g, u};
     const int Ngu[2] = {F, F};
-    if ((rc = kata_gemv_ptq1_wide_batch(2, Wgu, ygu, Ngu, h, KATA_F16, H, T, stream))) return rc;
-    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_F16, KATA_X_ROWS, F, T, 1, stream))) return rc;
-    return kata_gemv_ptq1_wide(d->wbase + offDown, t, KATA_F16, out, F, H, T, stream);
+    if ((rc = kata_gemv_ptq1_wide_batch(2, Wgu, ygu, Ngu, h, KATA_XQ, H, T, stream))) return rc;
+    if ((rc = kata_rms_fwht(g, u, gs_down, t, KATA_XQ, KATA_X_ROWS, F, T, 1, stream))) return rc;
+    return kata_gemv_ptq1_wide(d->wbase + offDown, t, KATA_XQ, out, F, H, T, stream);
 }
 
 // ------------------------------------------------------------------ sublayer halves
-// Work layout of kata_dispatch_in / _out for a transform width K and M rows: decode the
-// GEMV's operand form (kata_gemv_xq_bytes(K, 1) <= 4 K bytes, the size kept from fp32 rows);
-// verify fp16 [M][K]; prefill fp16 [M][K], then int8 [M][K] and fp32 [K/128][M] for the
+// Work layout of kata_dispatch_in / _out for a transform width K and M rows: decode and
+// verify the GEMV's operand form of the M rows (kata_gemv_xq_bytes(K, M); decode keeps the
+// 4 K bytes of fp32 rows, verify at least 2 M K); prefill fp16 [M][K], then int8 [M][K] and fp32 [K/128][M] for the
 // int8 path's quantised rows and scales (16-byte aligned parts).
-static size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
 size_t kata_dispatch_work_bytes(int form, int K, int M) {
     if (K <= 0 || M <= 0) return 0;
     const size_t k = (size_t)K, m = (size_t)M;
     switch (form) {
         case KATA_FORM_DECODE: return align16(4 * k);
-        case KATA_FORM_VERIFY: return align16(2 * m * k);
+        case KATA_FORM_VERIFY: return std::max(align16(2 * m * k), align16(kata_gemv_xq_bytes(K, M)));
         case KATA_FORM_PREFILL: return align16(2 * m * k) + align16(m * k) + align16(4 * (k / 128) * m);
         default: return 0;
     }
@@ -632,7 +645,7 @@ size_t kata_dispatch_work_bytes(int form, int K, int M) {
 
 namespace {
 struct HalfWork {
-    void* act;      // the transformed activation: the GEMV operand form (decode) or fp16 rows
+    void* act;      // the transformed activation: the GEMV operand form (decode, verify) or fp16 rows
     int8_t* A8;     // prefill: quantised rows
     float* SX;      // prefill: their group scales [K/128][M]
 };
@@ -660,7 +673,7 @@ int half_matmul(kata_dispatch* d, int form, uint64_t off, const char* name, cons
         case KATA_FORM_DECODE:
             return kata_gemv_ptq1(Wm, w.act, KATA_XQ, KATA_X_ROWS, out, K, N, 1, st);
         case KATA_FORM_VERIFY:
-            return kata_gemv_ptq1_wide(Wm, w.act, KATA_F16, out, K, N, M, st);
+            return kata_gemv_ptq1_wide(Wm, w.act, KATA_XQ, out, K, N, M, st);
         default:
             if (kata_dispatch_i8(d, name)) {
                 int rc = quantised ? KATA_OK : kata_quant_rows_i8((const uint16_t*)w.act, w.A8, w.SX, M, K, M, st);
@@ -685,14 +698,14 @@ int kata_dispatch_in(kata_dispatch* d, int form, int count, const uint64_t* offs
     }
     const hipStream_t st = (hipStream_t)stream;
     const HalfWork w = half_work(work, H, M);
-    const int act_dt = form == KATA_FORM_DECODE ? KATA_XQ : KATA_F16;
+    const int act_dt = form == KATA_FORM_PREFILL ? KATA_F16 : KATA_XQ;
     int rc = kata_add_rms_fwht(x, y, gs, w.act, act_dt, KATA_X_ROWS, xnew, gamma, hout, hout_dtype, H, M, stream);
     if (rc) return rc;
     if (form != KATA_FORM_PREFILL) {                 // one launch for all matrices that read h
         const uint8_t* Wm[4];
         for (int i = 0; i < count; i++) Wm[i] = d->wbase + offs[i];
         if (form == KATA_FORM_DECODE) return kata_gemv_ptq1_batch(count, Wm, outs, N, w.act, KATA_XQ, KATA_X_ROWS, H, 1, stream);
-        return kata_gemv_ptq1_wide_batch(count, Wm, outs, N, w.act, KATA_F16, H, M, stream);
+        return kata_gemv_ptq1_wide_batch(count, Wm, outs, N, w.act, KATA_XQ, H, M, stream);
     }
     bool quantised = false;                          // prefill: quantise h once for its int8 matrices
     for (int i = 0; i < count; i++) {
@@ -710,13 +723,15 @@ int kata_dispatch_out(kata_dispatch* d, int form, uint64_t off, const char* name
     if (int rc = check_form(form, M, W)) return rc;
     if (H <= 0) return fail(KATA_EINVAL, "H=%d must be positive", H);
     const HalfWork w = half_work(work, W, M);
-    int rc = kata_rms_fwht(src, src2, gs, w.act, form == KATA_FORM_DECODE ? KATA_XQ : KATA_F16, KATA_X_ROWS, W, M, mode,
+    int rc = kata_rms_fwht(src, src2, gs, w.act, form == KATA_FORM_PREFILL ? KATA_F16 : KATA_XQ, KATA_X_ROWS, W, M, mode,
                            stream);
     if (rc) return rc;
     return half_matmul(d, form, off, name, w, out, W, H, M, false, (hipStream_t)stream);
 }
 
-size_t kata_ffn_verify_work_bytes(int H, int F, int T) { return (size_t)T * H * 2 + (size_t)T * F * 10; }
+size_t kata_ffn_verify_work_bytes(int H, int F, int T) {
+    return align16(kata_gemv_xq_bytes(H, T)) + (size_t)T * F * 8 + kata_gemv_xq_bytes(F, T);
+}
 
 size_t kata_ffn_prefill_work_bytes(int H, int F, int M) {
     const size_t kmax = (size_t)std::max(H, F);

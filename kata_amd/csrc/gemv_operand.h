@@ -17,6 +17,11 @@
 //   scales [4 nq][T] pairs (s, 0) of fp32 bits (8 B each)
 // which is the GEMV's LDS layout less the pads between its quarters, so a workgroup copies
 // it with 16-byte loads and stores.
+//
+// For T = 3..8 rows (the wide verification GEMV) the operand form is that kernel's image:
+//   image  [block nb][m 2][g 4][row 16][16 B]   (rows of tokens >= T zero)
+//   scales [block nb][token pair 4] (s of token 2p, s of token 2p + 1) fp32
+// 2080 bytes per block, read by every workgroup of the wide GEMV from L2.
 #pragma once
 #include "common.h"
 
@@ -63,8 +68,13 @@ __host__ __device__ constexpr int gemv_nq(int K) { return ((K / kGroup + 3) / 4 
 // image bytes of one block and of one quarter
 __host__ __device__ constexpr int gemv_xq_blk_bytes(int T) { return kAImageBytes * 2 * T; }
 __host__ __device__ constexpr int gemv_xq_qbytes(int K, int T) { return gemv_nq(K) * gemv_xq_blk_bytes(T); }
-// the whole operand form: image + scale pairs
-__host__ __device__ constexpr int gemv_xq_bytes(int K, int T) { return 4 * gemv_xq_qbytes(K, T) + 8 * 4 * gemv_nq(K) * T; }
+// the whole operand form: image + scale pairs (T <= 2), the wide image + scales (T = 3..8)
+constexpr int kWideImgBlk = kDenseMfma * 4 * 16 * 16;   // wide image bytes per block (2048)
+constexpr int kWideSclBlk = 4 * 8;                       // wide scale bytes per block
+__host__ __device__ constexpr long long gemv_xq_bytes(int K, int T) {
+    return T <= 2 ? 4LL * gemv_xq_qbytes(K, T) + 8LL * 4 * gemv_nq(K) * T
+                  : (long long)(K / kGroup) * (kWideImgBlk + kWideSclBlk);
+}
 
 // Block scale from the block's amax (inf for a block holding a non-finite value):
 // inv = 32639 / amax (0 for amax = 0 or a non-finite block), s = amax / 32639 (NaN for a

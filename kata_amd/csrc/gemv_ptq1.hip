@@ -427,7 +427,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     }
     // XQ: the operand form, 16 bytes per thread and piece, loaded before the weight ring so
     // that it lands first; pieces past its end read zero (whole absent pieces are skipped)
-    const int xqb = 4 * qbytes + 8 * nbv * T;
+    const int xqb = 4 * qbytes + 8 * nbv * T;     // gemv_xq_bytes(K, T)
     uint4 xr[XQ ? kXqChunks : 1];
     if constexpr (XQ) {
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, xqb, 0x00020000);
@@ -700,7 +700,7 @@ constexpr int kVwCBMax = 40;                     // blocks per K chunk (the wave
 constexpr int kVwWaves = 8;
 constexpr int kVwBB = kVwCBMax / kVwWaves;       // blocks of a wave per chunk
 constexpr int kVwLR = 6;                         // 64 trit-table replicas (conflict-free lookups)
-constexpr int kVwImgBlk = kDenseMfma * 4 * 16 * 16;   // image bytes per block (2048)
+constexpr int kVwImgBlk = kWideImgBlk;           // image bytes per block (2048)
 constexpr int kVwPrepBlocks = 1;                 // blocks per prep workgroup (one: the shortest chain)
 constexpr int kVwPrepThreads = kVwPrepBlocks >= 2 ? 256 : 128;   // 8 tokens x 16 chunks per block
 static_assert(8 * kVwPrepBlocks * 16 % kVwPrepThreads == 0, "whole quantisation tasks per prep thread");
@@ -1157,7 +1157,10 @@ __global__ __launch_bounds__(256) void k_gemv_prepare(const void* __restrict__ x
     }
 }
 
+static hipError_t launch_gemv_vw_prep(const void* x, int x_dtype, int K, int T, uint8_t* ximg, hipStream_t s);
+
 hipError_t launch_gemv_prepare(const void* x, int x_dtype, int x_layout, int K, int T, void* xq, hipStream_t s) {
+    if (T > 2) return launch_gemv_vw_prep(x, x_dtype, K, T, (uint8_t*)xq, s);
     const dim3 grid((unsigned)((gemv_nq(K) + 3) / 4));
     if (T == 1)
         hipLaunchKernelGGL(k_gemv_prepare<1>, grid, dim3(256), 0, s, x, x_dtype, x_layout, K, (uint8_t*)xq);
@@ -1196,7 +1199,20 @@ hipError_t launch_gemv_ptq1(const uint8_t* W, const void* x, int x_dtype, int x_
 // the 1..4 matrices sharing them: about one workgroup per CU (more when a CU would get more
 // than kVwTMax tiles).
 constexpr size_t kVwImgBytesPerBlock = kVwImgBlk + 4 * sizeof(float2);
+static_assert(kVwImgBytesPerBlock == kWideImgBlk + kWideSclBlk, "the wide operand form is the prep kernel's image");
 size_t gemv_wide_image_bytes(int K) { return (size_t)(K / kGroup) * kVwImgBytesPerBlock; }
+
+// the image and scales of T (1..8) fp16 / fp32 token rows [T][K] into ximg
+static hipError_t launch_gemv_vw_prep(const void* x, int x_dtype, int K, int T, uint8_t* ximg, hipStream_t s) {
+    const int nb = K / kGroup;
+    float2* xscl = (float2*)(ximg + (size_t)nb * kVwImgBlk);
+    const dim3 pgrid((nb + kVwPrepBlocks - 1) / kVwPrepBlocks);
+    if (x_dtype == 1)
+        hipLaunchKernelGGL(k_gemv_vw_prep<true>, pgrid, dim3(kVwPrepThreads), 0, s, x, K, T, ximg, xscl);
+    else
+        hipLaunchKernelGGL(k_gemv_vw_prep<false>, pgrid, dim3(kVwPrepThreads), 0, s, x, K, T, ximg, xscl);
+    return hipGetLastError();
+}
 
 static hipError_t launch_gemv_vw(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
                                  int x_dtype, int K, int T, uint8_t* ximg, hipStream_t s) {
@@ -1217,14 +1233,13 @@ static hipError_t launch_gemv_vw(int count, const uint8_t* const* W, float* cons
     }
     for (int i = count; i <= kMaxMats; i++) P.t0[i] = (int)total;
     if (total > 0x3fffffffLL) return hipErrorInvalidValue;
+    // the operand form (x_dtype kXDtypeOperand) is the image itself: no prep launch
+    if (x_dtype == kXDtypeOperand) ximg = (uint8_t*)x;
     float2* xscl = (float2*)(ximg + (size_t)nb * kVwImgBlk);
-    const dim3 pgrid((nb + kVwPrepBlocks - 1) / kVwPrepBlocks);
-    if (x_dtype == 1)
-        hipLaunchKernelGGL(k_gemv_vw_prep<true>, pgrid, dim3(kVwPrepThreads), 0, s, x, K, T, ximg, xscl);
-    else
-        hipLaunchKernelGGL(k_gemv_vw_prep<false>, pgrid, dim3(kVwPrepThreads), 0, s, x, K, T, ximg, xscl);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (x_dtype != kXDtypeOperand) {
+        hipError_t e = launch_gemv_vw_prep(x, x_dtype, K, T, ximg, s);
+        if (e != hipSuccess) return e;
+    }
     const int n_cu = device_cus();
     const long long grid = std::min<long long>(total, std::max<long long>(n_cu, (total + kVwTMax - 1) / kVwTMax));
     hipLaunchKernelGGL(k_gemv_vw, dim3((unsigned)grid), dim3(512), 0, s, P, ximg, xscl, K, T, (int)total);
@@ -1234,6 +1249,7 @@ static hipError_t launch_gemv_vw(int count, const uint8_t* const* W, float* cons
 // the image in the calling stream's buffer (allocated on the stream's first wide call)
 hipError_t launch_gemv_wide_batch(int count, const uint8_t* const* W, float* const* y, const int* N, const void* x,
                                   int x_dtype, int K, int T, hipStream_t s) {
+    if (x_dtype == kXDtypeOperand) return launch_gemv_vw(count, W, y, N, x, x_dtype, K, T, nullptr, s);
     void* img = nullptr;
     hipError_t e = stream_buffer(kBufWideImage, gemv_wide_image_bytes(K), s, &img);
     if (e != hipSuccess) return e;
@@ -1279,6 +1295,7 @@ bool gemv_wide_noalloc_fits(int K, int T) {
 
 hipError_t launch_gemv_wide_noalloc(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
                                     hipStream_t s) {
+    if (x_dtype == kXDtypeOperand) return launch_gemv_vw(1, &W, &y, &N, x, x_dtype, K, T, nullptr, s);
     uint8_t* img = nullptr;
     hipError_t e = noalloc_scratch(&img);
     if (e != hipSuccess) return e;

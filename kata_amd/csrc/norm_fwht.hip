@@ -143,6 +143,52 @@ __device__ inline void store_operand(const float (&v)[4], int tid, int blk, int 
     }
 }
 
+// The same for M = 3..8 tokens in the wide GEMV's operand form: block b's image at 2048 b,
+// A row 2 m + limb of lane group g of MFMA mm at 1024 mm + 256 g + 16 (2 m + limb), the
+// scales of token pair p at 2048 nb + 32 b + 8 p.  The workgroups of token 0 also clear
+// the rows and scales of tokens M..7 of their blocks.
+__device__ inline void store_operand_wide(const float (&v)[4], int tid, int blk, int m, int M, int W, uint8_t* xs,
+                                          uint8_t* __restrict__ xq) {
+#pragma clang fp contract(off)
+    constexpr int BLK = kWideImgBlk;
+    const int nb = W >> 7;
+    float a = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) a = fmaxf(a, gemv_amax_term(v[r]));
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+    float inv, sc;
+    gemv_block_scale(a, inv, sc);
+    const int bl = tid >> 5, b = 8 * blk + bl;
+    __syncthreads();                              // the transform's last reads of xs
+    // staging: per block the token's 16 A rows [mm 2][g 4][limb 2][16 B] (256 B)
+    uint8_t* img = xs + bl * 256;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int o = gemv_dense_img_off((4 * tid + r) & 127, 8);   // [mm][g][row 16][16 B]
+        const int so = (o >> 10) * 128 + ((o >> 8) & 3) * 32 + (o & 15);
+        gemv_limbs(v[r], inv, img[so], img[so + 16]);
+    }
+    float* scl = (float*)(xq + (size_t)nb * BLK);
+    if ((tid & 31) == 0) scl[b * 8 + m] = sc;
+    __syncthreads();
+    if (tid < 128) {
+        const int pb = tid >> 4, mm = (tid >> 3) & 1, g = (tid >> 1) & 3, limb = tid & 1;
+        const int bb = 8 * blk + pb;
+        *(uint4*)(xq + (size_t)bb * BLK + mm * 1024 + g * 256 + (2 * m + limb) * 16) =
+            *(const uint4*)(xs + pb * 256 + mm * 128 + g * 32 + limb * 16);
+    }
+    if (m == 0) {
+        // rows 2 M .. 15 of the 8 blocks' 8 (mm, g) groups, and the scales of tokens M..7
+        const int nr = 16 - 2 * M;
+        for (int i = tid; i < 8 * 8 * nr; i += 256) {
+            const int pb = i / (8 * nr), rem = i % (8 * nr), grp = rem / nr, row = 2 * M + rem % nr;
+            *(uint4*)(xq + (size_t)(8 * blk + pb) * BLK + grp * 256 + row * 16) = make_uint4(0, 0, 0, 0);
+        }
+        if (tid < 8 * (8 - M)) scl[(8 * blk + tid / (8 - M)) * 8 + M + tid % (8 - M)] = 0.0f;
+    }
+}
+
 template <int NB>
 __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src, const float* __restrict__ src2,
                                                    const float* __restrict__ gs, void* __restrict__ out, int out_dtype,
@@ -226,7 +272,11 @@ __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src
         }
         fwht1024(v, tid, xs);
         if (out_dtype == 2) {
-            store_operand(v, tid, blk0 + b, m, NB == 1 ? gridDim.y : gridDim.x, W, (uint8_t*)xs, (uint8_t*)out);
+            const int M = NB == 1 ? gridDim.y : gridDim.x;
+            if (M <= 2)
+                store_operand(v, tid, blk0 + b, m, M, W, (uint8_t*)xs, (uint8_t*)out);
+            else
+                store_operand_wide(v, tid, blk0 + b, m, M, W, (uint8_t*)xs, (uint8_t*)out);
         } else if (out_dtype == 0) {
             *(float4*)((float*)out + ro + base) = make_float4(v[0], v[1], v[2], v[3]);
         } else if (out_layout == 0) {
@@ -247,7 +297,7 @@ hipError_t launch_norm_fwht(const float* src, const float* src2, const float* gs
                             int out_layout, float* xnew, const float* gamma, void* hout, int flags, int W, int M,
                             int mode, hipStream_t s) {
     // whole rows per workgroup once there are enough rows to fill the CUs (hidden width 5120);
-    // the operand form (out_dtype 2) takes M <= 2
+    // the operand form (out_dtype 2) takes M <= 8
     if (W == 5120 && M >= 64 && out_dtype != 2)
         hipLaunchKernelGGL(k_norm_fwht<5>, dim3(M), dim3(256), 0, s, src, src2, gs, out, out_dtype, out_layout, xnew,
                            gamma, hout, flags, W, mode);

@@ -117,11 +117,22 @@ def gemv_ptq1_batch(Ws, x: torch.Tensor, K: int, Ns, T: int = 1, half2: bool = F
     return ys
 
 
-def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Wide verification GEMV: y[T][N] fp32 for x [T][K] (fp16 or fp32), T = x.shape[0] in 1..8."""
-    T = x.shape[0]
+def _rows(x: torch.Tensor, T: int | None) -> int:
+    """Token rows of an activation: x.shape[0] for rows, the given T for the operand form."""
+    if x.dtype == torch.uint8:
+        if T is None:
+            raise ValueError("the operand form needs T")
+        return T
+    return x.shape[0]
+
+
+def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.Tensor | None = None,
+                   T: int | None = None) -> torch.Tensor:
+    """Wide verification GEMV: y[T][N] fp32 for x [T][K] (fp16 or fp32, T = x.shape[0] in 1..8)
+    or the operand form of T rows (uint8, from gemv_prepare_x or a transform)."""
+    T = _rows(x, T)
     _need_bytes("W", W, _ptq1_bytes(K, N))
-    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("x", x, _x_bytes(x, K, T))
     _need_bytes("out", out, T * N * 4)
     _need_gpu(W, x)
     y = out if out is not None else torch.empty((T, N), dtype=torch.float32, device=W.device)
@@ -129,16 +140,17 @@ def gemv_ptq1_wide(W: torch.Tensor, x: torch.Tensor, K: int, N: int, out: torch.
     return y
 
 
-def gemv_ptq1_wide_batch(Ws, x: torch.Tensor, K: int, Ns, outs=None):
+def gemv_ptq1_wide_batch(Ws, x: torch.Tensor, K: int, Ns, outs=None, T: int | None = None):
     """Wide verification GEMVs of up to 4 matrices sharing the token rows x [T][K] (fp16 or
-    fp32, T = x.shape[0] in 1..8), one launch: returns [y_i], y_i [T][N_i] fp32."""
-    T = x.shape[0]
+    fp32, T = x.shape[0] in 1..8, or their operand form with T given), one launch: returns
+    [y_i], y_i [T][N_i] fp32."""
+    T = _rows(x, T)
     if len(Ws) != len(Ns) or (outs is not None and len(outs) != len(Ns)):
         raise ValueError("Ws, Ns (and outs) must have the same length")
     for i, (W, N) in enumerate(zip(Ws, Ns)):
         _need_bytes(f"Ws[{i}]", W, _ptq1_bytes(K, N))
         _need_bytes(f"outs[{i}]", outs[i] if outs is not None else None, T * N * 4)
-    _need_bytes("x", x, T * K * x.element_size())
+    _need_bytes("x", x, _x_bytes(x, K, T))
     _need_gpu(x, *Ws)
     n = len(Ws)
     ys = outs if outs is not None else [torch.empty((T, N), dtype=torch.float32, device=x.device) for N in Ns]

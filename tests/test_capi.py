@@ -157,7 +157,8 @@ def test_dispatch_ffn_rejects():
         assert lib.kata_dispatch_ffn_verify(h, 0, 0, 0, p, None, None, p, p, p, p, 2000, 3072, 2, None) == KATA_EINVAL
     finally:
         lib.kata_dispatch_destroy(h)
-    assert lib.kata_ffn_verify_work_bytes(1024, 2048, 3) == 3 * 1024 * 2 + 3 * 2048 * 10
+    # h and t in the wide GEMV's operand form (2080 B per 128-block), g and u fp32
+    assert lib.kata_ffn_verify_work_bytes(1024, 2048, 3) == 8 * 2080 + 3 * 2048 * 8 + 16 * 2080
     # g, u fp32 + h, t fp16 + int8 rows + 16 alignment + scales
     assert lib.kata_ffn_prefill_work_bytes(1024, 2048, 8) == 8 * 2048 * 8 + 8 * 1024 * 2 + 8 * 2048 * 2 + 8 * 2048 + 16 + 16 * 8 * 4
 
@@ -192,7 +193,8 @@ def test_dispatch_sub_rejects():
     finally:
         lib.kata_dispatch_destroy(h)
     assert lib.kata_dispatch_work_bytes(0, 5120, 1) == 4 * 5120
-    assert lib.kata_dispatch_work_bytes(2, 5120, 3) == 2 * 3 * 5120
+    assert lib.kata_dispatch_work_bytes(2, 5120, 3) == 40 * 2080          # the wide operand form
+    assert lib.kata_dispatch_work_bytes(2, 5120, 1) == 10560               # the decode operand form (T = 1)
     assert lib.kata_dispatch_work_bytes(1, 5120, 5) == 2 * 5 * 5120 + 5 * 5120 + 4 * 40 * 5
     assert lib.kata_dispatch_work_bytes(3, 5120, 5) == 0
 
@@ -310,13 +312,16 @@ def test_gemv_operand_form_sizes_and_rejects():
     nq = lambda K: ((K // 128 + 3) // 4 + 1) & ~1
     for K, T in ((128, 1), (1152, 2), (5120, 1), (5120, 2), (17408, 1), (17408, 2)):
         assert lib.kata_gemv_xq_bytes(K, T) == nq(K) * T * (1024 + 32)
-    assert lib.kata_gemv_xq_bytes(5120, 3) == 0 and lib.kata_gemv_xq_bytes(100, 1) == 0
+    for K, T in ((5120, 3), (17408, 8), (128, 5)):                       # the wide GEMV's image
+        assert lib.kata_gemv_xq_bytes(K, T) == K // 128 * (2048 + 32)
+    assert lib.kata_gemv_xq_bytes(5120, 9) == 0 and lib.kata_gemv_xq_bytes(100, 1) == 0
     assert lib.kata_gemv_xq_bytes(0, 1) == 0
     big = lib.kata_gemv_ptq1_max_k(1) + 128
     assert lib.kata_gemv_xq_bytes(big, 1) == 0
     prep = lib.kata_gemv_prepare_x
     out = ctypes.c_void_p(0x20000)
-    assert prep(FAKE, 1, 0, 5120, 3, out, None) == KATA_EINVAL          # T
+    assert prep(FAKE, 1, 0, 5120, 9, out, None) == KATA_EINVAL          # T
+    assert prep(FAKE, 1, 1, 5120, 3, out, None) == KATA_EINVAL          # half2 only for T = 2
     assert prep(FAKE, 1, 0, 5000, 1, out, None) == KATA_EINVAL          # K % 128
     assert prep(FAKE, 2, 0, 5120, 1, out, None) == KATA_EINVAL          # x dtype (not itself)
     assert prep(FAKE, 0, 1, 5120, 2, out, None) == KATA_EINVAL          # half2 needs fp16
@@ -328,5 +333,5 @@ def test_gemv_operand_form_sizes_and_rejects():
     # transforms: the operand form takes M <= 2 and the rows layout
     fwht = lib.kata_rms_fwht
     g = ctypes.c_void_p(0x40000)
-    assert fwht(FAKE, None, g, out, 2, 0, 5120, 3, 3, None) == KATA_EINVAL
+    assert fwht(FAKE, None, g, out, 2, 0, 5120, 9, 3, None) == KATA_EINVAL
     assert fwht(FAKE, None, g, out, 2, 1, 5120, 2, 3, None) == KATA_EINVAL

@@ -73,21 +73,20 @@ def _mm_ref(form, W, A, K, i8):
 
 
 def _act(work, form, K, M):
-    """The transformed activation in the work buffer: the decode form holds the GEMV's
-    operand form (decoded here), the others fp16 rows."""
+    """The transformed activation in the work buffer: the decode and verify forms hold the
+    GEMVs' operand form (decoded here), the prefill form fp16 rows."""
     wk = work.cpu().numpy()
-    if form == "decode":
-        return operand_form.decode(wk[:operand_form.nbytes(K, 1)], K, 1)
+    if form != "prefill":
+        return operand_form.decode(wk[:operand_form.nbytes(K, M)], K, M)
     return wk[:2 * M * K].view(np.float16).reshape(M, K)
 
 
-def _act_ok(a, ref, form, rel):
-    """Transform output within rel of the reference's max; the operand form also within its
-    block quantiser's bound (amax / 65278 per 128-block)."""
-    q = 0.0
-    if form == "decode":
-        q = (np.abs(ref).reshape(ref.shape[0], -1, 128).max(axis=2) / 65278 * 1.01).repeat(128, axis=1)
-    return np.all(np.abs(a.astype(np.float64) - ref) <= np.abs(ref).max() * rel + q)
+def _act_ok(a, ref, form):
+    """Transform output: fp16 rows within 2^-11 of the reference's max; the operand form
+    within its block quantiser's bound plus 1e-5 of the max (the fp32 transform)."""
+    if form == "prefill":
+        return np.abs(a.astype(np.float64) - ref).max() <= np.abs(ref).max() * 2.0 ** -11
+    return operand_form.bound_ok(a, ref, np.abs(ref).max() * 1e-5)
 
 
 @pytest.mark.parametrize("form,M,i8", [("decode", 1, "none"), ("prefill", 24, "none"), ("prefill", 24, "all"),
@@ -113,7 +112,7 @@ def test_sub_in_out(mixer, form, M, i8):
     assert np.array_equal(xnew.cpu().numpy(), x + y)
     h = _act(work, form, H, M)
     h_ref, _ = orc.norm_fwht(x, gs, 0, src2=y, add=True)
-    assert _act_ok(h, h_ref, form, 1e-5 if form == "decode" else 2.0 ** -11)
+    assert _act_ok(h, h_ref, form)
     for (nm, N), o in zip(spec["ins"], outs):
         ref, rows = _mm_ref(form, mats[nm], h, H, i8 == "all")
         e = rel_l2(o.cpu().numpy()[:, rows], ref)
@@ -128,7 +127,7 @@ def test_sub_in_out(mixer, form, M, i8):
     torch.cuda.synchronize()
     t = _act(work, form, W, M)
     t_ref, _ = orc.norm_fwht(o, gso, mode)
-    assert _act_ok(t, t_ref, form, 1e-5 if form == "decode" else 2.0 ** -11)
+    assert _act_ok(t, t_ref, form)
     ref, rows = _mm_ref(form, mats[nm], t, W, i8 == "all")
     e = rel_l2(out.cpu().numpy()[:, rows], ref)
     assert e.max() < tol, (mix, form, nm, e.max())

@@ -12,6 +12,7 @@ import torch
 
 from kata_amd.engine import Dispatch, ffn_prefill_work_bytes
 from oracle import oracle as orc
+from tests import operand_form
 from tests.conftest import rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -147,9 +148,8 @@ def test_ffn_prefill_decode_agree(dev):
 @pytest.mark.parametrize("T", [1, 3, 8])
 def test_ffn_verify(dev, T):
     """T verification tokens through the wide GEMV: each step against the oracle fed with
-    the GPU's previous step (work buffer: h fp16 [T][H], g, u fp32 [T][F], t fp16 [T][F]),
-    then end to end against the composition from x (fp16 rounding of h and t may differ by
-    one ulp from the double-precision composition)."""
+    the GPU's previous step (work buffer: h and t in the GEMV operand form, decoded here;
+    g, u fp32 [T][F]), then end to end against the composition from x."""
     from kata_amd.capi import lib
     H, F = 2048, 3072
     buf, (og, ou, od), W = _weights(H, F, 42 + T)
@@ -163,16 +163,17 @@ def test_ffn_verify(dev, T):
     assert np.array_equal(xnew.cpu().numpy(), x + y)
     wk = work.cpu().numpy()
     o = 0
-    h = wk[o:o + 2 * T * H].view(np.float16).reshape(T, H); o += 2 * T * H
+    hb = operand_form.nbytes(H, T)
+    h = operand_form.decode(wk[o:o + hb], H, T); o += (hb + 15) // 16 * 16
     g = wk[o:o + 4 * T * F].view(np.float32).reshape(T, F); o += 4 * T * F
     u = wk[o:o + 4 * T * F].view(np.float32).reshape(T, F); o += 4 * T * F
-    t = wk[o:o + 2 * T * F].view(np.float16).reshape(T, F)
+    t = operand_form.decode(wk[o:o + operand_form.nbytes(F, T)], F, T)
     h_ref, _ = orc.norm_fwht(x, gs_in, 0, src2=y, add=True)
-    assert np.abs(h.astype(np.float64) - h_ref).max() <= np.abs(h_ref).max() * 2.0 ** -11
+    assert operand_form.bound_ok(h, h_ref, np.abs(h_ref).max() * 1e-5)
     assert rel_l2(g, orc.gemv_ptq1(Wg, h.astype(np.float32), H, F, T)).max() < 2e-4
     assert rel_l2(u, orc.gemv_ptq1(Wu, h.astype(np.float32), H, F, T)).max() < 2e-4
     t_ref, _ = orc.norm_fwht(g, gs_down, 1, src2=u)
-    assert np.abs(t.astype(np.float64) - t_ref).max() <= np.abs(t_ref).max() * 2.0 ** -11
+    assert operand_form.bound_ok(t, t_ref, np.abs(t_ref).max() * 1e-5)
     assert rel_l2(out, orc.gemv_ptq1(Wd, t.astype(np.float32), F, H, T)).max() < 2e-4
     ref = _ref_decode(W, x[:1], y[:1], gs_in, gs_down, H, F)
     assert rel_l2(out[:1], ref).max() < 2e-3

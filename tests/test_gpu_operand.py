@@ -15,6 +15,7 @@ import torch
 from kata_amd import ops
 from oracle import oracle as orc
 from tests.conftest import rel_l2
+from tests import operand_form
 from tests.operand_form import decode as _decode
 
 pytestmark = pytest.mark.gpu
@@ -70,7 +71,7 @@ def _signs(W, seed):
     return np.random.default_rng(seed).choice([-1.0, 1.0], size=W).astype(np.float32)
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 8])
 @pytest.mark.parametrize("mode,W", [(0, 5120), (1, 17408), (2, 6144), (3, 6144)])
 def test_transform_writes_operand(dev, M, mode, W):
     """The transforms' operand form equals kata_gemv_prepare_x of their fp32 rows byte for
@@ -87,3 +88,27 @@ def test_transform_writes_operand(dev, M, mode, W):
         f32 = ops.rms_fwht(src, gs, mode, src2=src2 if mode == 1 else None)
         xq = ops.rms_fwht(src, gs, mode, src2=src2 if mode == 1 else None, out_dtype=torch.uint8)
     assert torch.equal(xq, ops.gemv_prepare_x(f32, W, M))
+
+
+@pytest.mark.parametrize("K,Ns,T,dtype", [
+    (384, (33,), 3, np.float32), (5120, (1000, 64), 4, np.float16), (5120, (300,), 8, np.float32),
+    (17408, (40, 17), 5, np.float16), (6144, (129,), 7, np.float16),
+])
+def test_wide_operand_bit_exact(dev, K, Ns, T, dtype):
+    """T = 3..8: the wide GEMV on the operand form (its prep kernel's image, written once)
+    equals its launch on the raw rows bit for bit, single and batched; the bytes decode to x
+    within the quantiser's bound, rows of tokens >= T zero."""
+    seed = K + T
+    mats = [orc.synth_ptq1(N, K, seed + i)[0] for i, N in enumerate(Ns)]
+    Ws = [torch.from_numpy(m).to(dev) for m in mats]
+    x_np = orc.synth_x(T, K, seed + 9, dtype)
+    x = torch.from_numpy(x_np).to(dev)
+    xq = ops.gemv_prepare_x(x, K, T)
+    assert xq.numel() == K // 128 * 2080
+    for W, N in zip(Ws, Ns):
+        assert torch.equal(ops.gemv_ptq1_wide(W, x, K, N), ops.gemv_ptq1_wide(W, xq, K, N, T=T))
+    for a, b in zip(ops.gemv_ptq1_wide_batch(Ws, x, K, list(Ns)), ops.gemv_ptq1_wide_batch(Ws, xq, K, list(Ns), T=T)):
+        assert torch.equal(a, b)
+    ref = orc.gemv_ptq1(mats[0], x_np.astype(np.float32), K, Ns[0], T)
+    assert rel_l2(ops.gemv_ptq1_wide(Ws[0], xq, K, Ns[0], T=T).cpu().numpy(), ref).max() < 2e-4
+    assert operand_form.bound_ok(operand_form.decode(xq.cpu().numpy(), K, T), x_np.astype(np.float64))
