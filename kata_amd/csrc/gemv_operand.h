@@ -85,6 +85,32 @@ __device__ inline void gemv_block_scale(float amax, float& inv, float& sc) {
     inv = (amax > 0.0f && !bad) ? kQMax / amax : 0.0f;
     sc = bad ? __builtin_nanf("") : amax * (1.0f / kQMax);
 }
+// max over the 32 lanes of a half wave: the 16 lanes of a DPP row (xor 1, xor 2, the
+// half-row and row mirrors), then the other row of the half (a swizzle, xor 16)
+__device__ inline float half32_max(float a) {
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0xb1, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4e, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x141, 0xf, 0xf, false)));
+    a = fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x140, 0xf, 0xf, false)));
+    // ds_swizzle bit mode: and 0x1f, or 0, xor 0x10
+    return fmaxf(a, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a), 0x401f)));
+}
+
+// Element e's byte in a block's A image for T = 1, 2 and 8 rows (gemv_dense_img_off), as
+// a table for the producers that place elements by a run-time index.
+struct alignas(16) DenseImgOff {
+    uint16_t v[3][128];
+};
+constexpr DenseImgOff make_dense_img_off() {
+    DenseImgOff t{};
+    for (int e = 0; e < 128; e++) {
+        t.v[0][e] = (uint16_t)gemv_dense_img_off(e, 1);
+        t.v[1][e] = (uint16_t)gemv_dense_img_off(e, 2);
+        t.v[2][e] = (uint16_t)gemv_dense_img_off(e, 8);
+    }
+    return t;
+}
+
 // |x| for the amax, infinity for NaN / infinity
 __device__ inline float gemv_amax_term(float v) {
     const float a = fabsf(v);

@@ -564,8 +564,8 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // pcur + 64 T (u/2) (an immediate offset); after a pass pcur advances by 64 T D/2 on the
     // diagonal lanes and stays on the others, whose scratch words stay inside the 1 KB area.
     const uint32_t diag = g == kq ? 1u : 0u;
-    // (strided: the pair slots of a wave are G tiles apart, at most 5 x 128 B: the scratch
-    // words of the other lanes still stay inside the 1 KB area)
+    // (strided: the pair slots of a wave are G tiles apart; the launch takes the strided
+    // order only where the other lanes' scratch words still stay inside the 1 KB area)
     const uint32_t pstep = (uint32_t)(strided ? G : 1) * T * 64;
     uint8_t* pcur = diag ? (uint8_t*)part + (g * 4 + r) * 4 + (uint32_t)(strided ? sp * Tt + sh : s0 >> 1) * T * 64
                          : Js + lane * 4;
@@ -1025,9 +1025,13 @@ static hipError_t launch_gemv_cfg(const GemvMats& P, const void* x, int x_dtype,
 // The tile-strided order pays off for one matrix with long tile ranges (the 248320-row
 // lm_head: 88 -> 78 us) and rows of few step pairs that fill the 16 waves (5 pairs: 15
 // waves busy); for the sweep's 6-34 tiles per workgroup it was slower.
-static bool gemv_strided(const GemvMats& P, int K) {
-    const int np = gemv_nq(K) / 2, G = 16 / np;
-    return P.count == 1 && np > 0 && G >= 2 && G * np >= 15 && P.tpw[0] >= 64;
+// The off-diagonal lanes' scratch stores of a ring pass reach (kRing / 2 - 1) pair slots,
+// G T 64 bytes apart, past their word (lane 4 + token 64) in the 1 KB scratch area: the
+// strided order is taken only where they stay inside it (G <= 12 for T = 1, <= 5 for T = 2).
+static bool gemv_strided(const GemvMats& P, int K, int T) {
+    const int np = gemv_nq(K) / 2, G = np > 0 ? 16 / np : 0;
+    return P.count == 1 && np > 0 && G >= 2 && G * np >= 15 && P.tpw[0] >= 64 &&
+           (kRing / 2 - 1) * G * T * 64 + 64 * (T - 1) + 64 * 4 <= 1024;
 }
 
 template <int T, int LR, int XM>
@@ -1036,7 +1040,7 @@ static hipError_t launch_gemv_pad(const GemvMats& P, const void* x, int x_dtype,
     if (P.count > 1)
         return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XM, true>(P, x, x_dtype, x_layout, K, lds, s)
                                 : launch_gemv_cfg<T, LR, false, XM, true>(P, x, x_dtype, x_layout, K, lds, s);
-    if ((K / kGroup) % 8 == 0 && gemv_strided(P, K))
+    if ((K / kGroup) % 8 == 0 && gemv_strided(P, K, T))
         return launch_gemv_cfg<T, LR, false, XM, false, true>(P, x, x_dtype, x_layout, K, lds, s);
     return (K / kGroup) % 8 ? launch_gemv_cfg<T, LR, true, XM, false>(P, x, x_dtype, x_layout, K, lds, s)
                             : launch_gemv_cfg<T, LR, false, XM, false>(P, x, x_dtype, x_layout, K, lds, s);

@@ -29,6 +29,7 @@ namespace kata {
 namespace {
 
 constexpr float kRmsEps = 1e-6f;   // config/kata_m6.h:21
+__constant__ DenseImgOff kOperandOff = make_dense_img_off();
 
 __device__ inline float wave_sum(float a) {
     // fixed-order butterfly over the 64 lanes
@@ -113,15 +114,14 @@ __device__ inline int gdn_perm(int i) {
 // This workgroup's 8 blocks of token m (elements 4 tid + r of the 1024-block blk) in the
 // decode GEMV's operand form: the 32 lanes of a block reduce its amax, the limbs go to an
 // LDS copy of the 8 block images, then 128 threads store the token's 16-byte A rows.
-__device__ inline void store_operand(const float (&v)[4], int tid, int blk, int m, int M, int W, uint8_t* xs,
-                                     uint8_t* __restrict__ xq) {
+__device__ inline void store_operand(const float (&v)[4], uint2 offw, int tid, int blk, int m, int M, int W,
+                                     uint8_t* xs, uint8_t* __restrict__ xq) {
 #pragma clang fp contract(off)
     const int BLK = gemv_xq_blk_bytes(M), qbytes = gemv_xq_qbytes(W, M);
     float a = 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; r++) a = fmaxf(a, gemv_amax_term(v[r]));
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+    a = half32_max(a);
     float inv, sc;
     gemv_block_scale(a, inv, sc);
     const int bl = tid >> 5, b = 8 * blk + bl;
@@ -129,7 +129,7 @@ __device__ inline void store_operand(const float (&v)[4], int tid, int blk, int 
     uint8_t* img = xs + bl * BLK + 32 * m;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int off = gemv_dense_img_off((4 * tid + r) & 127, M);
+        const int off = (int)(((r < 2 ? offw.x : offw.y) >> (16 * (r & 1))) & 0xffffu);
         gemv_limbs(v[r], inv, img[off], img[off + 16]);
     }
     if ((tid & 31) == 0) ((int2*)(xq + 4 * qbytes))[b * M + m] = make_int2(__builtin_bit_cast(int, sc), 0);
@@ -147,16 +147,15 @@ __device__ inline void store_operand(const float (&v)[4], int tid, int blk, int 
 // A row 2 m + limb of lane group g of MFMA mm at 1024 mm + 256 g + 16 (2 m + limb), the
 // scales of token pair p at 2048 nb + 32 b + 8 p.  The workgroups of token 0 also clear
 // the rows and scales of tokens M..7 of their blocks.
-__device__ inline void store_operand_wide(const float (&v)[4], int tid, int blk, int m, int M, int W, uint8_t* xs,
-                                          uint8_t* __restrict__ xq) {
+__device__ inline void store_operand_wide(const float (&v)[4], uint2 offw, int tid, int blk, int m, int M, int W,
+                                          uint8_t* xs, uint8_t* __restrict__ xq) {
 #pragma clang fp contract(off)
     constexpr int BLK = kWideImgBlk;
     const int nb = W >> 7;
     float a = 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; r++) a = fmaxf(a, gemv_amax_term(v[r]));
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+    a = half32_max(a);
     float inv, sc;
     gemv_block_scale(a, inv, sc);
     const int bl = tid >> 5, b = 8 * blk + bl;
@@ -165,7 +164,7 @@ __device__ inline void store_operand_wide(const float (&v)[4], int tid, int blk,
     uint8_t* img = xs + bl * 256;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int o = gemv_dense_img_off((4 * tid + r) & 127, 8);   // [mm][g][row 16][16 B]
+        const int o = (int)(((r < 2 ? offw.x : offw.y) >> (16 * (r & 1))) & 0xffffu);   // [mm][g][row 16][16 B]
         const int so = (o >> 10) * 128 + ((o >> 8) & 3) * 32 + (o & 15);
         gemv_limbs(v[r], inv, img[so], img[so + 16]);
     }
@@ -200,6 +199,13 @@ __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src
     const int tid = threadIdx.x;
     const int m = NB == 1 ? blockIdx.y : blockIdx.x, blk0 = NB == 1 ? blockIdx.x : 0;
     const size_t ro = (size_t)m * W;
+    // the operand form's image offsets of this thread's 4 elements, loaded first (their
+    // latency then overlaps the row loads)
+    uint2 offw = make_uint2(0, 0);
+    if (out_dtype == 2) {
+        const int M = NB == 1 ? gridDim.y : gridDim.x;
+        offw = *(const uint2*)&kOperandOff.v[M <= 2 ? M - 1 : 2][(4 * tid) & 127];
+    }
     // v = x (+ y) of this thread's elements 1024 (blk0 + b) + 4 tid + r, b < NB
     float s[NB][4];
     if (mode == 0) {
@@ -274,9 +280,9 @@ __global__ __launch_bounds__(256) void k_norm_fwht(const float* __restrict__ src
         if (out_dtype == 2) {
             const int M = NB == 1 ? gridDim.y : gridDim.x;
             if (M <= 2)
-                store_operand(v, tid, blk0 + b, m, M, W, (uint8_t*)xs, (uint8_t*)out);
+                store_operand(v, offw, tid, blk0 + b, m, M, W, (uint8_t*)xs, (uint8_t*)out);
             else
-                store_operand_wide(v, tid, blk0 + b, m, M, W, (uint8_t*)xs, (uint8_t*)out);
+                store_operand_wide(v, offw, tid, blk0 + b, m, M, W, (uint8_t*)xs, (uint8_t*)out);
         } else if (out_dtype == 0) {
             *(float4*)((float*)out + ro + base) = make_float4(v[0], v[1], v[2], v[3]);
         } else if (out_layout == 0) {

@@ -119,6 +119,27 @@ def test_full_shape_17408x5120(dev):
         assert rel_l2(y.cpu().numpy()[:, rows], ref_o).max() < TIGHT
 
 
+@pytest.mark.parametrize("K,T", [(1024, 1), (2048, 2), (3072, 2), (4096, 1), (5120, 2)])
+def test_long_single_matrix_orders(dev, K, T):
+    """One matrix of >= 64 tiles per workgroup (66000 rows): the launch picks the tile-strided
+    order where its scratch stores fit (K = 3072..5120) and the run order elsewhere (K = 1024,
+    and 2048 at T = 2, whose strided pair slots would reach past the scratch area into the
+    item sums).  Every row against a torch fp32 product of the GPU-expanded weights, sampled
+    rows against the oracle."""
+    N = 66000
+    W_np, _, _ = orc.synth_ptq1(N, K, K + T)
+    x_np = orc.synth_x(T, K, K + T + 1)
+    W = torch.from_numpy(W_np).to(dev)
+    x = torch.from_numpy(x_np).to(dev)
+    y = ops.gemv_ptq1(W, x, K, N, T)
+    ref = x.float() @ ops.expand_f16(W, K, N).float().T
+    torch.cuda.synchronize()
+    assert rel_l2(y.cpu().numpy(), ref.cpu().numpy()).max() < TIGHT
+    rows = np.arange(0, N, 331)
+    ref_o = orc.gemv_ptq1(np.ascontiguousarray(W_np[rows]), x_np.astype(np.float32), K, len(rows), T)
+    assert rel_l2(y.cpu().numpy()[:, rows], ref_o).max() < TIGHT
+
+
 @pytest.mark.parametrize("K,Ns,T,half2", [
     (5120, (96, 8, 8), 1, False), (6144, (40, 13), 2, True), (1024, (5, 64, 3, 17), 2, False),
     (17408, (20,), 1, False),
