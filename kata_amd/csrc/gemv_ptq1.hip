@@ -5,14 +5,16 @@
 //
 // Design (MI355X-first, not the reference's simdgroup float decode):
 //  * The packed weight bytes are never expanded in memory.  Per 128-weight block four lanes
-//    each hold 8 bytes of it (lane group g = lane/16 takes block bytes 20..27, 0..7, 8..15
-//    or 16..19, rotated by the block's position) and turn them into trits {-1,0,1} as int8:
-//    the trits of digits 1..4 of a byte come from one 4-byte LDS table entry, the digit-0
-//    trit ((3b) >> 8) - 1 from 16-bit-lane multiply-adds.  The trits are the B operand
-//    (B[k][column]) of three v_mfma_i32_16x16x64_i8 per block.
-//  * The activation is the A operand (A[i][k]) in an integer form the kernel builds itself
-//    in LDS from the fp16/fp32 input (no separate preparation launch): per 128-block a
-//    scale s = amax/32639 and q = rint(x/s) split into two int8 limbs (q = 256*hi + lo);
+//    each hold 32 of its trits (the dense layout of gemv_operand.h: lane group g = lane/16
+//    takes qs bytes 6g..6g+5 and two digits of a qh byte, read as 12 bytes per lane) and
+//    turn them into trits {-1,0,1} as int8: the trits of digits 1..4 of a byte come from
+//    one 4-byte LDS table entry, the digit-0 trit ((3b) >> 8) - 1 from 16-bit-lane
+//    multiply-adds.  The trits are the B operand (B[k][column]) of two
+//    v_mfma_i32_16x16x64_i8 per block.
+//  * The activation is the A operand (A[i][k]) in an integer form: per 128-block a scale
+//    s = amax/32639 and q = rint(x/s) split into two int8 limbs (q = 256*hi + lo), either
+//    written once by the activation's producer (the operand form, copied into LDS) or
+//    built in LDS by every workgroup from fp16/fp32 rows;
 //    A rows are (block, token, limb), so T = 2 costs no extra matrix-core work.  The matrix
 //    core sums trit*limb exactly in int32, so sum(trit*q) = 256*D_hi + D_lo per block and
 //    token, and y += d * s * that in fp32.  The only approximation is the 16-bit
@@ -657,7 +659,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 
 // ---------------------------------------------------------------------------------------
 // Padded LDS image the wide quantiser scatters into: per lane group 256 B of A rows + 16 B,
-// per MFMA 4 groups, per block 3 MFMAs.  The pads spread the quantiser's byte stores over
+// per MFMA 4 groups, per block 2 MFMAs.  The pads spread the quantiser's byte stores over
 // the LDS banks (a store instruction of the unpadded layout needs ~15 passes, this one
 // ~1.25).  kWideOff[e]: offset of element e's high limb for token 0 in that layout.
 constexpr int kWideG = 272, kWideM = 4 * kWideG;
@@ -679,20 +681,22 @@ __constant__ WideOffTable kWideOff = make_wide_off_table();
 // Wide verification GEMV for T = 3..8 token rows: the same integer arithmetic as the decode
 // GEMV (16-bit block fixed-point activation in two int8 limbs, exact int32 block sums,
 // fp32 scale and accumulate) with the MFMA operands laid out for tokens: B column = one of
-// 16 weight rows of a tile (lane group g decodes segment g of the row's block, no
-// rotation), A row i = (token i >> 1, limb i & 1) of the same block, so all 16 x 16
-// products are used (3 v_mfma_i32_16x16x64_i8 per 16 rows x 128 weights).
+// 16 weight rows of a tile (lane group g decodes its dense share of the row's block), A row
+// i = (token i >> 1, limb i & 1) of the same block, so all 16 x 16 products are used (2
+// v_mfma_i32_16x16x64_i8 per 16 rows x 128 weights).
 //
-// Two launches.  k_gemv_vw_prep quantises the T token rows once into the A operand image
-// in device memory: [block][mfma 3][lane group 4][A row 16][16 B] (3072 B per block) and
-// the per (block, token) scales [block][token pair] (float2).  k_gemv_vw: one 512-thread
+// The A operand image of the T token rows, [block][mfma 2][lane group 4][A row 16][16 B]
+// (2048 B per block), and the per (block, token) scales [block][token pair] (float2) are
+// the operand form of gemv_operand.h: written once by its producer (an input transform, or
+// k_gemv_vw_prep from fp16 / fp32 rows into a stream buffer).  k_gemv_vw: one 512-thread
 // workgroup (8 waves) per CU owns a contiguous range of at most kVwTMax tiles of 16 rows
 // of the concatenated rows of 1..4 matrices that share the tokens (the batch form) and
 // all of K.  Per K chunk of at most kVwCBMax blocks wave w takes blocks [w cb / 8,
 // (w+1) cb / 8) of the chunk: it loads their A operands from the image (L2-resident, read by
-// every workgroup) into registers, issues the weight loads of those blocks for all the
-// workgroup's tiles, then runs the tiles in order, adding into one fp32 accumulator pair
-// per tile.  At the end the 8 waves' accumulators add in a fixed tree
+// every workgroup) into registers, then runs the workgroup's tiles in order, the weight loads
+// of tile t + 1 issued before tile t is computed (issuing every tile's loads first left the
+// compute waiting for the whole stream: 13.6 against 11.5 us on ffn_gate at T = 8), adding
+// into one fp32 accumulator pair per tile.  At the end the 8 waves' accumulators add in a fixed tree
 // order (waves 4..7 into 0..3, 2..3 into 0..1, 1 into 0) through LDS: deterministic, and
 // no K split over workgroups (no partial sums, no reduction launch).
 constexpr int kVwTMax = 9;                       // tiles per workgroup (the switch in k_gemv_vw)
@@ -700,6 +704,7 @@ constexpr int kVwCBMax = 40;                     // blocks per K chunk (the wave
 constexpr int kVwWaves = 8;
 constexpr int kVwBB = kVwCBMax / kVwWaves;       // blocks of a wave per chunk
 constexpr int kVwLR = 6;                         // 64 trit-table replicas (conflict-free lookups)
+constexpr int kVwAhead = 1;                      // tiles whose weight loads run ahead of the compute
 constexpr int kVwImgBlk = kWideImgBlk;           // image bytes per block (2048)
 constexpr int kVwPrepBlocks = 1;                 // blocks per prep workgroup (one: the shortest chain)
 constexpr int kVwPrepThreads = kVwPrepBlocks >= 2 ? 256 : 128;   // 8 tokens x 16 chunks per block
@@ -850,14 +855,6 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
         wp[t] = Wm + (size_t)row * row_bytes + gemv_dense_byte0(g);
     }
 
-    // trit table (visible after the LDS-only barrier in the first chunk)
-#pragma unroll
-    for (int i = 0; i < lut_bytes(kVwLR) / 16 / 512; i++) {
-        const int o = tid + i * 512;
-        const uint32_t e = trit_entry((uint32_t)o / (REPS / 4));
-        lut[o] = make_uint4(e, e, e, e);
-    }
-
     const uint32_t laneoff = (uint32_t)(lane & (REPS - 1)) * 4u;
     lds_u8* lb = (lds_u8*)lut;
     const DenseLane dl = dense_lane<kVwLR>(g);
@@ -881,17 +878,18 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
             for (int m = 0; m < kDenseMfma; m++) A[bb][m] = *(const v4i*)(xa + (size_t)b * kVwImgBlk + m * 1024);
             sc[bb] = xscl[(size_t)b * 4 + g];
         }
-        // (3) every weight load of the wave's blocks for all TT tiles first (76 KB per CU for
-        // an FFN matrix: all of it in flight at once), then the tiles in order.  The tile loop
-        // is instantiated for each tile count (a switch on Tt), so it is straight-line code
-        // and each tile waits only for its own loads.  Blocks past the wave's (a ragged
+        // (3) the weight loads of the wave's blocks run kVwAhead tiles ahead of the tile being
+        // computed: tiles 0 .. kVwAhead-1 are issued first (and, in the first chunk, the trit
+        // table is built while they are in flight), then tile t is computed and tile
+        // t + kVwAhead issued, so the weight stream and the decode + MFMA overlap.  The tile
+        // loop is instantiated for each tile count (a switch on Tt), so it is straight-line
+        // code and each tile waits only for its own loads.  Blocks past the wave's (a ragged
         // chunk) load a valid dummy address.
         auto run = [&](auto ttc) {
             constexpr int TT = decltype(ttc)::value;
             // 12 bytes per lane and block: the lane's 8 and (lane group 3) the qh / scale dword
             uint32_t wl[TT][kVwBB], wh[TT][kVwBB], wq[TT][kVwBB];
-#pragma unroll
-            for (int t = 0; t < TT; t++)
+            auto issue = [&](int t) {
 #pragma unroll
                 for (int bb = 0; bb < kVwBB; bb++) {
                     const uint8_t* a = bb < nbw ? wp[t] + (size_t)(kb0 + bw0 + bb) * kBlockBytes : ximg;
@@ -901,14 +899,23 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
                     wh[t][bb] = w.y;
                     wq[t][bb] = w.z;
                 }
+            };
+#pragma unroll
+            for (int t = 0; t < TT && t < kVwAhead; t++) issue(t);
             if (kb0 == 0) {                      // every wave runs the same chunks: uniform
-                // the trit table (built before the loads) is visible to every wave after
-                // this LDS-only barrier
+                // the trit table, visible to every wave after this LDS-only barrier
+#pragma unroll
+                for (int i = 0; i < lut_bytes(kVwLR) / 16 / 512; i++) {
+                    const int o = tid + i * 512;
+                    const uint32_t e = trit_entry((uint32_t)o / (REPS / 4));
+                    lut[o] = make_uint4(e, e, e, e);
+                }
                 __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));   // lgkmcnt(0)
                 __builtin_amdgcn_s_barrier();
             }
             static_for<TT>([&](auto tc) {
                 constexpr int t = decltype(tc)::value;
+                if constexpr (t + kVwAhead < TT) issue(t + kVwAhead);
 #pragma unroll
                 for (int bb = 0; bb < kVwBB; bb++) {
                     if (bb < nbw) {
