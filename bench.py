@@ -475,6 +475,38 @@ def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
     return verify_wide
 
 
+def run_calib_sweep(torch, ops, dev, stream, cap_stream):
+    """The plain read at the sweep's sizes over every geometry of kata_calib_read_cfg:
+    threads 256/512/1024 x workgroups per CU 1/2/4/8 (<= 2048 threads per CU) x loads in
+    flight 2/4/8/16 x non-temporal hint off/on, graph-replayed over rotating buffers (>= 512
+    MB per size); per size every configuration's us and the best."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    cword = torch.zeros(4, dtype=torch.int32, device=dev)
+    out = {}
+    for label, nbytes in (("19.5MB", packed_bytes(5120, 17408)), ("39MB", 2 * packed_bytes(5120, 17408)),
+                          ("278MB", packed_bytes(5120, 248320))):
+        nb = max(2, -(-512 * 1024 * 1024 // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nb)]
+        for b_ in bufs:
+            b_.fill_(1)
+        reps = 100 if nbytes < 1e8 else 20
+        res = {}
+        for threads in (256, 512, 1024):
+            for wpc in (1, 2, 4, 8):
+                if threads * wpc > 2048:
+                    continue
+                for inflight in (2, 4, 8, 16):
+                    for nt in (False, True):
+                        us = graph_time(torch, lambda r: ops.calib_read_cfg(bufs[r % nb], cword, threads, cus * wpc,
+                                                                            inflight, nt), reps, stream, cap_stream)
+                        res[f"{threads}x{wpc} d{inflight}{' nt' if nt else ''}"] = round(us, 3)
+        best = min(res, key=res.get)
+        out[label] = {"bytes": nbytes, "best": best, "best_us": res[best],
+                      "best_GBps": round(nbytes / (res[best] * 1e-6) / 1e9, 1), "all_us": res}
+        del bufs
+    return out
+
+
 def run_calibration(torch, ops, dev, stream, cap_stream, reps):
     """The launch floor of an empty kernel at the decode GEMV's geometry and a plain streaming
     read at the sweep's sizes (same protocol as per_matrix), over rotating buffers (>= 512 MB
@@ -524,6 +556,9 @@ def main():
     ap.add_argument("--step-only", action="store_true",
                     help="only the timed decode-sweep steps (for counter runs), then print value and exit")
     ap.add_argument("--reps", type=int, default=200, help="repeats per matrix for the per-matrix tables")
+    ap.add_argument("--calib-sweep", action="store_true",
+                    help="only the plain-read sweep over geometries (threads, workgroups per CU, loads in "
+                         "flight, non-temporal hint) behind the read ceiling, then print it and exit")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MB",
                     help="only run 20 plain torch copies of MB MiB (HBM-counter calibration) and exit")
     args = ap.parse_args()
@@ -540,6 +575,10 @@ def main():
     stream = torch.cuda.current_stream(dev)
     if args.calib_only:
         print(json.dumps({"calibration": run_calibration(torch, ops, dev, stream, torch.cuda.Stream(dev), args.reps)}))
+        return
+
+    if args.calib_sweep:
+        print(json.dumps({"calib_sweep": run_calib_sweep(torch, ops, dev, stream, torch.cuda.Stream(dev))}))
         return
 
     if args.calib_copy:

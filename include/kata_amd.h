@@ -221,6 +221,11 @@ int kata_rms_fwht(const float* src, const float* src2, const float* gs, void* ou
 int kata_calib_empty(uint32_t* out, int wgs, void* stream);
 int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* stream);
 int kata_calib_read_peak(const void* p, size_t bytes, uint32_t* out, void* stream);
+/* The same read at any geometry of the sweep that chose the ceiling: threads per workgroup
+ * 256, 512 or 1024, wgs workgroups (1..65536), inflight 2, 4, 8 or 16 loads per lane, nt
+ * nonzero for the non-temporal hint. */
+int kata_calib_read_cfg(const void* p, size_t bytes, uint32_t* out, int threads, int wgs, int inflight, int nt,
+                        void* stream);
 
 /* Greedy argmax of n fp32 logits into *out (device int): an element counts only if strictly
  * greater than the best so far (NaN and -inf never do), lowest index on ties, 0x7fffffff

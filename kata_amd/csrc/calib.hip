@@ -4,14 +4,15 @@
 // achievable HBM read rate at a given size.
 //
 // The read kernel: each wave streams a contiguous share of the buffer with 16-byte raw
-// buffer loads, four in flight per lane, and folds what it read into one word so the loads
+// buffer loads, D in flight per lane, and folds what it read into one word so the loads
 // cannot be dropped; bytes past the last whole 1 KB piece of a share are read by the
 // share's last wave with the same loads (out-of-range lanes read zero).  Two forms:
 //   - the decode GEMV's geometry (1024-thread workgroups, one per CU, ordinary loads);
 //   - the read ceiling: the fastest plain read found by a sweep over workgroup size
-//     (256/512/1024), workgroups per CU (1/2/4/8), loads in flight (2/4/8/16), load width
-//     (8/16 B), LDS-DMA loads and the non-temporal hint, at 19.5 MB, 39 MB and 278 MB:
-//     256-thread workgroups, two per CU, 16-byte non-temporal loads (slc), four in flight.
+//     (256/512/1024), workgroups per CU (1/2/4/8), loads in flight (2/4/8/16) and the
+//     non-temporal hint (launch_calib_read_cfg, bench.py --calib-sweep), at 19.5 MB, 39 MB
+//     and 278 MB: 256-thread workgroups, two per CU, 16-byte non-temporal loads (slc), four
+//     in flight.
 #include "common.h"
 #include "launch.h"
 
@@ -25,10 +26,10 @@ __global__ __launch_bounds__(1024) void k_calib_empty(uint32_t* out) {
     if (threadIdx.x == 1023 && blockIdx.x == 0x7fffffff) out[0] = 1;
 }
 
-template <int BLK, int AUX>
+template <int BLK, int AUX, int D = 4>
 __global__ __launch_bounds__(BLK) void k_calib_read(const uint8_t* __restrict__ p, uint32_t bytes,
                                                     uint32_t* __restrict__ out) {
-    constexpr int D = 4, WPG = BLK / 64;
+    constexpr int WPG = BLK / 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t nw = gridDim.x * WPG, w = blockIdx.x * WPG + wave;
     const uint32_t pieces = (bytes + 1023) / 1024;            // 1 KB per wave load
@@ -52,7 +53,36 @@ __global__ __launch_bounds__(BLK) void k_calib_read(const uint8_t* __restrict__ 
     if (acc == 0x9e3779b9u) out[0] = acc;     // practically never: keeps the loads
 }
 
+template <int BLK, int AUX, int D>
+hipError_t launch_read(const uint8_t* p, uint32_t bytes, uint32_t* out, int wgs, hipStream_t s) {
+    hipLaunchKernelGGL((k_calib_read<BLK, AUX, D>), dim3(wgs), dim3(BLK), 0, s, p, bytes, out);
+    return hipGetLastError();
+}
+template <int BLK, int AUX>
+hipError_t launch_read_d(const uint8_t* p, uint32_t bytes, uint32_t* out, int wgs, int inflight, hipStream_t s) {
+    switch (inflight) {
+        case 2: return launch_read<BLK, AUX, 2>(p, bytes, out, wgs, s);
+        case 4: return launch_read<BLK, AUX, 4>(p, bytes, out, wgs, s);
+        case 8: return launch_read<BLK, AUX, 8>(p, bytes, out, wgs, s);
+        default: return launch_read<BLK, AUX, 16>(p, bytes, out, wgs, s);
+    }
+}
+template <int BLK>
+hipError_t launch_read_nt(const uint8_t* p, uint32_t bytes, uint32_t* out, int wgs, int inflight, bool nt,
+                          hipStream_t s) {
+    return nt ? launch_read_d<BLK, 2>(p, bytes, out, wgs, inflight, s) : launch_read_d<BLK, 0>(p, bytes, out, wgs, inflight, s);
+}
+
 }  // namespace
+
+hipError_t launch_calib_read_cfg(const uint8_t* p, uint32_t bytes, uint32_t* out, int threads, int wgs, int inflight,
+                                 bool nt, hipStream_t s) {
+    switch (threads) {
+        case 256: return launch_read_nt<256>(p, bytes, out, wgs, inflight, nt, s);
+        case 512: return launch_read_nt<512>(p, bytes, out, wgs, inflight, nt, s);
+        default: return launch_read_nt<1024>(p, bytes, out, wgs, inflight, nt, s);
+    }
+}
 
 hipError_t launch_calib_empty(uint32_t* out, int wgs, hipStream_t s) {
     hipLaunchKernelGGL(k_calib_empty, dim3(wgs), dim3(1024), 0, s, out);

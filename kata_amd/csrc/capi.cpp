@@ -389,6 +389,19 @@ int kata_calib_read(const void* p, size_t bytes, uint32_t* out, int wgs, void* s
                         "calib_read");
 }
 
+int kata_calib_read_cfg(const void* p, size_t bytes, uint32_t* out, int threads, int wgs, int inflight, int nt,
+                        void* stream) {
+    if (!p || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (bytes == 0 || bytes > 0x7fffffffu) return fail(KATA_EINVAL, "bytes=%zu must be in 1..2^31-1", bytes);
+    if (!aligned(p, 16)) return fail(KATA_EINVAL, "p must be 16-byte aligned");
+    if (threads != 256 && threads != 512 && threads != 1024) return fail(KATA_EINVAL, "threads=%d", threads);
+    if (wgs < 1 || wgs > 65536) return fail(KATA_EINVAL, "wgs=%d", wgs);
+    if (inflight != 2 && inflight != 4 && inflight != 8 && inflight != 16) return fail(KATA_EINVAL, "inflight=%d", inflight);
+    return check_launch(kata::launch_calib_read_cfg((const uint8_t*)p, (uint32_t)bytes, out, threads, wgs, inflight, nt != 0,
+                                                    (hipStream_t)stream),
+                        "calib_read_cfg");
+}
+
 int kata_calib_read_peak(const void* p, size_t bytes, uint32_t* out, void* stream) {
     if (!p || !out) return fail(KATA_EINVAL, "null pointer argument");
     if (bytes == 0 || bytes > 0x7fffffffu) return fail(KATA_EINVAL, "bytes=%zu must be in 1..2^31-1", bytes);

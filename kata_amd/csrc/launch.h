@@ -66,6 +66,9 @@ hipError_t launch_calib_empty(uint32_t* out, int wgs, hipStream_t s);
 hipError_t launch_calib_read(const uint8_t* p, uint32_t bytes, uint32_t* out, int wgs, hipStream_t s);
 // the read ceiling: two 256-thread workgroups per CU, non-temporal 16-byte loads
 hipError_t launch_calib_read_peak(const uint8_t* p, uint32_t bytes, uint32_t* out, int cus, hipStream_t s);
+// any swept geometry: threads 256/512/1024 per workgroup, wgs workgroups, 2/4/8/16 loads in flight
+hipError_t launch_calib_read_cfg(const uint8_t* p, uint32_t bytes, uint32_t* out, int threads, int wgs, int inflight,
+                                 bool nt, hipStream_t s);
 
 // ---- argmax of the logits (argmax.hip)
 hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s);

@@ -346,6 +346,15 @@ def calib_read(buf: torch.Tensor, out: torch.Tensor, nbytes: int | None = None, 
     check(lib().kata_calib_read(_ptr(buf), n, _ptr(out), wgs, _stream(buf)))
 
 
+def calib_read_cfg(buf: torch.Tensor, out: torch.Tensor, threads: int, wgs: int, inflight: int, nt: bool,
+                   nbytes: int | None = None) -> None:
+    """Plain streaming read at a given geometry (the sweep behind the read ceiling)."""
+    _need_gpu(buf, out)
+    n = _bytes(buf) if nbytes is None else nbytes
+    _need_bytes("buf", buf, n)
+    check(lib().kata_calib_read_cfg(_ptr(buf), n, _ptr(out), threads, wgs, inflight, int(nt), _stream(buf)))
+
+
 def calib_read_peak(buf: torch.Tensor, out: torch.Tensor, nbytes: int | None = None) -> None:
     """Plain streaming read of nbytes (default: all) of buf at the fastest plain-read geometry."""
     _need_gpu(buf, out)
