@@ -47,7 +47,9 @@ const char* kata_version(void);
 /* ---------------------------------------------------------------- decode GEMVs -------
  * y[t][n] = sum_b d[n,b] * sum_e trit[n,b,e] * x[t][128b+e], fp32 out, t < T, T in {1,2}.
  * K % 128 == 0, K <= kata_gemv_ptq1_max_k(T), N >= 1.  x is 16-byte aligned; y is [T][N]
- * fp32.  One kernel launch; no work buffer (the activation is quantised in-kernel).
+ * fp32.  One kernel launch, no work buffer: fp16 / fp32 rows are quantised by every
+ * workgroup; x_dtype KATA_XQ (x_layout KATA_X_ROWS) takes the operand form of the T rows,
+ * quantised once by its producer, with the same y bit for bit.
  * Replaces Engine::dGemvPtq1 (src/engine.cpp:97-101, src/engine.h:155; kernel
  * k_gemv_v1_nr4_sg4, shaders/gemv_fast.metal:9-50) for T = 1, and the `gv` lambda of
  * Engine::verify2 (src/engine.cpp:440-443; k_gemv_lut2_nr4_sg4, shaders/mtp.metal:164-205,
@@ -89,7 +91,9 @@ int kata_gemv_ptq1_batch(int count, const uint8_t* const* W, float* const* y, co
  * stream's first such call (which must not be captured; calls on one stream are ordered,
  * calls on different streams use their own buffers), then one launch reads every weight
  * byte once for all T rows.  T <= 2 runs the decode GEMV above (same result as
- * kata_gemv_ptq1 with these rows, no buffer).
+ * kata_gemv_ptq1 with these rows, no buffer).  x_dtype KATA_XQ takes the operand form of
+ * the T rows (kata_gemv_prepare_x, or an input transform with out_dtype KATA_XQ): no prep
+ * launch, no buffer, the same y bit for bit.
  * Replaces Engine::dWide / xWideGemv (src/engine.cpp:542-556, src/engine.h:109,140; kernel
  * k_wide_m16_n16_k128_g4, shaders/wide.metal:41-99, whose x is fp16 rows padded to 16). */
 int kata_gemv_ptq1_wide(const uint8_t* W, const void* x, int x_dtype, float* y, int K, int N, int T,
