@@ -118,3 +118,54 @@ def test_graph_replay_after_scratch_grows(dev):
         ops.gemv_ptq1_wide(Ws[0], xs[0], Ks[0], Ns[0], out=ys[0])      # reallocates
     torch.cuda.synchronize()
     assert torch.equal(ys[0], ref_small)
+
+
+def test_graph_dispatcher_operand_paths_capture_first(dev):
+    """The dispatcher's decode and verify FFN sublayers keep their activations in the GEMVs'
+    operand form and allocate nothing: they are captured on a fresh stream with no eager call
+    before (an allocation under capture would fail the capture), and every replay equals an
+    eager run on another stream bit for bit."""
+    from kata_amd.engine import Dispatch
+    from kata_amd.capi import lib
+    H, F = 2048, 3072
+    Wg, _, _ = orc.synth_ptq1(F, H, 71)
+    Wu, _, _ = orc.synth_ptq1(F, H, 72)
+    Wd, _, _ = orc.synth_ptq1(H, F, 73)
+    buf = np.concatenate([Wg.ravel(), Wu.ravel(), Wd.ravel()])
+    offs = (0, Wg.size, Wg.size + Wu.size)
+    d = Dispatch(torch.from_numpy(buf).to(dev))
+    rng = np.random.default_rng(5)
+    t = lambda a: torch.from_numpy(a.astype(np.float32)).to(dev)
+    gs_in, gs_down = t(rng.choice([-1.0, 1.0], H)), t(rng.choice([-1.0, 1.0], F))
+    cases = []
+    for T in (1, 3, 8):
+        x, y = t(rng.standard_normal((T, H))), t(0.3 * rng.standard_normal((T, H)))
+        out, xnew = torch.empty((T, H), device=dev), torch.empty((T, H), device=dev)
+        if T == 1:
+            work = torch.empty(H + 3 * F, dtype=torch.float32, device=dev)
+            fn = (lambda x=x, y=y, out=out, xnew=xnew, work=work:
+                  d.ffn_decode(*offs, x[0], y[0], gs_in, gs_down, H, F, out=out[0], xnew=xnew[0], work=work))
+        else:
+            work = torch.empty(int(lib().kata_ffn_verify_work_bytes(H, F, T)), dtype=torch.uint8, device=dev)
+            fn = (lambda x=x, y=y, out=out, xnew=xnew, work=work:
+                  d.ffn_verify(*offs, x, y, gs_in, gs_down, H, F, out=out, xnew=xnew, work=work))
+        cases.append((fn, out))
+    cs = torch.cuda.Stream(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        for fn, _ in cases:
+            fn()
+    es = torch.cuda.Stream(dev)
+    with torch.cuda.stream(es):
+        for fn, _ in cases:
+            fn()
+    torch.cuda.synchronize()
+    ref = [o.clone() for _, o in cases]
+    for r in range(3):
+        for _, o in cases:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for (_, o), e in zip(cases, ref):
+            assert torch.equal(o, e), f"replay {r}"
