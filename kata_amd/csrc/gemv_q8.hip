@@ -80,9 +80,9 @@ struct Q8Mats {
 // Workgroup = 4 waves = (4 / KS) row groups x KS slices of the row's blocks (KS per matrix,
 // the same as a launch of that matrix alone, so a batch equals the single launches bit for bit).
 // XL: the activation rows are copied into LDS once per workgroup and every wave reads its
-// blocks' activations from there (one K slice: the workgroup's 8 waves are 8 row groups that
-// share them; 8 waves copy half as much per row as 4, 24.1 -> 23.5 us at 17408 x 5120, 16
-// were slower), instead of each row group reading them from L2.
+// blocks' activations from there (8 waves: at T = 2 one K slice, 8 row groups; at T = 1 each
+// matrix's own K slices; 8 waves copy half as much per row as 4, 24.1 -> 23.5 us at 17408 x
+// 5120 T = 2, 16 were slower), instead of each row group reading them from L2.
 template <int T, bool XH, int R, bool MULTI, bool XL>
 __global__ __launch_bounds__(XL ? kQ8XlWaves * 64 : 256) void k_gemv_q8(Q8Mats P, const void* __restrict__ xg, int K) {
     constexpr int WV = XL ? kQ8XlWaves : 4;
@@ -259,7 +259,7 @@ hipError_t launch_q8_r(Q8Mats& P, const void* x, int K, bool xl, hipStream_t s) 
     P.wg0[0] = 0;
     for (int i = 0; i < P.count; i++) {
         const int N = P.N[i];
-        P.lks[i] = xl ? 0 : (T == 1 && nb >= 256) ? 1 : (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) ? 2 : 0;
+        P.lks[i] = (xl && T == 2) ? 0 : (T == 1 && nb >= 256) ? 1 : (nb >= 256 || (nb >= 128 && (T == 2 || N < 8192))) ? 2 : 0;
         const int rpw = R * ((xl ? kQ8XlWaves : 4) >> P.lks[i]);     // rows per workgroup
         P.wg0[i + 1] = P.wg0[i] + (N + rpw - 1) / rpw;
     }
@@ -288,7 +288,9 @@ hipError_t launch_q8_r(Q8Mats& P, const void* x, int K, bool xl, hipStream_t s) 
 }
 
 // One fp16 row (v_dot2 form, little VALU per byte): 2 rows per wave, twice the waves of 4
-// (17408 x 5120: 26.1 -> 20.9 us).  Two rows (fp32 FMAs per quant and token): rows of fewer
+// (17408 x 5120: 26.1 -> 20.9 us); launches of >= 8192 rows with rows of < 256 blocks share
+// the activation through LDS too, each matrix keeping its K-slice geometry, so results do not
+// change (gate + up batched 41.7 -> 38.4 us; a lone 1024-row matrix was slower that way).  Two rows (fp32 FMAs per quant and token): rows of fewer
 // than 256 blocks with the activations shared through LDS (XL) and 2 rows per wave
 // (17408 x 5120: 29.8 -> 24.0 us; XL at 4 rows per wave 27.2, at 8 37.9); longer rows read
 // them per row group and keep 4 rows per wave to reuse each block's activations (5120 x 17408:
@@ -299,7 +301,9 @@ hipError_t launch_q8_r(Q8Mats& P, const void* x, int K, bool xl, hipStream_t s) 
 template <int T, bool XH>
 hipError_t launch_q8_t(Q8Mats& P, const void* x, int K, hipStream_t s) {
     const int nb = K / kQ8Group;
-    const bool xl = T == 2 && T * K * (XH ? 2 : 4) <= kQ8XlMax && nb < 256;
+    int rows = 0;
+    for (int i = 0; i < P.count; i++) rows += P.N[i];
+    const bool xl = T * K * (XH ? 2 : 4) <= kQ8XlMax && nb < 256 && (T == 2 || rows >= 8192);
     if (xl) return launch_q8_r<T, XH, kQ8XlRows>(P, x, K, true, s);
     return launch_q8_r<T, XH, T == 1 ? 2 : 4>(P, x, K, false, s);
 }
