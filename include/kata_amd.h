@@ -230,6 +230,12 @@ int kata_calib_read_peak(const void* p, size_t bytes, uint32_t* out, void* strea
  * nonzero for the non-temporal hint. */
 int kata_calib_read_cfg(const void* p, size_t bytes, uint32_t* out, int threads, int wgs, int inflight, int nt,
                         void* stream);
+/* The decode GEMV's weight-load stream alone: the loads kata_gemv_ptq1 issues for one K x N
+ * PTQ1_0 matrix at T = 1 (the same workgroups, item order, 12-byte lane windows and ring of
+ * four items) with the decode, the matrix-core work and the row sums left out, the rate
+ * that loop would reach if the rest of each item were free.  K a multiple of 128, the matrix
+ * 16-byte aligned and < 2^31 bytes; out as above. */
+int kata_calib_read_ptq1(const void* W, int K, int N, uint32_t* out, void* stream);
 
 /* Greedy argmax of n fp32 logits into *out (device int): an element counts only if strictly
  * greater than the best so far (NaN and -inf never do), lowest index on ties, 0x7fffffff

@@ -87,6 +87,7 @@ SIGNATURES = {
     "kata_calib_read": (I, [P, SZ, P, I, P]),
     "kata_calib_read_peak": (I, [P, SZ, P, P]),
     "kata_calib_read_cfg": (I, [P, SZ, P, I, I, I, I, P]),
+    "kata_calib_read_ptq1": (I, [P, I, I, P, P]),
     "kata_gemv_xq_bytes": (SZ, [I, I]),
     "kata_gemv_prepare_x": (I, [P, I, I, I, I, P, P]),
 }

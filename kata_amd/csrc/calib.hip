@@ -13,7 +13,11 @@
 //     non-temporal hint (launch_calib_read_cfg, bench.py --calib-sweep), at 19.5 MB, 39 MB
 //     and 278 MB: 256-thread workgroups, two per CU, 16-byte non-temporal loads (slc), four
 //     in flight.
+// A third kernel replays the decode GEMV's weight-load stream alone (k_gemv_ptq1, one
+// matrix, T = 1): the reads of its loop with the decode, the matrix-core work and the item
+// sums left out, which is what that loop could reach if the rest of each item were free.
 #include "common.h"
+#include "gemv_operand.h"
 #include "launch.h"
 
 namespace kata {
@@ -21,6 +25,7 @@ namespace kata {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 __global__ __launch_bounds__(1024) void k_calib_empty(uint32_t* out) {
     if (threadIdx.x == 1023 && blockIdx.x == 0x7fffffff) out[0] = 1;
@@ -48,6 +53,75 @@ __global__ __launch_bounds__(BLK) void k_calib_read(const uint8_t* __restrict__ 
         for (int u = 0; u < D; u++) {
             acc ^= r[u].x + r[u].y + r[u].z + r[u].w;
             r[u] = ld(i + D + u);
+        }
+    }
+    if (acc == 0x9e3779b9u) out[0] = acc;     // practically never: keeps the loads
+}
+
+// The decode GEMV's weight loads for one matrix (gemv_ptq1.hip, k_gemv_ptq1 with T = 1):
+// one 1024-thread workgroup per CU owns tpw tiles of 4 rows; its 16 waves walk the items
+// (4 consecutive blocks of the tile's 4 rows) in the kernel's run order, or its tile-strided
+// order when `strided` (wave w: step pair w % np of tiles h, h + G, ...; h = w / np,
+// G = 16 / np); each lane loads the same 12 bytes (row x & 3, block x >> 2 of the step, the
+// lane group's window at gemv_dense_byte0) into a ring of 4 items, and item u + 1 is read
+// before slot u is reloaded, as in the kernel.
+__global__ __launch_bounds__(1024) void k_calib_read_ptq1(const uint8_t* __restrict__ W, int N, int nb, int tpw,
+                                                           int strided_ok, uint32_t* __restrict__ out) {
+    constexpr int D = 4;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int x_ = lane & 15, g = lane >> 4;
+    const int nq = gemv_nq(nb * kGroup), np = nq >> 1, G = 16 / np;
+    const int tiles = (N + 3) >> 2, wt0 = (int)blockIdx.x * tpw, Tt = min(tiles, wt0 + tpw) - wt0;
+    const uint32_t row_bytes = (uint32_t)nb * kBlockBytes, tstep = 4 * row_bytes, cstep = 4 * kBlockBytes;
+    const bool strided = strided_ok && Tt >= 2 * G;
+    int n, lt, Tw;
+    uint32_t lso, tnext, cwrap;
+    if (strided) {
+        const int sp = wave % np, sh = wave / np;
+        n = wave < G * np && sh < Tt ? 2 * ((Tt - sh + G - 1) / G) : 0;
+        lt = sh;
+        lso = (uint32_t)(wt0 + sh) * tstep + (uint32_t)(2 * sp) * cstep;
+        Tw = 0x7fffffff;
+        tnext = (uint32_t)G * tstep - cstep;
+        cwrap = 0;
+    } else {
+        const int S = nq * Tt;
+        const int s0 = ((wave * S) / 16) & ~1, s1 = wave == 15 ? S : (((wave + 1) * S) / 16) & ~1;
+        n = s1 - s0;
+        lt = (s0 % (2 * Tt)) >> 1;
+        lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(2 * (s0 / (2 * Tt))) * cstep;
+        Tw = Tt;
+        tnext = tstep - cstep;
+        cwrap = cstep - (uint32_t)(Tt - 1) * tstep;
+    }
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((uint32_t)N * row_bytes), 0x00020000);
+    const uint32_t voff = (uint32_t)(x_ & 3) * row_bytes + (uint32_t)(x_ >> 2) * kBlockBytes + (uint32_t)gemv_dense_byte0(g);
+    int lrem = n, par = 0;
+    // past the wave's items: an offset beyond the buffer (zeros, no memory access)
+    auto ld = [&]() -> u32x4 {
+        const uint32_t so = lrem > 0 ? lso : 0x80000000u;
+        const u32x3 v = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, (int)voff, (int)so, 0));
+        if (par) {
+            const bool wrap = ++lt == Tw;
+            lt = wrap ? 0 : lt;
+            lso += wrap ? cwrap : tnext;
+        } else {
+            lso += cstep;
+        }
+        par ^= 1;
+        --lrem;
+        return u32x4{v.x, v.y, v.z, 0u};
+    };
+    u32x4 ring[D];
+#pragma unroll
+    for (int u = 0; u < D; u++) ring[u] = ld();
+    uint32_t acc = ring[0].x + ring[0].y + ring[0].z;
+    for (int j = 0; j < n; j += D) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            const int v = (u + 1) % D;
+            acc ^= ring[v].x + ring[v].y + ring[v].z;
+            ring[u] = ld();
         }
     }
     if (acc == 0x9e3779b9u) out[0] = acc;     // practically never: keeps the loads
@@ -97,6 +171,17 @@ hipError_t launch_calib_read(const uint8_t* p, uint32_t bytes, uint32_t* out, in
 hipError_t launch_calib_read_peak(const uint8_t* p, uint32_t bytes, uint32_t* out, int cus, hipStream_t s) {
     // aux 2 = slc: the non-temporal hint on the load
     hipLaunchKernelGGL((k_calib_read<256, 2>), dim3(2 * cus), dim3(256), 0, s, p, bytes, out);
+    return hipGetLastError();
+}
+
+// The decode GEMV's split for one matrix at one workgroup per CU, and its rule for the
+// tile-strided order at T = 1 (gemv_ptq1.hip, gemv_strided: whole step pairs of 8 blocks,
+// 15 or 16 waves busy, >= 64 tiles per workgroup, G <= 12 for the scratch slots).
+hipError_t launch_calib_read_ptq1(const uint8_t* W, int K, int N, uint32_t* out, int cus, hipStream_t s) {
+    const int nb = K / kGroup, np = gemv_nq(K) / 2, G = np > 0 ? 16 / np : 0;
+    const int tiles = (N + 3) / 4, tpw = (tiles + cus - 1) / cus, wgs = (tiles + tpw - 1) / tpw;
+    const int strided = nb % 8 == 0 && np > 0 && G >= 2 && G * np >= 15 && tpw >= 64 && G * 64 + 256 <= 1024;
+    hipLaunchKernelGGL(k_calib_read_ptq1, dim3(wgs), dim3(1024), 0, s, W, N, nb, tpw, strided, out);
     return hipGetLastError();
 }
 

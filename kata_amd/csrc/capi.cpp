@@ -402,6 +402,16 @@ int kata_calib_read_cfg(const void* p, size_t bytes, uint32_t* out, int threads,
                         "calib_read_cfg");
 }
 
+int kata_calib_read_ptq1(const void* W, int K, int N, uint32_t* out, void* stream) {
+    if (!W || !out) return fail(KATA_EINVAL, "null pointer argument");
+    if (K <= 0 || K % kata::kGroup || N <= 0) return fail(KATA_EINVAL, "K=%d (a positive multiple of 128), N=%d", K, N);
+    if ((long long)N * (K / kata::kGroup) * kata::kBlockBytes > 0x7fffffffLL)
+        return fail(KATA_EINVAL, "N*K matrix of %lld bytes exceeds 2^31-1", (long long)N * (K / kata::kGroup) * kata::kBlockBytes);
+    if (!aligned(W, 16)) return fail(KATA_EINVAL, "W must be 16-byte aligned");
+    return check_launch(kata::launch_calib_read_ptq1((const uint8_t*)W, K, N, out, calib_wgs(0), (hipStream_t)stream),
+                        "calib_read_ptq1");
+}
+
 int kata_calib_read_peak(const void* p, size_t bytes, uint32_t* out, void* stream) {
     if (!p || !out) return fail(KATA_EINVAL, "null pointer argument");
     if (bytes == 0 || bytes > 0x7fffffffu) return fail(KATA_EINVAL, "bytes=%zu must be in 1..2^31-1", bytes);

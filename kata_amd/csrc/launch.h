@@ -69,6 +69,8 @@ hipError_t launch_calib_read_peak(const uint8_t* p, uint32_t bytes, uint32_t* ou
 // any swept geometry: threads 256/512/1024 per workgroup, wgs workgroups, 2/4/8/16 loads in flight
 hipError_t launch_calib_read_cfg(const uint8_t* p, uint32_t bytes, uint32_t* out, int threads, int wgs, int inflight,
                                  bool nt, hipStream_t s);
+// the decode GEMV's weight-load stream alone (one matrix, T = 1, one workgroup per CU)
+hipError_t launch_calib_read_ptq1(const uint8_t* W, int K, int N, uint32_t* out, int cus, hipStream_t s);
 
 // ---- argmax of the logits (argmax.hip)
 hipError_t launch_argmax(const float* x, int n, int* out, hipStream_t s);

@@ -363,6 +363,14 @@ def calib_read_peak(buf: torch.Tensor, out: torch.Tensor, nbytes: int | None = N
     check(lib().kata_calib_read_peak(_ptr(buf), n, _ptr(out), _stream(buf)))
 
 
+def calib_read_ptq1(W: torch.Tensor, K: int, N: int, out: torch.Tensor) -> None:
+    """The decode GEMV's weight-load stream alone for the K x N PTQ1_0 matrix W at T = 1 (its
+    loads in its order, nothing else): the rate its loop would reach if the rest were free."""
+    _need_gpu(W, out)
+    _need_bytes("W", W, N * (K // 128) * 28)
+    check(lib().kata_calib_read_ptq1(_ptr(W), K, N, _ptr(out), _stream(W)))
+
+
 def _np_ptr(a: np.ndarray):
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(ctypes.c_void_p)

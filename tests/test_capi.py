@@ -89,6 +89,10 @@ def test_other_entry_points_reject_bad_shapes():
     assert lib.kata_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, 5120, 1, 2, None) == KATA_EINVAL
     assert lib.kata_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, 5120, 1, 1, None) == KATA_EINVAL   # mode 1 needs src2
     assert lib.kata_rms_fwht(FAKE, None, FAKE, FAKE, 0, 0, 5120, 1, 4, None) == KATA_EINVAL
+    assert lib.kata_calib_read_ptq1(FAKE, 5000, 64, FAKE, None) == KATA_EINVAL        # K % 128
+    assert lib.kata_calib_read_ptq1(FAKE, 5120, 0, FAKE, None) == KATA_EINVAL
+    assert lib.kata_calib_read_ptq1(FAKE, 5120, 2_000_000, FAKE, None) == KATA_EINVAL  # >= 2^31 bytes
+    assert lib.kata_calib_read_ptq1(ctypes.c_void_p(0x10008), 5120, 64, FAKE, None) == KATA_EINVAL  # alignment
     # the 27B shapes (K up to 17408) must fit for both T
     assert lib.kata_gemv_ptq1_max_k(1) >= 17408 and lib.kata_gemv_ptq1_max_k(2) >= 17408
     assert lib.kata_gemv_ptq1_max_k(1) % 128 == 0 and lib.kata_gemv_ptq1_max_k(2) % 128 == 0
