@@ -494,6 +494,27 @@ def run_verify_wide(torch, ops, dev, copies, ncopies, time_reps, reps):
     return verify_wide
 
 
+def run_lm_head(torch, ops, dev, lx, time_reps):
+    """The lm_head GEMV (5120 -> 248320, 278 MB; two weight copies, 556 MB, past the MALL) on
+    the operand form lx, the greedy argmax of its logits, and the GEMV's weight-load stream
+    alone (kata_calib_read_ptq1) on the same weights."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 700)
+    lm = [device_weights(torch, dev, 5120, 248320, gen) for _ in range(2)]
+    ly = torch.empty((1, 248320), dtype=torch.float32, device=dev)
+    lidx = torch.empty(1, dtype=torch.int32, device=dev)
+    cw = torch.zeros(4, dtype=torch.int32, device=dev)
+    us_lm = time_reps(lambda r: ops.gemv_ptq1(lm[r % 2], lx, 5120, 248320, 1, out=ly), 40)
+    us_am = time_reps(lambda r: ops.argmax(ly, out=lidx), 40)
+    us_lws = time_reps(lambda r: ops.calib_read_ptq1(lm[r % 2], 5120, 248320, cw), 40)
+    nbytes = lm[0].numel()
+    del lm
+    return {"K": 5120, "N": 248320, "gemv_us": round(us_lm, 2), "GBps": round(nbytes / (us_lm * 1e-6) / 1e9, 1),
+            "argmax_us": round(us_am, 2), "weight_stream_us": round(us_lws, 2),
+            "weight_stream_GBps": round(nbytes / (us_lws * 1e-6) / 1e9, 1),
+            "vs_weight_stream": round(us_lm / us_lws, 3)}
+
+
 def run_calib_sweep(torch, ops, dev, stream, cap_stream):
     """The plain read at the sweep's sizes over every geometry of kata_calib_read_cfg:
     threads 256/512/1024 x workgroups per CU 1/2/4/8 (<= 2048 threads per CU) x loads in
@@ -570,6 +591,8 @@ def main():
                     help="only the wide verification GEMV figures (for profiler runs), then exit")
     ap.add_argument("--ffn-only", action="store_true",
                     help="only the FFN sublayer figures (for profiler runs), then exit")
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="only the lm_head GEMV, its argmax and its weight-load stream alone, then exit")
     ap.add_argument("--q8-only", action="store_true",
                     help="only the Q8_0 MTP-head GEMV figures (for profiler runs), then exit")
     ap.add_argument("--step-only", action="store_true",
@@ -633,6 +656,11 @@ def main():
         cs = torch.cuda.Stream(dev)
         print(json.dumps({"ffn_sublayer": run_ffn(torch, ops, dev, stream,
                                                   lambda fn, n: graph_time(torch, fn, n, stream, cs))}))
+        return
+    if args.lm_head_only:
+        cs = torch.cuda.Stream(dev)
+        print(json.dumps({"lm_head": run_lm_head(torch, ops, dev, xqs[next(g for _, K, _, g in SWEEP if K == 5120)],
+                                                 lambda fn, n: graph_time(torch, fn, n, stream, cs))}))
         return
     if args.q8_only:
         cs = torch.cuda.Stream(dev)
@@ -784,20 +812,7 @@ def main():
     q8 = run_q8(torch, ops, dev, time_reps, args.reps)
 
     # ---- lm_head (5120 -> 248320 PTQ1_0 GEMV, 278 MB) and the greedy argmax of its logits
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(SEED + 700)
-    lm = [device_weights(torch, dev, 5120, 248320, gen) for _ in range(2)]   # 556 MB: past the MALL
-    lx = xqs[next(g for _, K, _, g in SWEEP if K == 5120)]
-    ly = torch.empty((1, 248320), dtype=torch.float32, device=dev)
-    lidx = torch.empty(1, dtype=torch.int32, device=dev)
-    cw = torch.zeros(4, dtype=torch.int32, device=dev)
-    us_lm = time_reps(lambda r: ops.gemv_ptq1(lm[r % 2], lx, 5120, 248320, 1, out=ly), 40)
-    us_am = time_reps(lambda r: ops.argmax(ly, out=lidx), 40)
-    us_lws = time_reps(lambda r: ops.calib_read_ptq1(lm[r % 2], 5120, 248320, cw), 40)
-    lm_head = {"K": 5120, "N": 248320, "gemv_us": round(us_lm, 2),
-               "GBps": round(lm[0].numel() / (us_lm * 1e-6) / 1e9, 1), "argmax_us": round(us_am, 2),
-               "weight_stream_us": round(us_lws, 2), "weight_stream_GBps": round(lm[0].numel() / (us_lws * 1e-6) / 1e9, 1)}
-    del lm
+    lm_head = run_lm_head(torch, ops, dev, xqs[next(g for _, K, _, g in SWEEP if K == 5120)], time_reps)
 
     # ---- matmul input transform (residual add + RMSNorm + sign + FWHT), decode and prefill
     xform = {}
