@@ -119,7 +119,7 @@ def test_full_shape_17408x5120(dev):
         assert rel_l2(y.cpu().numpy()[:, rows], ref_o).max() < TIGHT
 
 
-@pytest.mark.parametrize("K,T", [(1024, 1), (2048, 2), (3072, 2), (4096, 1), (5120, 2)])
+@pytest.mark.parametrize("K,T", [(1024, 1), (2048, 2), (3072, 2), (4096, 1), (5120, 1), (5120, 2)])
 def test_long_single_matrix_orders(dev, K, T):
     """One matrix of >= 64 tiles per workgroup (66000 rows): the launch picks the tile-strided
     order where its scratch stores fit (K = 3072..5120) and the run order elsewhere (K = 1024,
