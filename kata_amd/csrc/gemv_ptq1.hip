@@ -596,7 +596,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // The pending item: its MFMA results Dp, its scales fp (d s, fixed when its MFMAs issue),
     // its slot dp.  DEFER (the tile-strided order: long runs): an item is scaled and stored in
     // the next item's body, after that item's MFMAs are issued, so the next decode covers
-    // their latency (lm_head 67.4 -> 64.6 us); the first pending item is a dummy (odd, zero)
+    // their latency (lm_head 68.3 -> 63.8 us); the first pending item is a dummy (odd, zero)
     // whose store goes to the lane's scratch word, and the run's last item, always odd (runs
     // are whole pairs), is finished after the loop.  Otherwise an item is finished in its own
     // body (short runs: 0.05-0.1 us faster on the sweep's small matrices).
