@@ -20,11 +20,15 @@ LIB = os.path.join(HERE, "libkata_amd.so")
 SOURCES = ["gemv_ptq1.hip", "gemv_q8.hip", "gemm_f16.hip", "gemm_q8.hip", "gemm_i8.hip", "expand.hip", "norm_fwht.hip", "argmax.hip", "calib.hip", "workspace.cpp", "gguf.cpp", "capi.cpp"]
 # Per-source extra flags.  The prefill GEMM keeps 144 fp32 accumulators per lane beside its
 # decode code; LLVM's iterative-ILP scheduler keeps them in place (the default one shuttles
-# them between register files every stage).  The GEMV source takes the max-ILP scheduler
-# (decode sweep step 45.1 -> 44.7 us, wide T = 8 gate 10.5 -> 10.3 us; results unchanged).
+# them between register files every stage).  The GEMV and int8 GEMM sources take the
+# max-ILP scheduler (decode sweep step 45.1 -> 44.7 us, wide T = 8 gate 10.5 -> 10.3 us;
+# pp512 int8 gate / down 88.1 / 81.7 -> 86.6 / 79.7 us; results unchanged).  Measured and
+# left at the default: the Q8_0 GEMV (max-ILP slower; iterative-ILP 21.2 -> 31.9 us on
+# 5120 x 17408) and the input transform (no change).
 EXTRA_FLAGS = {"gemm_f16.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
                "gemm_q8.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
-               "gemv_ptq1.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
+               "gemv_ptq1.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+               "gemm_i8.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
