@@ -28,7 +28,7 @@ def _replays_equal_eager(dev, fn, outs, n_replays=4):
     junk = torch.randn(1 << 20, device=dev)
     for r in range(n_replays):
         for o in outs:
-            o.fill_(float("nan"))                    # eager work between the replays
+            o.fill_(float("nan") if o.is_floating_point() else -1)   # eager work between the replays
         junk.mul_(1.0001)
         torch.cuda.synchronize()
         g.replay()
@@ -69,6 +69,23 @@ def test_graph_wide_batch_and_t2(dev):
         ops.gemv_ptq1(Ws[0], x2, K, Ns[0], 2, out=y2)
 
     _replays_equal_eager(dev, calls, y8 + [y2])
+
+
+def test_graph_long_matrix_strided_and_argmax(dev):
+    """One long matrix in the tile-strided order, whose items are scaled and stored one item
+    later (K = 5120, 66000 rows: >= 64 tiles per workgroup), on the operand form, followed by
+    the greedy argmax of its outputs (two launches and the argmax's stream buffer)."""
+    K, N = 5120, 66000
+    W = torch.from_numpy(orc.synth_ptq1(N, K, 77)[0]).to(dev)
+    xq = ops.gemv_prepare_x(torch.from_numpy(orc.synth_x(1, K, 78)).to(dev), K, 1)
+    y = torch.empty((1, N), device=dev)
+    idx = torch.empty(1, dtype=torch.int32, device=dev)
+
+    def calls():
+        ops.gemv_ptq1(W, xq, K, N, 1, out=y)
+        ops.argmax(y, out=idx)
+
+    _replays_equal_eager(dev, calls, [y, idx])
 
 
 def test_graph_prefill_gemm_with_pieces(dev):
