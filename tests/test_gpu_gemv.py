@@ -119,12 +119,13 @@ def test_full_shape_17408x5120(dev):
         assert rel_l2(y.cpu().numpy()[:, rows], ref_o).max() < TIGHT
 
 
-@pytest.mark.parametrize("K,T", [(1024, 1), (2048, 2), (3072, 2), (4096, 1), (5120, 1), (5120, 2)])
+@pytest.mark.parametrize("K,T", [(1024, 1), (2048, 1), (2048, 2), (3072, 1), (3072, 2), (4096, 1), (4096, 2),
+                                 (5120, 1), (5120, 2)])
 def test_long_single_matrix_orders(dev, K, T):
     """One matrix of >= 64 tiles per workgroup (66000 rows): the launch picks the tile-strided
-    order where its scratch stores fit (K = 3072..5120) and the run order elsewhere (K = 1024,
-    and 2048 at T = 2, whose strided pair slots would reach past the scratch area into the
-    item sums).  Every row against a torch fp32 product of the GPU-expanded weights, sampled
+    order where its scratch stores fit (K = 3072..5120, and 2048 at T = 1) and the run order
+    elsewhere (K = 1024, and 2048 at T = 2, whose strided pair slots would reach past the
+    scratch area into the item sums).  Every row against a torch fp32 product of the GPU-expanded weights, sampled
     rows against the oracle."""
     N = 66000
     W_np, _, _ = orc.synth_ptq1(N, K, K + T)
