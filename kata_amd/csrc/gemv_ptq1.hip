@@ -937,19 +937,49 @@ __global__ __launch_bounds__(512) void k_gemv_vw(VwMats P, const uint8_t* __rest
             static_for<TT>([&](auto tc) {
                 constexpr int t = decltype(tc)::value;
                 if constexpr (t + kVwAhead < TT) issue(t + kVwAhead);
+                // block bb's MFMAs and scales (d s of both tokens of the lane's pair)
+                auto blk = [&](int bb, v4i& D, float& fx, float& fy) {
+                    // the row's qh / scale dword, read by lane group 3
+                    const uint32_t wqc = (uint32_t)__builtin_amdgcn_ds_bpermute(qsrc, (int)wq[t][bb]);
+                    v4i B[kDenseMfma];
+                    dense_decode<kVwLR>(wl[t][bb], wh[t][bb], wqc, lb, laneoff, dl, B);
+                    D = v4i{0, 0, 0, 0};
 #pragma unroll
-                for (int bb = 0; bb < kVwBB; bb++) {
-                    if (bb < nbw) {
-                        // the row's qh / scale dword, read by lane group 3
-                        const uint32_t wqc = (uint32_t)__builtin_amdgcn_ds_bpermute(qsrc, (int)wq[t][bb]);
-                        v4i B[kDenseMfma];
-                        dense_decode<kVwLR>(wl[t][bb], wh[t][bb], wqc, lb, laneoff, dl, B);
-                        v4i D = {0, 0, 0, 0};
+                    for (int m = 0; m < kDenseMfma; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[bb][m], B[m], D, 0, 0, 0);
+                    const float d = half_bits_to_float(wqc >> 16);
+                    fx = d * sc[bb].x;
+                    fy = d * sc[bb].y;
+                };
+                auto add = [&](const v4i& D, float fx, float fy) {
+                    acc[t][0] += (float)(D[0] * 256 + D[1]) * fx;
+                    acc[t][1] += (float)(D[2] * 256 + D[3]) * fy;
+                };
+                if (nbw == kVwBB) {
+                    // a whole chunk share (wave-uniform): block bb - 1 is added after block bb's
+                    // MFMAs issue, so the next decode covers their latency (same order of adds)
+                    v4i Dp;
+                    float px, py;
+                    blk(0, Dp, px, py);
 #pragma unroll
-                        for (int m = 0; m < kDenseMfma; m++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[bb][m], B[m], D, 0, 0, 0);
-                        const float d = half_bits_to_float(wqc >> 16);
-                        acc[t][0] += (float)(D[0] * 256 + D[1]) * (d * sc[bb].x);
-                        acc[t][1] += (float)(D[2] * 256 + D[3]) * (d * sc[bb].y);
+                    for (int bb = 1; bb < kVwBB; bb++) {
+                        v4i D;
+                        float fx, fy;
+                        blk(bb, D, fx, fy);
+                        add(Dp, px, py);
+                        Dp = D;
+                        px = fx;
+                        py = fy;
+                    }
+                    add(Dp, px, py);
+                } else {
+#pragma unroll
+                    for (int bb = 0; bb < kVwBB; bb++) {
+                        if (bb < nbw) {
+                            v4i D;
+                            float fx, fy;
+                            blk(bb, D, fx, fy);
+                            add(D, fx, fy);
+                        }
                     }
                 }
             });
