@@ -717,7 +717,9 @@ __constant__ WideOffTable kWideOff = make_wide_off_table();
 // every workgroup) into registers, then runs the workgroup's tiles in order, the weight loads
 // of tile t + 1 issued before tile t is computed (issuing every tile's loads first left the
 // compute waiting for the whole stream: 13.6 against 11.5 us on ffn_gate at T = 8), adding
-// into one fp32 accumulator pair per tile.  At the end the 8 waves' accumulators add in a fixed tree
+// into one fp32 accumulator pair per tile, blocks in order (in a whole share of a chunk a
+// block's products are added after the next block's MFMAs issue, so that decode covers
+// their latency).  At the end the 8 waves' accumulators add in a fixed tree
 // order (waves 4..7 into 0..3, 2..3 into 0..1, 1 into 0) through LDS: deterministic, and
 // no K split over workgroups (no partial sums, no reduction launch).
 constexpr int kVwTMax = 9;                       // tiles per workgroup (the switch in k_gemv_vw)
