@@ -441,12 +441,18 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 
     // (1b) trit table.  Consecutive threads store consecutive 16-byte words (no bank
     // conflicts); word o holds 4 replicas of entry o / (REPS / 4): trits of digits 1..4.
+    // A batch launch builds it after the first half of its weight ring (below): its longer
+    // ring runs gain from the earlier loads (decode sweep step 43.4 -> 42.8 us), one-matrix
+    // launches lose 1-5 % that way.
+    auto build_table = [&]() {
 #pragma unroll
-    for (int i = 0; i < lut_bytes(LR) / 16 / 1024; i++) {
-        const int o = tid + i * 1024;
-        const uint32_t e = trit_entry((uint32_t)o / (REPS / 4));
-        lut[o] = make_uint4(e, e, e, e);
-    }
+        for (int i = 0; i < lut_bytes(LR) / 16 / 1024; i++) {
+            const int o = tid + i * 1024;
+            const uint32_t e = trit_entry((uint32_t)o / (REPS / 4));
+            lut[o] = make_uint4(e, e, e, e);
+        }
+    };
+    if constexpr (!MULTI) build_table();
     // clear the A image (slots without an element and padding blocks stay zero) and the
     // scales of the padding blocks
     if constexpr (!XQ) {
@@ -496,6 +502,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // once (decode sweep step 45.4 -> 44.9 us; the whole ring after the operand: 3 % slower)
 #pragma unroll
     for (int u = 0; u < (XQ ? D / 2 : D); u++) load_next(u);
+    if constexpr (MULTI) build_table();
 
     // XQ: the operand form into the LDS layout (piece at byte o of the form: o plus one pad
     // per quarter before it; the scale pairs follow the fourth quarter's pad)
