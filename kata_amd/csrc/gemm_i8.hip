@@ -102,8 +102,11 @@ __device__ inline float row_bcast(float v) {
 }
 // acc[q] += float(I[q]) * (w * sx[row of output q]), where lane 16 R + Q of the caller's
 // 16-lane row R holds the row scale of output q = Q
+// (the empty asm gives each call its own copy of sxv, so every broadcast is used once and
+// becomes the DPP operand of its multiply instead of a move held across the column tiles)
 template <int... Q>
 __device__ inline void fold_tile(v16f& acc, const v16i& I, float w, float sxv, std::integer_sequence<int, Q...>) {
+    asm volatile("" : "+v"(sxv));
     ((acc[Q] += (float)I[Q] * (w * row_bcast<Q>(sxv))), ...);
 }
 
@@ -120,7 +123,9 @@ __device__ inline void dma4(const void* g, uint32_t lds) {
 // 32 x 32.  Per stage (one group of 128 k) the A fragments of both row tiles stay in
 // registers; for each column tile j the two tiles' int32 sums are 4 dependent
 // v_mfma_i32_32x32x32_i8 each, then folded: acc += float(I) * (sw[n] * sx[m]), the row
-// scale spread across the lanes by DPP.
+// scale spread across the lanes by DPP.  The order is (j, 1) MFMAs, fold (j, 0), (j + 1, 0)
+// MFMAs, fold (j, 1): each fold follows the MFMAs of the next tile, with the B fragments of
+// two column tiles in registers.
 // Barriers as in the fp16 consumer: two before the first stage, one per stage (after the
 // stage's last LDS read).
 template <bool C_F16>
@@ -159,23 +164,34 @@ __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int
         float sw[NT];
 #pragma unroll
         for (int j = 0; j < NT; j++) sw[j] = sws[(st & 1) * BN + j * 32];
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-            v4i bf[4];
+        v16i I[2];
+        v4i bfA[4], bfB[4];
+        auto ldb = [&](int j, v4i (&bf)[4]) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) bf[kk] = *(const v4i*)(bt + j * 32 * ROWB + (((2 * kk + lh) ^ xs) << 4));
             if (j == NT - 1) barrier_lds();  // stage st + 1 produced; stage st's buffers free
-            v16i I[2];
+        };
+        auto mmi = [&](int i, v4i (&bf)[4]) {
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int q = 0; q < 16; q++) I[i][q] = 0;
 #pragma unroll
-                for (int q = 0; q < 16; q++) I[i][q] = 0;
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][kk], bf[kk], I[i], 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++) fold_tile(acc[i][j], I[i], sw[j], sxv[i], std::make_integer_sequence<int, 16>());
-        }
+            for (int kk = 0; kk < 4; kk++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][kk], bf[kk], I[i], 0, 0, 0);
+        };
+        auto fold = [&](int i, int j) { fold_tile(acc[i][j], I[i], sw[j], sxv[i], std::make_integer_sequence<int, 16>()); };
+        // the fold of one 32 x 32 tile runs under the MFMAs of the next
+        auto step = [&](int j, v4i (&bc)[4], v4i (&bn)[4]) {
+            mmi(1, bc);
+            if (j + 1 < NT) ldb(j + 1, bn);
+            fold(0, j);
+            if (j + 1 < NT) mmi(0, bn);
+            fold(1, j);
+        };
+        ldb(0, bfA);
+        mmi(0, bfA);
+        step(0, bfA, bfB);
+        step(1, bfB, bfA);
+        step(2, bfA, bfB);
+        step(3, bfB, bfA);
     }
     // store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
     if (job >= J.n_full) {
