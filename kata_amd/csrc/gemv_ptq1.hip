@@ -393,8 +393,11 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     // wave w takes pair w % np for tiles h, h + G, h + 2G, ... (h = w / np, G = 16 / np
     // phases), so at any time the waves read neighbouring pieces of the same few tiles; the
     // waves past G np stay idle.  Same items and slots as the run order: the same results.
+    // Every workgroup of such a launch takes it (a short last range too: the waves whose
+    // phase has no tile get no items), so a wave's pair never changes and the loop has no
+    // pair-change or tile-wrap test (lm_head 62.1 -> 61.0 us).
     const int np = nq >> 1, G = kWaves / np;
-    const bool strided = STRIDE && Tt >= 2 * G;
+    constexpr bool strided = STRIDE;
     const int sp = strided ? wave % np : 0, sh = strided ? wave / np : 0;
     const int n = !strided ? s1 - s0                     // this wave's run length (even, wave-uniform)
                            : (wave < G * np && sh < Tt ? 2 * ((Tt - sh + G - 1) / G) : 0);
@@ -475,7 +478,7 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     int lt = strided ? sh : (s0 % (2 * Tt)) >> 1;   // load cursor: tile, item offset, items left
     uint32_t lso = (uint32_t)(wt0 + lt) * tstep + (uint32_t)(2 * (strided ? sp : s0 / (2 * Tt))) * 4 * kBlockBytes;
     int lrem = n;
-    const int Tw = strided ? 0x7fffffff : Tt;    // the pair changes after tile Tw - 1 (strided: never)
+    const int Tw = Tt;                           // run order: the pair changes after tile Tw - 1
     const uint32_t cstep = 4 * kBlockBytes;      // even c -> c + 1, same tile
     const uint32_t tnext = (strided ? G : 1) * tstep - cstep;    // odd c -> c - 1, next tile
     const uint32_t cwrap = cstep - (uint32_t)(Tt - 1) * tstep;   // odd c, last tile -> next pair
@@ -489,9 +492,13 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         wl[slot] = w.x;
         wh[slot] = w.y;
         if (slot & 1) {
-            const bool wrap = ++lt == Tw;
-            lt = wrap ? 0 : lt;
-            lso += wrap ? cwrap : tnext;
+            if constexpr (STRIDE) {
+                lso += tnext;
+            } else {
+                const bool wrap = ++lt == Tw;
+                lt = wrap ? 0 : lt;
+                lso += wrap ? cwrap : tnext;
+            }
         } else {
             lso += cstep;
         }
@@ -648,10 +655,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
 #pragma unroll
         for (int t = 0; t < T; t++) fp[t] = d * sc[u & 1][t];
         if constexpr (!DEFER) finish(std::integral_constant<bool, (u & 1) == 1>{});
-        if ((u & 1) && ++ct == Tw) {
-            ct = 0;
-            ++cp;
-            if (next) load_a(cp);
+        if constexpr (!STRIDE) {
+            if ((u & 1) && ++ct == Tw) {
+                ct = 0;
+                ++cp;
+                if (next) load_a(cp);
+            }
         }
     };
     if (n > 0) {

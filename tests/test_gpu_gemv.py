@@ -158,3 +158,26 @@ def test_batch_equals_single_calls(dev, K, Ns, T, half2):
         assert torch.equal(yb, y1)
         ref = orc.gemv_ptq1(W_np, x_np.astype(np.float32), K, N, T)
         assert rel_l2(yb.cpu().numpy(), ref).max() < TIGHT
+
+
+@pytest.mark.parametrize("K", [3072, 4096, 5120])
+def test_strided_short_last_range(dev, K):
+    """Tile-strided launch whose last workgroup gets a single, ragged tile: 65283 rows are
+    16321 tiles, 64 per workgroup on 256 CUs, so workgroup 255 holds one 3-row tile (fewer
+    tiles than the order's phases: most of its waves get no items).  Every row against a
+    torch fp32 product of the GPU-expanded weights, sampled rows and the last rows against
+    the oracle."""
+    N, T = 65283, 1
+    W_np, _, _ = orc.synth_ptq1(N, K, K + 7)
+    x_np = orc.synth_x(T, K, K + 8)
+    W = torch.from_numpy(W_np).to(dev)
+    x = torch.from_numpy(x_np).to(dev)
+    y = ops.gemv_ptq1(W, x, K, N, T)
+    ref = x.float() @ ops.expand_f16(W, K, N).float().T
+    torch.cuda.synchronize()
+    assert rel_l2(y.cpu().numpy(), ref.cpu().numpy()).max() < TIGHT
+    rows = np.concatenate([np.arange(0, N, 509), np.arange(N - 9, N)])
+    ref_o = orc.gemv_ptq1(np.ascontiguousarray(W_np[rows]), x_np.astype(np.float32), K, len(rows), T)
+    got = y.cpu().numpy()[:, rows]
+    assert rel_l2(got, ref_o).max() < TIGHT
+    assert np.abs(got[:, -9:] - ref_o[:, -9:]).max() <= 2e-4 * np.abs(ref_o[:, -9:]).max()
