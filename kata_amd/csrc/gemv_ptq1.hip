@@ -614,8 +614,10 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     };
     int ct = strided ? 0 : (s0 % (2 * Tt)) >> 1, cp = strided ? sp : s0 / (2 * Tt);   // compute cursor: tile, pair
     v4i B0[kDenseMfma], B1[kDenseMfma];
-    // The pending item: its MFMA results Dp, its scales fp (d s, fixed when its MFMAs issue),
-    // its slot dp.  DEFER (the tile-strided order: long runs): an item is scaled and stored in
+    // The pending item: its MFMA results Dp, its scales fp (the activation scale s, and d as
+    // the upper half of its qh/scale word dw; with PAD the product d s), its slot dp.  Without
+    // PAD the sum is d * (D s): one mixed-precision fma takes d straight from the fp16 bits
+    // (decode sweep step -0.7 %).  DEFER (the tile-strided order: long runs): an item is scaled and stored in
     // the next item's body, after that item's MFMAs are issued, so the next decode covers
     // their latency (lm_head 68.3 -> 63.8 us); the first pending item is a dummy (odd, zero)
     // whose store goes to the lane's scratch word, and the run's last item, always odd (runs
@@ -627,16 +629,26 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
     float* dp = (float*)(Js + lane * 4);
 #pragma unroll
     for (int t = 0; t < T; t++) fp[t] = vprev[t] = 0.0f;
+    uint32_t dw = 0;
     auto finish = [&](auto oc) {
 #pragma unroll
         for (int t = 0; t < T; t++) {
             // explicit fma, contraction off (below): every instantiation (one matrix or a
             // batch) rounds alike, so a batched launch equals the per-matrix launches bit for bit
             const float fi = (float)(Dp[2 * t] * 256 + Dp[2 * t + 1]);
-            if constexpr (decltype(oc)::value)
-                dp[16 * t] = __builtin_fmaf(fi, fp[t], vprev[t]);
-            else
-                vprev[t] = fi * fp[t];
+            if constexpr (PAD) {
+                if constexpr (decltype(oc)::value)
+                    dp[16 * t] = __builtin_fmaf(fi, fp[t], vprev[t]);
+                else
+                    vprev[t] = fi * fp[t];
+            } else {
+                const float dd = (float)__builtin_bit_cast(_Float16, (unsigned short)(dw >> 16));
+                const float q = fi * fp[t];
+                if constexpr (decltype(oc)::value)
+                    dp[16 * t] = __builtin_fmaf(dd, q, vprev[t]);
+                else
+                    vprev[t] = __builtin_fmaf(dd, q, 0.0f);
+            }
         }
     };
     // item in ring slot u; `next`: item + 1 is in the run (its operands are read here)
@@ -647,13 +659,19 @@ __global__ __launch_bounds__(1024) void k_gemv_ptq1(GemvMats P, const void* __re
         v4i Dm = {0, 0, 0, 0};
 #pragma unroll
         for (int m = 0; m < kDenseMfma; m++) Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u & 1][m], B[m], Dm, 0, 0, 0);
-        float d = half_bits_to_float(wq[u] >> 16);
-        if (PAD && 4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
         if constexpr (DEFER) finish(std::integral_constant<bool, (u & 1) == 0>{});   // the previous item
         Dp = Dm;
         dp = (float*)(pcur + (u >> 1) * pstep);
+        if constexpr (PAD) {
+            float d = half_bits_to_float(wq[u] >> 16);
+            if (4 * (2 * cp + (u & 1)) + kq >= nb) d = 0.0f;
 #pragma unroll
-        for (int t = 0; t < T; t++) fp[t] = d * sc[u & 1][t];
+            for (int t = 0; t < T; t++) fp[t] = d * sc[u & 1][t];
+        } else {
+            dw = wq[u];
+#pragma unroll
+            for (int t = 0; t < T; t++) fp[t] = sc[u & 1][t];
+        }
         if constexpr (!DEFER) finish(std::integral_constant<bool, (u & 1) == 1>{});
         if constexpr (!STRIDE) {
             if ((u & 1) && ++ct == Tw) {
