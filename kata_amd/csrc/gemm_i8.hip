@@ -7,9 +7,9 @@
 // gemm (shaders/prefill.metal:382-415): I = sum_{k in g} A8[m][k]*trit[n][k] (exact int32),
 //   C[m][n] = sum_g float(I) * (d[n][g] * SX[g][m]) in fp32, groups ascending.
 //
-// Design: the tile machinery of the fp16 GEMM (256 x 128 C tiles, 8 waves: 4 consumers
-// on v_mfma_i32_32x32x32_i8, 4 producers copying A by DMA and decoding weights into LDS,
-// whole tiles per CU then K pieces summed by a second kernel).  A stage is one 128-group:
+// Design: the tile machinery of the fp16 GEMM (256 x 128 C tiles, 12 waves: 8 consumers
+// on v_mfma_i32_32x32x32_i8, two per SIMD, 4 producers copying A by DMA and decoding weights
+// into LDS, whole tiles per CU then K pieces summed by a second kernel).  A stage is one 128-group:
 // an int8 A row of 128 k is 128 bytes, the byte layout of an fp16 stage row of 64 k, so the
 // A copies, swizzle and fragment reads are the fp16 kernel's, with half the stages.  The
 // producers also stage the group's row scales (A side) and column scales (decoded weights)
@@ -119,48 +119,46 @@ __device__ inline void dma4(const void* g, uint32_t lds) {
                  : "memory");
 }
 
-// Consumer waves (wave < 4): wave w owns rows 64w..64w+63 and all 128 columns, 2 x 4 tiles of
-// 32 x 32.  Per stage (one group of 128 k) the A fragments of both row tiles stay in
-// registers; for each column tile j the two tiles' int32 sums are 4 dependent
-// v_mfma_i32_32x32x32_i8 each, then folded: acc += float(I) * (sw[n] * sx[m]), the row
-// scale spread across the lanes by DPP.  The order is (j, 1) MFMAs, fold (j, 0), (j + 1, 0)
-// MFMAs, fold (j, 1): each fold follows the MFMAs of the next tile, with the B fragments of
-// two column tiles in registers.
+// Consumer waves (wave < kCW): wave w owns rows 32w..32w+31 and all 128 columns, 4 tiles of
+// 32 x 32.  Per stage (one group of 128 k) the A fragments stay in registers; for each column
+// tile j the int32 sum is 4 dependent v_mfma_i32_32x32x32_i8, then folded: acc += float(I) *
+// (sw[n] * sx[m]), the row scale spread across the lanes by DPP.  The fold of tile j follows
+// the MFMAs of tile j + 1.  A wave's VALU does not overlap its own MFMAs; with two consumers
+// on each SIMD one's fold can run under the other's MFMAs (2.5 % faster than four consumers
+// of 64 rows; 64 x 64 per wave, fewer LDS reads, gains nothing over it).
 // Barriers as in the fp16 consumer: two before the first stage, one per stage (after the
 // stage's last LDS read).
+constexpr int kCW = 8;                   // consumer waves; each owns BM / kCW rows
+constexpr int kRH = BM / kCW;             // rows per consumer wave
+constexpr int kRT = kRH / 32;             // 32-row MFMA tiles per consumer wave
 template <bool C_F16>
 __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int job, const GemmJobs& J, float* ws,
                                   void* C, int ldc, int M, int m0, int n0, int R) {
     const int l32 = lane & 31, lh = lane >> 5;
-    v16f acc[2][NT];
+    v16f acc[kRT][NT];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < kRT; i++)
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
-    // lane l holds row / column l % 32 of each 32-row tile at k = 32 kk + 16 (l / 32) .. +15,
-    // chunk 2 kk + l / 32 (the same byte positions as the fp16 fragments)
     const int xs = (l32 >> 1) & 7;
-    const uint32_t a_row = (uint32_t)(wave * 64 + l32) * ROWB, b_row = (uint32_t)l32 * ROWB;
-    // lane 16 R + p reads the row scale of output p of a lane in 16-lane row R: output row
-    // 8 (p / 4) + 4 (R / 2) + p % 4 of the 32-row tile (one LDS read per row tile and stage)
-    const float* sxs = (const float*)(smem + kSxOff) + wave * 64 + 8 * ((lane & 15) >> 2) + 4 * lh + (lane & 3);
+    const uint32_t a_row = (uint32_t)(wave * kRH + l32) * ROWB, b_row = (uint32_t)l32 * ROWB;
+    const float* sxs = (const float*)(smem + kSxOff) + wave * kRH + 8 * ((lane & 15) >> 2) + 4 * lh + (lane & 3);
     const float* sws = (const float*)(smem + kSwOff) + l32;
     barrier_lds();                           // the producers' first copies landed
     barrier_lds();                           // stage 0 produced
     for (int st = 0; st < nb; st++) {
         const uint8_t* at = tile_a(smem, st % kABuf) + a_row;
         const uint8_t* bt = tile_b(smem, st & 1) + b_row;
-        v4i af[2][4];
+        v4i af[kRT][4];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < kRT; i++)
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) af[i][kk] = *(const v4i*)(at + i * 32 * ROWB + (((2 * kk + lh) ^ xs) << 4));
-        // row scales of the lane's output rows 8 (q / 4) + 4 (l / 32) + q % 4 of each row tile
-        float sxv[2];
+        float sxv[kRT];
 #pragma unroll
-        for (int i = 0; i < 2; i++) sxv[i] = sxs[(st % kABuf) * BM + i * 32];
+        for (int i = 0; i < kRT; i++) sxv[i] = sxs[(st % kABuf) * BM + i * 32];
         float sw[NT];
 #pragma unroll
         for (int j = 0; j < NT; j++) sw[j] = sws[(st & 1) * BN + j * 32];
@@ -171,49 +169,53 @@ __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int
             for (int kk = 0; kk < 4; kk++) bf[kk] = *(const v4i*)(bt + j * 32 * ROWB + (((2 * kk + lh) ^ xs) << 4));
             if (j == NT - 1) barrier_lds();  // stage st + 1 produced; stage st's buffers free
         };
-        auto mmi = [&](int i, v4i (&bf)[4]) {
+        auto mmi = [&](int i, int slot, v4i (&bf)[4]) {
 #pragma unroll
-            for (int q = 0; q < 16; q++) I[i][q] = 0;
+            for (int q = 0; q < 16; q++) I[slot][q] = 0;
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][kk], bf[kk], I[i], 0, 0, 0);
+            for (int kk = 0; kk < 4; kk++)
+                I[slot] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][kk], bf[kk], I[slot], 0, 0, 0);
         };
-        auto fold = [&](int i, int j) { fold_tile(acc[i][j], I[i], sw[j], sxv[i], std::make_integer_sequence<int, 16>()); };
-        // the fold of one 32 x 32 tile runs under the MFMAs of the next
-        auto step = [&](int j, v4i (&bc)[4], v4i (&bn)[4]) {
-            mmi(1, bc);
-            if (j + 1 < NT) ldb(j + 1, bn);
-            fold(0, j);
-            if (j + 1 < NT) mmi(0, bn);
-            fold(1, j);
+        auto fold = [&](int i, int j, int slot) {
+            fold_tile(acc[i][j], I[slot], sw[j], sxv[i], std::make_integer_sequence<int, 16>());
         };
+        // one 32-row tile: the fold of column tile j follows the MFMAs of tile j + 1
+        auto step = [&](int j, v4i (&bn)[4]) {
+            if (j + 1 < NT) {
+                ldb(j + 1, bn);
+                mmi(0, (j + 1) & 1, bn);
+            }
+            fold(0, j, j & 1);
+        };
+        static_assert(NT == 4, "the steps below cover four column tiles");
         ldb(0, bfA);
-        mmi(0, bfA);
-        step(0, bfA, bfB);
-        step(1, bfB, bfA);
-        step(2, bfA, bfB);
-        step(3, bfB, bfA);
+        mmi(0, 0, bfA);
+        step(0, bfB);
+        step(1, bfA);
+        step(2, bfB);
+        step(3, bfA);
     }
     // store: lane holds D[8(q/4) + 4(l/32) + q%4][l % 32] of each 32x32 tile
     if (job >= J.n_full) {
         float* P = ws + (size_t)(job - J.n_full) * (BM * BN);
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < kRT; i++)
 #pragma unroll
             for (int j = 0; j < NT; j++)
 #pragma unroll
                 for (int q = 0; q < 16; q++)
-                    P[(wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3)) * BN + j * 32 + l32] = acc[i][j][q];
+                    P[(wave * kRH + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3)) * BN + j * 32 + l32] = acc[i][j][q];
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < kRT; i++)
 #pragma unroll
         for (int j = 0; j < NT; j++) {
             const int gc = j * 32 + l32;
             const int gn = n0 + gc;
 #pragma unroll
             for (int q = 0; q < 16; q++) {
-                const int gm = m0 + wave * 64 + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
+                const int gm = m0 + wave * kRH + i * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
                 if (gm < M && gc < R) {
                     if (C_F16) ((_Float16*)C)[(size_t)gm * ldc + gn] = (_Float16)acc[i][j][q];
                     else ((float*)C)[(size_t)gm * ldc + gn] = acc[i][j][q];
@@ -222,14 +224,14 @@ __device__ inline void consume_i8(uint8_t* smem, int wave, int lane, int nb, int
         }
 }
 
-// Stage = one PTQ1_0 block (128 k).  Producer waves 4..7: A stage copies (8 DMA per wave)
+// Stage = one PTQ1_0 block (128 k).  Producer waves kCW..kCW+3: A stage copies (8 DMA per wave)
 // plus the stage's row scales (one dword DMA per wave, rows 64 pw .. +63, clamped to M - 1),
 // two stages ahead into three buffers; packed weight bytes of a block staged by DMA two
 // blocks ahead; decode of the next stage into one of two B buffers.  Producer lane decodes
 // half q = pw & 1 of tile row 64 (pw >> 1) + lane: chunks 0..3 (q = 0: dwords 0..3 at digits
 // 0..3) or chunks 4..7 (q = 1: digit 4 of dwords 0..3, dwords 4, 5, the qh bytes).
 template <bool C_F16>
-__global__ __launch_bounds__(512) void k_gemm_ptq1_i8(const int8_t* __restrict__ A8, const float* __restrict__ SX,
+__global__ __launch_bounds__(64 * (kCW + 4)) void k_gemm_ptq1_i8(const int8_t* __restrict__ A8, const float* __restrict__ SX,
                                                       int ldS, const uint8_t* __restrict__ W, void* __restrict__ C,
                                                       int ldc, float* __restrict__ ws, int M, int K, int N,
                                                       GemmJobs J) {
@@ -244,13 +246,13 @@ __global__ __launch_bounds__(512) void k_gemm_ptq1_i8(const int8_t* __restrict__
     const int R = min(BN, N - n0);
     const uint32_t row_bytes = (uint32_t)nbk * kBlockBytes;
 
-    if (wave < 4) {
+    if (wave < kCW) {
         consume_i8<C_F16>(smem, wave, lane, nb, job, J, ws, C, ldc, M, m0, n0, R);
         return;
     }
 
     // ================= producers =================
-    const int pw = wave - 4;
+    const int pw = wave - kCW;
     // an int8 row of 128 k has the byte layout of an fp16 stage row of 64 k
     const _Float16* Ah = (const _Float16*)(A8 + (size_t)kb0 * kGroup);
     const float* sxsrc = SX + (size_t)kb0 * ldS + min(m0 + 64 * pw + lane, M - 1);
@@ -353,10 +355,10 @@ hipError_t launch_gemm_i8(const int8_t* A8, const float* SX, int ldS, const uint
     const GemmJobs J = plan_gemm_jobs(M, N, K, BM, BN, n_cu);   // one workgroup per CU
     if (J.n_jobs > J.n_full && (e = gemm_device(true, s, &n_cu, &ws)) != hipSuccess) return e;
     if (c_dtype == 1)
-        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, A8, SX, ldS, W, C, ldc, ws,
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<true>, dim3(J.n_jobs), dim3(64 * (kCW + 4)), kLdsBytes, s, A8, SX, ldS, W, C, ldc, ws,
                            M, K, N, J);
     else
-        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, dim3(J.n_jobs), dim3(512), kLdsBytes, s, A8, SX, ldS, W, C, ldc,
+        hipLaunchKernelGGL(k_gemm_ptq1_i8<false>, dim3(J.n_jobs), dim3(64 * (kCW + 4)), kLdsBytes, s, A8, SX, ldS, W, C, ldc,
                            ws, M, K, N, J);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
