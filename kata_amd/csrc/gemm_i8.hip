@@ -74,18 +74,16 @@ __host__ __device__ constexpr uint32_t p3x2(int n) {
 
 // int8 trits (digit - 1) of the 4 bytes of w, in byte order: bytes 0, 1 at the digit of
 // multiplier p3lo, bytes 2, 3 at p3hi.  The bytes go to 16-bit lanes (v_perm selector 0x0c is
-// a zero byte); ((b * 3^n) mod 256) * 3 has the digit in its high byte; a v_perm table maps
-// digits 0, 1, 2 to the bytes 0xff, 0x00, 0x01.
+// a zero byte); ((b * 3^n) mod 256) * 3 - 256 has the trit in its high byte (0xff, 0x00, 0x01).
 __device__ inline uint32_t trits4(uint32_t w, uint32_t p3lo, uint32_t p3hi) {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     u16x2 e = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c010c00u));
     u16x2 o = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0c030c02u));
     e = (e * __builtin_bit_cast(u16x2, p3lo)) & (u16x2){0xff, 0xff};
     o = (o * __builtin_bit_cast(u16x2, p3hi)) & (u16x2){0xff, 0xff};
-    e = e * (u16x2){3, 3};
-    o = o * (u16x2){3, 3};
-    const uint32_t dg = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, o), __builtin_bit_cast(uint32_t, e), 0x07050301u);
-    return __builtin_amdgcn_perm(0u, 0x000100ffu, dg);
+    e = e * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    o = o * (u16x2){3, 3} + (u16x2){0xff00, 0xff00};
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, o), __builtin_bit_cast(uint32_t, e), 0x07050301u);
 }
 
 using namespace gemm;
